@@ -1,0 +1,337 @@
+/*
+ * l0hip: MI355X (gfx950) implementation of the l0llm decoder matmul and
+ * decode-attention path, behind a plain C ABI.
+ *
+ * The reference (hf-laboratories/l0llm) is C#; its kernels come from the
+ * external LevelZero.NET package, consumed through LevelZero.ComputeDevice,
+ * SharedBuffer<T>, LevelZeroRuntime and LevelZero.Kernels.LlmKernelSuite.
+ * Each entry point below names the reference member it replaces, with the
+ * call site (file:line, relative to src/HFLabs.ML.LLM.LevelZero/ unless a
+ * path is given) that fixes its argument order and meaning. A C# P/Invoke
+ * shim maps these onto the LevelZero-shaped classes.
+ *
+ * Conventions
+ *  - Every function returns an int status: L0H_OK (0) or a negative L0H_ERR_*
+ *    code; l0h_last_error() returns the calling thread's message for the last
+ *    failure. The codes map onto the .NET exceptions the reference throws.
+ *  - Pointers named x, y, q, k, v, w, table, logits, ... are DEVICE pointers
+ *    obtained from l0h_alloc (or from a matrix/model object). Host pointers
+ *    are named host_*.
+ *  - All sizes are element counts (int, as the reference) unless named *_bytes.
+ *  - Outside recording, operations are enqueued in order on the device's
+ *    stream; l0h_read and l0h_synchronize wait for them. Between
+ *    l0h_begin_recording and l0h_end_recording they are captured into one HIP
+ *    graph, launched and waited for at l0h_end_recording.
+ *  - Calls may come from any thread; every entry point selects its device.
+ */
+#ifndef L0HIP_H
+#define L0HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ----------------------------------------------------- */
+#define L0H_OK 0
+#define L0H_ERR_INVALID_ARG (-1)    /* ArgumentException / ArgumentNull / ArgumentOutOfRange */
+#define L0H_ERR_UNSUPPORTED (-2)    /* NotSupportedException */
+#define L0H_ERR_INVALID_OP (-3)     /* InvalidOperationException */
+#define L0H_ERR_INVALID_DATA (-4)   /* InvalidDataException */
+#define L0H_ERR_OUT_OF_MEMORY (-5)  /* allocation failure */
+#define L0H_ERR_DEVICE (-6)         /* HIP runtime / device failure */
+
+/* ---- element types ---------------------------------------------------- */
+#define L0H_F32 0
+#define L0H_F16 1
+#define L0H_BF16 2
+#define L0H_I8PC 3 /* int8 weight-only, one fp16 scale per output row */
+
+/* ---- LlmWeightPrecision (LlmWeightPrecision.cs:3-19), plus BFloat16 ---- */
+#define L0H_PRECISION_AUTO 0
+#define L0H_PRECISION_FLOAT32 1
+#define L0H_PRECISION_FLOAT16 2
+#define L0H_PRECISION_INT8 3
+#define L0H_PRECISION_BFLOAT16 4
+
+typedef struct l0h_device l0h_device;
+typedef struct l0h_matrix l0h_matrix;
+typedef struct l0h_model l0h_model;
+
+/* ======================================================================
+ * Device runtime (replaces LevelZero.LevelZeroRuntime / ComputeDevice /
+ * SharedBuffer<T>)
+ * ==================================================================== */
+
+/* LevelZeroRuntime.IsAvailable (LevelZeroLlmEngine.cs:355-360): 1 if a gfx950 device is present. */
+int l0h_runtime_is_available(void);
+/* LevelZeroRuntime.EnumerateDevices (../l0llm/Program.cs:124): number of HIP devices. */
+int l0h_device_count(int* count);
+/* LevelZeroRuntime.GetDevice(0, id) (LevelZeroLlmEngine.cs:359). */
+int l0h_device_open(int ordinal, l0h_device** out);
+/* ComputeDevice.Dispose. */
+int l0h_device_close(l0h_device* dev);
+/* Device name and compute-unit count (../l0llm/Program.cs:138 prints the device). */
+int l0h_device_info(l0h_device* dev, char* host_name, size_t name_bytes, int* compute_units);
+/* ComputeDevice.AllocShared<T>(count) (LlmModel.cs:49-53): device memory, not zeroed. */
+int l0h_alloc(l0h_device* dev, size_t bytes, void** out);
+/* SharedBuffer<T>.Dispose. */
+int l0h_free(l0h_device* dev, void* ptr);
+/* SharedBuffer<T>.Write (LlmModel.cs:414, LlmDecoderLayer.cs:320): host -> device, visible to later operations. */
+int l0h_write(l0h_device* dev, void* dst, size_t dst_offset_bytes, const void* host_src, size_t bytes);
+/* SharedBuffer<T>.ToArray (LlmModel.cs:250, :443): waits for queued work, device -> host. */
+int l0h_read(l0h_device* dev, const void* src, size_t src_offset_bytes, void* host_dst, size_t bytes);
+/* Fill bytes (LlmKvCache.cs:30-31 zeroes its caches with Write(new float[count])). */
+int l0h_fill_zero(l0h_device* dev, void* dst, size_t bytes);
+/* ComputeDevice.BeginRecording (LlmModel.cs:353-356, :417-421). */
+int l0h_begin_recording(l0h_device* dev);
+/* ComputeDevice.EndRecording (LlmModel.cs:380-383, :439-442): submit the recorded list and wait. */
+int l0h_end_recording(l0h_device* dev);
+/* ComputeDevice.AbortRecording (LlmModel.cs:372-377, :431-437). */
+int l0h_abort_recording(l0h_device* dev);
+/* ComputeDevice.IsRecording (LlmModel.cs:353, :417). */
+int l0h_is_recording(l0h_device* dev, int* out);
+/* Wait for every queued operation. */
+int l0h_synchronize(l0h_device* dev);
+/* Message of the calling thread's last failure ("" if none). */
+const char* l0h_last_error(void);
+
+/* ======================================================================
+ * LlmKernelSuite operators, reference-shaped (fp32 activations)
+ * ==================================================================== */
+
+/* LlmGemvKernel.Supports(N) (LlmMatrix.cs:52, :136): N % 4 == 0. */
+int l0h_gemv_supports(int out_dim);
+/* LlmGemvKernel.MaxRows (LlmDecoderLayer.cs:111): rows per ExecuteRows call. */
+int l0h_gemv_max_rows(void);
+/* LlmGemvQ8Kernel.Supports(N, K) (LlmMatrix.cs:89): N % 4 == 0 and K % 32 == 0. */
+int l0h_gemv_q8_supports(int out_dim, int in_dim);
+
+/* Gemv.Execute(dev, outDim, inDim, x, W, y) (LlmMatrix.cs:134, :138): y[N] = x[K] * W,
+ * W in the reference's [K, N] layout, w_dtype L0H_F32 or L0H_F16. */
+int l0h_gemv_execute(l0h_device* dev, int out_dim, int in_dim, const float* x, const void* w,
+                     int w_dtype, float* y);
+/* Gemv.ExecuteRows(dev, rows, outDim, inDim, x, W, y) (LlmMatrix.cs:161, :165). */
+int l0h_gemv_execute_rows(l0h_device* dev, int rows, int out_dim, int in_dim, const float* x,
+                          const void* w, int w_dtype, float* y);
+/* Gemm.Execute(dev, M, N, K, x, W, y) (LlmMatrix.cs:142, :169): fp32 [M,K] x [K,N]. */
+int l0h_gemm_execute(l0h_device* dev, int m, int n, int k, const float* x, const float* w,
+                     float* y);
+/* GemvQ8.Execute / ExecuteRows (LlmMatrix.cs:130, :157, :235, :239) in this build's int8 format:
+ * weight-only int8 [N, K] with one fp16 scale per output row, fp32 x and y. The reference's
+ * GemvQ8.Quantize step (activation quantization) has no counterpart: activations stay fp32. */
+int l0h_gemv_q8_execute_rows(l0h_device* dev, int rows, int out_dim, int in_dim, const float* x,
+                             const int8_t* w, const uint16_t* scales, float* y);
+
+/* RMSNorm.Execute(dev, x, residual, w, out, eps, n, rows, addResidual)
+ * (LlmDecoderLayer.cs:167, :183-184; LlmModel.cs:394). residual may be NULL when add_residual is 0. */
+int l0h_rmsnorm_execute(l0h_device* dev, float* x, const float* residual, const float* w,
+                        float* out, float eps, int n, int rows, int add_residual);
+/* SwiGLU.Execute(dev, gate, up, n) (LlmDecoderLayer.cs:189). */
+int l0h_swiglu_execute(l0h_device* dev, float* gate, const float* up, int n);
+/* Add.Execute(dev, a, b, n) (LlmDecoderLayer.cs:194). */
+int l0h_add_execute(l0h_device* dev, float* a, const float* b, int n);
+/* BiasAdd.Execute(dev, x, bias, n, rows) (LlmDecoderLayer.cs:303-305). */
+int l0h_bias_add_execute(l0h_device* dev, float* x, const float* bias, int n, int rows);
+/* RoPE.Execute(dev, q, k, positions, headDim, nH, nKv, theta, tokens) (LlmDecoderLayer.cs:415-417). */
+int l0h_rope_execute(l0h_device* dev, float* q, float* k, const int* positions, int head_dim,
+                     int n_heads, int n_kv_heads, float theta, int tokens);
+/* RoPE.ExecuteWithFrequencies(dev, q, k, positions, invFreq, headDim, nH, nKv, attnScale, tokens,
+ * rotaryDim) (LlmDecoderLayer.cs:421-423). */
+int l0h_rope_execute_with_frequencies(l0h_device* dev, float* q, float* k, const int* positions,
+                                      const float* inv_freq, int head_dim, int n_heads,
+                                      int n_kv_heads, float attn_scale, int tokens,
+                                      int rotary_dim);
+/* KvCacheStore.Execute(dev, k, v, K$, V$, pos, kvDim) (LlmDecoderLayer.cs:322).
+ * cache_dtype L0H_F32 (the reference's cache, LlmKvCache.cs:21-24) or L0H_F16. */
+int l0h_kv_cache_store_execute(l0h_device* dev, const float* k, const float* v, void* k_cache,
+                               void* v_cache, int cache_dtype, int pos, int kv_dim);
+/* KvCacheStore.ExecuteRows(dev, k, v, K$, V$, pos0, kvDim, tokens) (LlmDecoderLayer.cs:368). */
+int l0h_kv_cache_store_execute_rows(l0h_device* dev, const float* k, const float* v,
+                                    void* k_cache, void* v_cache, int cache_dtype, int pos0,
+                                    int kv_dim, int tokens);
+/* Attention.Execute(dev, q, K$, V$, out, headDim, nH, nKv, seqLen, maxSeqLen)
+ * (LlmDecoderLayer.cs:325-327). Split-K over the sequence: no 15,000-token limit. */
+int l0h_attention_execute(l0h_device* dev, const float* q, const void* k_cache,
+                          const void* v_cache, int cache_dtype, float* out, int head_dim,
+                          int n_heads, int n_kv_heads, int seq_len, int max_seq_len);
+/* Attention.ExecutePrefill(dev, q, K$, V$, out, headDim, nH, nKv, pos0, tokens, maxSeqLen)
+ * (LlmDecoderLayer.cs:369-371): causal within the chunk, plus every cached slot before it. */
+int l0h_attention_execute_prefill(l0h_device* dev, const float* q, const void* k_cache,
+                                  const void* v_cache, int cache_dtype, float* out, int head_dim,
+                                  int n_heads, int n_kv_heads, int pos0, int tokens,
+                                  int max_seq_len);
+/* Embedding.Execute(dev, ids, table, out, h, n) (LlmModel.cs:360, :424). */
+int l0h_embedding_execute(l0h_device* dev, const int* ids, const float* table, float* out, int h,
+                          int n);
+/* Copy.Execute(dev, src, dst, srcOffset, n) (LlmModel.cs:368). */
+int l0h_copy_execute(l0h_device* dev, const float* src, float* dst, int src_offset, int n);
+/* Sampling.Execute(dev, logits, sampled, temperature, randomVal, vocab) (LlmModel.cs:398): greedy
+ * argmax, first maximal index (LlmAbstractions.cs:79-92). temperature > 0 is L0H_ERR_UNSUPPORTED. */
+int l0h_sampling_execute(l0h_device* dev, const float* logits, int* sampled, float temperature,
+                         float random_val, int vocab);
+
+/* ======================================================================
+ * Weight-streaming kernels in the BASELINE formats (HuggingFace [N, K]
+ * weight layout; the role of Gemv / GemvQ8 / Gemm in LlmMatrix.cs:122-218)
+ * ==================================================================== */
+
+/* y[r, n] = sum_k x[r, k] * W[n, k] (* scales[n] for L0H_I8PC), fp32 accumulation.
+ * w_dtype: L0H_I8PC, L0H_F16, L0H_BF16 or L0H_F32; x_dtype and y_dtype: L0H_F32, L0H_F16 or
+ * L0H_BF16. rows 1 is the decode GEMV (LlmMatrix.Project, :122); rows > 1 reads W once per
+ * group of rows (LlmMatrix.ProjectRows, :149). */
+int l0h_gemv_nk(l0h_device* dev, int w_dtype, int rows, int out_dim, int in_dim, const void* x,
+                int x_dtype, const void* w, const uint16_t* scales, void* y, int y_dtype);
+/* Prefill GEMM on MFMA: Y[M, N] = X[M, K] * W[N, K]^T, X and W both L0H_F16 or both L0H_BF16,
+ * fp32 accumulation, y_dtype L0H_F32, L0H_F16 or L0H_BF16. Replaces the row-chunked
+ * ProjectRows of LlmMatrix.cs:149-171 for M >= 64. */
+int l0h_gemm_nk(l0h_device* dev, int dtype, int m, int n, int k, const void* x, const void* w,
+                void* y, int y_dtype);
+/* Batched GQA decode attention (Attention.Execute generalised to a batch; LlmDecoderLayer.cs:325-327).
+ * q: [batch, n_heads*head_dim] (q_dtype L0H_F32 or L0H_F16); caches: [batch, max_seq_len,
+ * n_kv_heads*head_dim] of cache_dtype; out: [batch, n_heads*head_dim] of out_dtype. Each
+ * sequence attends to its slots 0 .. seq_len-1. */
+int l0h_attention_decode(l0h_device* dev, const void* q, int q_dtype, const void* k_cache,
+                         const void* v_cache, int cache_dtype, void* out, int out_dtype, int batch,
+                         int head_dim, int n_heads, int n_kv_heads, int seq_len, int max_seq_len);
+
+/* ======================================================================
+ * Host-side helpers (CPU, no device needed)
+ * ==================================================================== */
+
+/* LlmMatrix.FitsInHalf (LlmMatrix.cs:110-120): 1 if every value is finite and |v| <= 65000. */
+int l0h_fits_in_half(const float* host_values, size_t count);
+/* LlmLayerWeights.Transpose (LlmLayerWeights.cs:226-255): [rows, cols] -> [cols, rows]. */
+int l0h_transpose(const float* host_src, int rows, int cols, float* host_dst);
+/* Per-output-channel int8 quantization of a HuggingFace [N, K] tensor (role of
+ * LlmQ8Quantizer.QuantizeOutIn, LlmMatrix.cs:92): scale = half(max|w| / 127),
+ * q = clamp(rint(w / scale), -127, 127). */
+int l0h_quantize_i8pc(const float* host_w, int out_dim, int in_dim, int8_t* host_q,
+                      uint16_t* host_scales);
+/* RopeFrequencies.Compute (RopeFrequencies.cs:60-183). rope_type 0 default, 1 linear, 2 yarn,
+ * 3 llama3; negative optional values mean "absent". */
+int l0h_rope_frequencies(int head_dim, double theta, int max_position_embeddings, int rope_type,
+                         double factor, int original_max_position_embeddings, double beta_fast,
+                         double beta_slow, double mscale, double mscale_all_dim,
+                         double attention_factor, double low_freq_factor,
+                         double high_freq_factor, int truncate, float* host_inv_freq,
+                         float* host_attention_factor);
+
+/* ======================================================================
+ * LlmMatrix (LlmMatrix.cs:7-260): one projection resident on the device.
+ * Device layout is [out, in] (HuggingFace order) for every storage type.
+ * ==================================================================== */
+
+/* LlmMatrix.Upload(device, data, inDim, outDim, half) (LlmMatrix.cs:44-57): host data is [in, out]. */
+int l0h_matrix_upload(l0h_device* dev, const float* host_in_out, int in_dim, int out_dim,
+                      int half, l0h_matrix** out);
+/* LlmMatrix.FromHuggingFace(device, hf, sixteenBitSource, name, outDim, inDim, precision)
+ * (LlmMatrix.cs:80-106): host hf is [out, in]. L0H_ERR_INVALID_DATA for Float16 values that do
+ * not fit a half. */
+int l0h_matrix_from_hf(l0h_device* dev, const float* host_out_in, int sixteen_bit_source,
+                       int out_dim, int in_dim, int precision, l0h_matrix** out);
+/* InDim, OutDim, storage type (L0H_F32/F16/BF16/I8PC), SizeInBytes (LlmMatrix.cs:22-33). */
+int l0h_matrix_info(const l0h_matrix* m, int* in_dim, int* out_dim, int* storage,
+                    long long* size_in_bytes);
+/* Device pointers of the stored weights (and scales for L0H_I8PC, else NULL). */
+int l0h_matrix_data(const l0h_matrix* m, const void** w, const uint16_t** scales);
+/* LlmMatrix.Project (LlmMatrix.cs:122-144): y[out] = x[in] * W. */
+int l0h_matrix_project(l0h_device* dev, const l0h_matrix* m, const float* x, float* y);
+/* LlmMatrix.ProjectRows (LlmMatrix.cs:149-171). */
+int l0h_matrix_project_rows(l0h_device* dev, const l0h_matrix* m, int rows, const float* x,
+                            float* y);
+/* LlmMatrix.ProjectAny (LlmMatrix.cs:220-230). */
+int l0h_matrix_project_any(l0h_device* dev, const l0h_matrix* m, int rows, const float* x,
+                           float* y);
+/* LlmMatrix.ProjectShared (LlmMatrix.cs:177-218): 2 to 4 projections of the same x. */
+int l0h_matrix_project_shared(l0h_device* dev, int rows, const float* x, int count,
+                              const l0h_matrix* const* matrices, float* const* ys);
+/* LlmMatrix.Dispose (LlmMatrix.cs:254-260). */
+int l0h_matrix_destroy(l0h_matrix* m);
+
+/* ======================================================================
+ * LlmModel + LlmDecoderLayer (LlmModel.cs, LlmDecoderLayer.cs): a
+ * Llama/Qwen2-style decoder resident on the device.
+ * ==================================================================== */
+
+/* The HfModelConfig fields the path uses (HfModelConfig.cs:10-120). */
+typedef struct {
+    int hidden_size;
+    int intermediate_size;
+    int num_layers;
+    int num_attention_heads;
+    int num_key_value_heads;
+    int head_dim;
+    int vocab_size;
+    int max_position_embeddings;
+    float rms_norm_eps;
+    double rope_theta;
+    int attention_bias;     /* Qwen2 q/k/v bias (HfModelConfig.cs:186) */
+    int tie_word_embeddings; /* lm_head shares the embedding (LlmModel.cs:62) */
+    /* rope_scaling (HfRopeScaling, RopeFrequencies.cs:6-40); rope_type 0 means none. */
+    int rope_type;
+    double rope_factor;
+    int rope_original_max_position_embeddings;
+    double rope_beta_fast, rope_beta_slow;
+    double rope_mscale, rope_mscale_all_dim, rope_attention_factor;
+    double rope_low_freq_factor, rope_high_freq_factor;
+    int rope_truncate;
+} l0h_model_config;
+
+/* Allocates an empty model (LlmModel ctor, LlmModel.cs:34-87): weights must then be set with
+ * l0h_model_init_random or l0h_model_set_tensor. precision as LlmWeightPrecision (Auto means
+ * Int8, as LlmModel.Load does when int8 kernels exist, :131-134); cache_dtype L0H_F32 or L0H_F16;
+ * max_seq_len is the KV cache length (LlmModel.Load, :109-120). */
+int l0h_model_create(l0h_device* dev, const l0h_model_config* cfg, int precision, int cache_dtype,
+                     int max_seq_len, l0h_model** out);
+/* Random-init weights on the device: every projection and the embedding ~ N(0, std^2) from a
+ * counter-based generator keyed by seed, then stored at the model's precision; norm weights 1,
+ * biases 0. */
+int l0h_model_init_random(l0h_model* model, uint64_t seed, float std);
+/* Sets one tensor from host fp32 data in HuggingFace naming and layout, e.g.
+ * "model.layers.3.self_attn.q_proj.weight" [out, in], "model.norm.weight", "lm_head.weight"
+ * (LlmLayerWeights.Load, LlmLayerWeights.cs:110-212; LlmModel.cs:55-63). sixteen_bit_source
+ * follows LlmMatrix.FromHuggingFace's rule for Auto precision. */
+int l0h_model_set_tensor(l0h_model* model, const char* name, const float* host_data,
+                         size_t count, int sixteen_bit_source);
+/* Reads back a projection as stored, in HuggingFace [out, in] order: storage type, weights
+ * (out*in elements of the storage type: int8 / fp16 / bf16 / fp32) and, for int8, fp16 scales. */
+int l0h_model_export_matrix(l0h_model* model, const char* name, int* storage, int* out_dim,
+                            int* in_dim, void* host_w, uint16_t* host_scales);
+/* Reads a fp32 vector tensor ("model.norm.weight", "...input_layernorm.weight", biases) or the
+ * embedding ("model.embed_tokens.weight"). */
+int l0h_model_export_vector(l0h_model* model, const char* name, float* host_dst, size_t count);
+/* Device pointers of one layer's K and V caches ([max_seq_len, n_kv*head_dim], cache_dtype). */
+int l0h_model_kv_cache(l0h_model* model, int layer, void** k_cache, void** v_cache);
+/* Device pointer of the logits buffer [vocab] fp32. */
+int l0h_model_logits(l0h_model* model, float** logits);
+/* LlmModel.ProjectionBytes (LlmModel.cs:92). */
+int l0h_model_projection_bytes(l0h_model* model, long long* bytes);
+/* LlmModel.Position (LlmModel.cs:219). */
+int l0h_model_position(l0h_model* model, int* position);
+/* LlmModel.ResetSequence (LlmModel.cs:221). */
+int l0h_model_reset_sequence(l0h_model* model);
+/* LlmModel.ComputeLogits(tokenId, position) (LlmModel.cs:199-203): host_logits [vocab]. */
+int l0h_model_compute_logits(l0h_model* model, int token, int position, float* host_logits);
+/* LlmModel.Prefill(promptIds) (LlmModel.cs:224-239): host_logits may be NULL. */
+int l0h_model_prefill(l0h_model* model, const int* host_ids, int count, float* host_logits);
+/* LlmModel.Decode(tokenId) (LlmModel.cs:242-251): host_logits may be NULL. */
+int l0h_model_decode(l0h_model* model, int token, float* host_logits);
+/* LlmModel.GenerateGreedy(promptIds, maxNewTokens, stopTokenIds) (LlmModel.cs:156-193): writes
+ * up to max_new tokens to host_out and their count to n_out. */
+int l0h_model_generate_greedy(l0h_model* model, const int* host_prompt, int prompt_len,
+                              int max_new, const int* host_stop, int n_stop, int* host_out,
+                              int* n_out);
+/* Greedy decode of `steps` tokens from the current position with the step graph replayed
+ * back to back and the sampled token fed back on the device (no host round trip per token);
+ * starts from `token` at Position and advances Position. host_out receives the tokens. */
+int l0h_model_decode_greedy_device(l0h_model* model, int token, int steps, int* host_out);
+/* LlmModel.Dispose (LlmModel.cs:308). */
+int l0h_model_destroy(l0h_model* model);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

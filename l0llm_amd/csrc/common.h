@@ -1,0 +1,121 @@
+// Shared internals of libl0hip: device object, status handling, launch
+// helpers and the dtype tags of the C ABI. Host and device code.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <mutex>
+#include <string>
+
+#include "../../include/l0hip.h"
+
+namespace l0h {
+
+// ---------------------------------------------------------------- errors --
+
+void set_error(const std::string& msg);
+void clear_error();
+
+// Status with message; used as `return fail(L0H_ERR_INVALID_ARG, "...")`.
+int fail(int code, const std::string& msg);
+
+#define L0H_HIP_TRY(expr)                                                                   \
+    do {                                                                                    \
+        hipError_t e_ = (expr);                                                             \
+        if (e_ != hipSuccess) {                                                             \
+            return ::l0h::fail(L0H_ERR_DEVICE, std::string(#expr) + ": " + hipGetErrorString(e_)); \
+        }                                                                                   \
+    } while (0)
+
+#define L0H_CHECK_ARG(cond, msg)                                  \
+    do {                                                          \
+        if (!(cond)) return ::l0h::fail(L0H_ERR_INVALID_ARG, msg); \
+    } while (0)
+
+// Kernel launch status (launch-config errors surface here).
+int launch_status(const char* what);
+
+// ---------------------------------------------------------------- device --
+
+}  // namespace l0h
+
+struct l0h_device {
+    int ordinal = 0;
+    hipStream_t stream = nullptr;  // every operation runs here, in order
+    hipStream_t upload = nullptr;  // host writes issued while recording
+    int compute_units = 0;
+    bool recording = false;
+    hipGraphExec_t cached_exec = nullptr;  // reused by l0h_end_recording via hipGraphExecUpdate
+    // Split-reduction workspace (attention partials, argmax partials), grown on demand
+    // outside recording; like LlmKernelSuite.EnsureQ8Scratch it must be sized before a
+    // recording starts (LlmModel.cs:139-144).
+    void* workspace = nullptr;
+    size_t workspace_bytes = 0;
+    unsigned* tickets = nullptr;  // self-resetting completion counters (zeroed once)
+    size_t ticket_count = 0;
+    std::mutex mu;
+};
+
+namespace l0h {
+
+// Selects the device for this thread (calls can arrive on any thread).
+int use_device(l0h_device* dev);
+// Makes sure the workspace holds `bytes` and `tickets` counters. Fails while recording
+// if growth would be needed.
+int ensure_workspace(l0h_device* dev, size_t bytes, size_t tickets);
+
+// ---------------------------------------------------------------- dtypes --
+
+inline int dtype_size(int dt) {
+    switch (dt) {
+    case L0H_F32: return 4;
+    case L0H_F16:
+    case L0H_BF16: return 2;
+    case L0H_I8PC: return 1;
+    default: return 0;
+    }
+}
+
+__host__ __device__ inline float bf16_bits_to_float(uint32_t bits16) {
+    return __uint_as_float(bits16 << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16 bits.
+__host__ __device__ inline uint16_t float_to_bf16_bits(float f) {
+    uint32_t x = __float_as_uint(f);
+    if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x40u);
+    x += 0x7fffu + ((x >> 16) & 1u);
+    return (uint16_t)(x >> 16);
+}
+
+__device__ inline float load_act(const void* p, int dt, size_t i) {
+    if (dt == L0H_F32) return static_cast<const float*>(p)[i];
+    uint16_t b = static_cast<const uint16_t*>(p)[i];
+    if (dt == L0H_F16) return __half2float(__ushort_as_half(b));
+    return bf16_bits_to_float(b);
+}
+
+__device__ inline void store_act(void* p, int dt, size_t i, float v) {
+    if (dt == L0H_F32) {
+        static_cast<float*>(p)[i] = v;
+    } else if (dt == L0H_F16) {
+        static_cast<uint16_t*>(p)[i] = __half_as_ushort(__float2half_rn(v));
+    } else {
+        static_cast<uint16_t*>(p)[i] = float_to_bf16_bits(v);
+    }
+}
+
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+// 16-byte streaming load that bypasses cache retention (weights and KV rows are read once).
+__device__ __forceinline__ uint4 ld_nt16(const void* p) {
+    u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+inline unsigned ceil_div(size_t a, size_t b) { return (unsigned)((a + b - 1) / b); }
+
+}  // namespace l0h

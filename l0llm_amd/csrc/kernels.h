@@ -1,0 +1,123 @@
+// Internal launchers shared by the C-ABI entry points and the model. All
+// launch on `s` and return an L0H status.
+#pragma once
+
+#include "common.h"
+
+namespace l0h {
+
+// Epilogue of a [N, K] weight-streaming GEMV (one activation row when fused).
+enum GemvEpilogue : int {
+    EPI_STORE = 0,     // y[m, n] = acc (+ bias[n]) in y_dtype
+    EPI_RESIDUAL = 1,  // resid[m, n] += acc            (O-proj, down-proj: LlmDecoderLayer.cs:183, :194)
+    EPI_SWIGLU = 2,    // rows interleaved gate/up: y[i] = silu(acc[2i]) * acc[2i+1] (:188-189)
+    EPI_QKV = 3,       // fused q|k|v rows, RoPE on q/k, k/v written to the cache (:296-322)
+};
+
+struct GemvParams {
+    // weights [N, K]
+    int w_dtype = L0H_I8PC;
+    const void* w = nullptr;
+    const uint16_t* scales = nullptr;  // I8PC: fp16 per row
+    int n = 0, k = 0;
+    int m = 1;  // activation rows
+    // activations [m, K]
+    const void* x = nullptr;
+    int x_dtype = L0H_F32;
+    const float* norm_w = nullptr;  // when set: x is fp32 and RMSNorm(x) * norm_w is used
+    float eps = 0.f;
+    // epilogue
+    int epilogue = EPI_STORE;
+    const float* bias = nullptr;  // [N] in stored row order
+    void* y = nullptr;            // STORE / SWIGLU output
+    int y_dtype = L0H_F32;
+    float* resid = nullptr;       // RESIDUAL
+    // QKV epilogue: rows [0, q_dim) are q, [q_dim, q_dim+kv_dim) k, then v. Within every q and k
+    // head the rows are stored RoPE-paired: row 2i <-> dim i, row 2i+1 <-> dim i + rot/2
+    // (i < rot/2); rows >= rot keep their dim.
+    float* q_out = nullptr;
+    void* k_cache = nullptr;
+    void* v_cache = nullptr;
+    int cache_dtype = L0H_F16;
+    const int* position = nullptr;  // device scalar: slot to write, RoPE position
+    const float* inv_freq = nullptr;
+    float rope_scale = 1.f;
+    int q_dim = 0, kv_dim = 0, head_dim = 0, rotary_dim = 0;
+};
+
+int launch_gemv_nk(hipStream_t s, const GemvParams& p);
+
+// Reference layout [K, N] GEMV / GEMM (Gemv.Execute, Gemm.Execute).
+int launch_gemv_kn(hipStream_t s, int rows, int n, int k, const float* x, const void* w,
+                   int w_dtype, float* y);
+
+// Element-wise operators.
+int launch_rmsnorm(hipStream_t s, float* x, const float* residual, const float* w, float* out,
+                   float eps, int n, int rows, int add_residual);
+int launch_swiglu(hipStream_t s, float* gate, const float* up, int n);
+int launch_add(hipStream_t s, float* a, const float* b, int n);
+int launch_bias_add(hipStream_t s, float* x, const float* bias, int n, int rows);
+// inv_freq may be null: then inv_freq[i] = 1 / theta^(2i/head_dim) is computed in fp64.
+int launch_rope(hipStream_t s, float* q, float* k, const int* positions, const float* inv_freq,
+                float theta, int head_dim, int nh, int nkv, float attn_scale, int tokens,
+                int rotary_dim);
+int launch_kv_store(hipStream_t s, const float* k, const float* v, void* kc, void* vc,
+                    int cache_dtype, const int* pos_device, int pos0, int kv_dim, int tokens);
+int launch_embedding(hipStream_t s, const int* ids, const float* table, float* out, int h,
+                     size_t n);
+int launch_copy(hipStream_t s, const float* src, float* dst, size_t n);
+// Greedy argmax (first maximal index). `partials` holds 2*blocks words; `ticket` one counter.
+// When feed_token/feed_pos/out_list are set, the chosen id is also written to *feed_token,
+// out_list[*step] and *pos and *step are incremented (device-side greedy loop).
+struct ArgmaxFeed {
+    int* token = nullptr;
+    int* position = nullptr;
+    int* step = nullptr;
+    int* out_list = nullptr;
+    int capacity = 0;  // entries of out_list; later steps are not recorded
+};
+int argmax_blocks(int vocab);
+int launch_argmax(hipStream_t s, const float* logits, int vocab, int* sampled,
+                  unsigned long long* partials, unsigned* ticket, const ArgmaxFeed& feed);
+
+// Decode attention. q [batch, nh*hd] (fp32/fp16), caches [batch, max_seq, nkv*hd], out
+// [batch, nh*hd]. seq_len from `seq_len_device` (+ seq_len_add) when non-null, else seq_len.
+struct AttnParams {
+    const void* q = nullptr;
+    int q_dtype = L0H_F32;
+    const void* kc = nullptr;
+    const void* vc = nullptr;
+    int cache_dtype = L0H_F16;
+    void* out = nullptr;
+    int out_dtype = L0H_F32;
+    int batch = 1, head_dim = 128, nh = 32, nkv = 8;
+    int seq_len = 0;
+    const int* seq_len_device = nullptr;
+    int seq_len_add = 0;
+    int max_seq_len = 0;
+    int splits = 1;  // sequence partitions per (batch, kv head)
+    float* partials = nullptr;  // [batch, nkv, splits, group, head_dim + 2]
+    unsigned* tickets = nullptr;  // [batch * nkv]
+};
+int attention_default_splits(int batch, int nkv, int max_len, int compute_units);
+size_t attention_partials_bytes(const AttnParams& p);
+int launch_attention_decode(hipStream_t s, const AttnParams& p);
+// Prefill over a shared cache: token t of the chunk attends to slots 0 .. pos0 + t (q and out
+// are [tokens, nh*hd]; p.batch and p.seq_len are set from pos0/tokens).
+int launch_attention_prefill(hipStream_t s, AttnParams p, int pos0, int tokens);
+
+// MFMA GEMM Y[M,N] = X[M,K] * W[N,K]^T (f16 or bf16 operands).
+// Small M splits K into fp32 partials in `ws` (gemm_workspace_bytes) when it fits.
+size_t gemm_workspace_bytes(int m, int n, int k);
+int launch_gemm_nk(hipStream_t s, int dtype, int m, int n, int k, const void* x, const void* w,
+                   void* y, int y_dtype, float* ws, size_t ws_bytes, int compute_units);
+
+// Random init: w[i] ~ N(0, std^2) from (seed, i); stored as dtype (F32/F16/BF16).
+int launch_init_normal(hipStream_t s, void* dst, int dtype, size_t count, uint64_t seed,
+                       float stddev);
+// Random init + per-row int8 quantization of an [N, K] matrix.
+int launch_init_normal_i8pc(hipStream_t s, int8_t* q, uint16_t* scales, int n, int k,
+                            uint64_t seed, float stddev);
+int launch_fill(hipStream_t s, float* dst, float value, size_t count);
+
+}  // namespace l0h

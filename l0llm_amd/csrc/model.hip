@@ -1,0 +1,762 @@
+// LlmModel + LlmDecoderLayer (LlmModel.cs, LlmDecoderLayer.cs) on gfx950.
+//
+// One decode step is the reference's op sequence (LlmModel.Step, :402-444; Forward, :129-196;
+// MixFull, :291-334; AppendHead, :387-400) fused into 5 kernels per layer:
+//   1. q|k|v GEMV with the input RMSNorm in its prologue and bias + RoPE + KV-cache store in
+//      its epilogue (rows of every q/k head stored RoPE-paired: 2i <-> i, 2i+1 <-> i + rot/2)
+//   2. split-K GQA attention with an in-kernel log-sum-exp merge
+//   3. O GEMV, epilogue hidden += y                      (the residual half of :183-184)
+//   4. gate|up GEMV (rows interleaved) with the post-attention RMSNorm in its prologue and
+//      SwiGLU in its epilogue                            (:183-189)
+//   5. down GEMV, epilogue hidden += y                   (:190-194)
+// then the final RMSNorm fused into the lm_head GEMV and a one-launch greedy argmax. The
+// token and position live in device memory, so the whole step is captured once as a HIP graph
+// and replayed (the reference records one command list per token); the argmax can feed the
+// chosen token and the next position back on the device for back-to-back greedy decode.
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "host.h"
+#include "kernels.h"
+
+namespace l0h {
+namespace {
+
+struct Proj {
+    void* w = nullptr;
+    uint16_t* s = nullptr;
+    int n = 0, k = 0;
+};
+
+struct Layer {
+    Proj qkv, o, gu, down;
+    float* qkv_bias = nullptr;  // stored row order
+    float* input_norm = nullptr;
+    float* post_norm = nullptr;
+    void* k_cache = nullptr;
+    void* v_cache = nullptr;
+};
+
+__global__ void scatter_rows_kernel(char* dst, const char* src, const int* map, int rows, size_t row_bytes) {
+    const int r = blockIdx.x;
+    if (r >= rows) return;
+    const char* s = src + (size_t)r * row_bytes;
+    char* d = dst + (size_t)map[r] * row_bytes;
+    if ((row_bytes & 15) == 0) {
+        for (size_t i = threadIdx.x * 16; i < row_bytes; i += blockDim.x * 16)
+            *reinterpret_cast<uint4*>(d + i) = *reinterpret_cast<const uint4*>(s + i);
+    } else {
+        for (size_t i = threadIdx.x; i < row_bytes; i += blockDim.x) d[i] = s[i];
+    }
+}
+
+}  // namespace
+}  // namespace l0h
+
+using namespace l0h;
+
+struct l0h_model {
+    l0h_device* dev = nullptr;
+    l0h_model_config cfg{};
+    int storage = L0H_I8PC;  // projection storage
+    int cache_dtype = L0H_F16;
+    int max_seq = 0;
+    int qd = 0, kvd = 0, rot = 0;
+    float rope_scale = 1.f;
+    std::vector<Layer> layers;
+    Proj lm;
+    float* embedding = nullptr;
+    float* final_norm = nullptr;
+    float* inv_freq = nullptr;
+    // activations
+    float *hidden = nullptr, *q = nullptr, *attn = nullptr, *act = nullptr, *logits = nullptr;
+    int *token = nullptr, *position = nullptr, *sampled = nullptr, *step = nullptr, *out_list = nullptr;
+    int out_capacity = 0;
+    // workspaces
+    float* attn_partials = nullptr;
+    unsigned* attn_tickets = nullptr;
+    unsigned long long* argmax_partials = nullptr;
+    unsigned* argmax_ticket = nullptr;
+    int attn_splits = 1;
+    hipGraphExec_t step_exec = nullptr;
+    int pos = 0;  // LlmModel.Position
+    std::vector<void*> owned;
+};
+
+namespace l0h {
+namespace {
+
+int alloc_owned(l0h_model* m, size_t bytes, void** out) {
+    int st = l0h_alloc(m->dev, bytes, out);
+    if (st) return st;
+    m->owned.push_back(*out);
+    return L0H_OK;
+}
+
+template <class T>
+int alloc_t(l0h_model* m, size_t count, T** out) {
+    void* p = nullptr;
+    int st = alloc_owned(m, count * sizeof(T), &p);
+    *out = static_cast<T*>(p);
+    return st;
+}
+
+int alloc_proj(l0h_model* m, Proj& p, int n, int k) {
+    p.n = n;
+    p.k = k;
+    int st = alloc_owned(m, (size_t)n * k * dtype_size(m->storage), &p.w);
+    if (st) return st;
+    if (m->storage == L0H_I8PC) st = alloc_t(m, (size_t)n, &p.s);
+    return st;
+}
+
+// Stored row of HF row `r` of a q or k projection (RoPE pairing within each head).
+int paired_row(int r, int hd, int rot) {
+    const int head = r / hd, d = r - head * hd, half = rot / 2;
+    int j;
+    if (d < half) j = 2 * d;
+    else if (d < rot) j = 2 * (d - half) + 1;
+    else j = d;
+    return head * hd + j;
+}
+
+struct Target {
+    Proj* proj = nullptr;
+    std::vector<int> map;  // HF row -> stored row
+    int n = 0, k = 0;      // HF shape
+    float** vec = nullptr;  // vector tensor
+    size_t vec_count = 0;
+    std::vector<int> vec_map;  // bias rows
+    bool embedding = false;
+};
+
+// Resolves a HuggingFace tensor name to its place in the device layout.
+int resolve(l0h_model* m, const std::string& name, Target& t) {
+    const auto& c = m->cfg;
+    const int H = c.hidden_size, I = c.intermediate_size, hd = c.head_dim;
+    auto identity = [](int n) {
+        std::vector<int> v(n);
+        for (int i = 0; i < n; i++) v[i] = i;
+        return v;
+    };
+    if (name == "model.embed_tokens.weight") {
+        t.embedding = true;
+        t.n = c.vocab_size;
+        t.k = H;
+        return L0H_OK;
+    }
+    if (name == "model.norm.weight") {
+        t.vec = &m->final_norm;
+        t.vec_count = H;
+        return L0H_OK;
+    }
+    if (name == "lm_head.weight") {
+        t.proj = &m->lm;
+        t.n = c.vocab_size;
+        t.k = H;
+        t.map = identity(t.n);
+        return L0H_OK;
+    }
+    int li = -1;
+    char rest[128] = {0};
+    if (std::sscanf(name.c_str(), "model.layers.%d.%127s", &li, rest) != 2 || li < 0 || li >= c.num_layers)
+        return fail(L0H_ERR_INVALID_ARG, "unknown tensor '" + name + "'");
+    Layer& L = m->layers[li];
+    const std::string r = rest;
+    if (r == "input_layernorm.weight") { t.vec = &L.input_norm; t.vec_count = H; return L0H_OK; }
+    if (r == "post_attention_layernorm.weight") { t.vec = &L.post_norm; t.vec_count = H; return L0H_OK; }
+    const bool is_q = r.rfind("self_attn.q_proj.", 0) == 0, is_k = r.rfind("self_attn.k_proj.", 0) == 0,
+               is_v = r.rfind("self_attn.v_proj.", 0) == 0;
+    if (is_q || is_k || is_v) {
+        const int n = is_q ? m->qd : m->kvd;
+        const int base = is_q ? 0 : (is_k ? m->qd : m->qd + m->kvd);
+        std::vector<int> map(n);
+        for (int i = 0; i < n; i++) map[i] = base + (is_v ? i : paired_row(i, hd, m->rot));
+        if (r.size() > 5 && r.compare(r.size() - 5, 5, ".bias") == 0) {
+            if (!c.attention_bias) return fail(L0H_ERR_INVALID_ARG, "the config has no attention bias");
+            t.vec = &L.qkv_bias;
+            t.vec_count = n;
+            t.vec_map = map;
+            return L0H_OK;
+        }
+        t.proj = &L.qkv;
+        t.n = n;
+        t.k = H;
+        t.map = map;
+        return L0H_OK;
+    }
+    if (r == "self_attn.o_proj.weight") { t.proj = &L.o; t.n = H; t.k = m->qd; t.map = identity(H); return L0H_OK; }
+    if (r == "mlp.gate_proj.weight" || r == "mlp.up_proj.weight") {
+        const int off = r == "mlp.gate_proj.weight" ? 0 : 1;
+        t.proj = &L.gu;
+        t.n = I;
+        t.k = H;
+        t.map.resize(I);
+        for (int i = 0; i < I; i++) t.map[i] = 2 * i + off;
+        return L0H_OK;
+    }
+    if (r == "mlp.down_proj.weight") { t.proj = &L.down; t.n = H; t.k = I; t.map = identity(H); return L0H_OK; }
+    return fail(L0H_ERR_INVALID_ARG, "unknown tensor '" + name + "'");
+}
+
+// Copies rows of a [n, row_bytes] device buffer to their stored rows.
+int scatter(l0h_model* m, void* dst, const void* src, const std::vector<int>& map, size_t row_bytes) {
+    int* dmap = nullptr;
+    int st = l0h_alloc(m->dev, map.size() * sizeof(int), reinterpret_cast<void**>(&dmap));
+    if (st) return st;
+    st = l0h_write(m->dev, dmap, 0, map.data(), map.size() * sizeof(int));
+    if (!st) {
+        scatter_rows_kernel<<<(unsigned)map.size(), 256, 0, m->dev->stream>>>(
+            static_cast<char*>(dst), static_cast<const char*>(src), dmap, (int)map.size(), row_bytes);
+        st = launch_status("scatter_rows");
+    }
+    if (!st) st = l0h_synchronize(m->dev);
+    l0h_free(m->dev, dmap);
+    return st;
+}
+
+// Places an HF-ordered [n, k] matrix (device, storage type) into its projection.
+int place_matrix(l0h_model* m, const Target& t, const void* dev_w, const uint16_t* dev_s) {
+    const size_t row_bytes = (size_t)t.k * dtype_size(m->storage);
+    int st = scatter(m, t.proj->w, dev_w, t.map, row_bytes);
+    if (!st && m->storage == L0H_I8PC) st = scatter(m, t.proj->s, dev_s, t.map, 2);
+    return st;
+}
+
+int enqueue_step(l0h_model* m, hipStream_t s) {
+    const auto& c = m->cfg;
+    const int H = c.hidden_size;
+    int st = launch_embedding(s, m->token, m->embedding, m->hidden, H, (size_t)H);  // LlmModel.cs:424
+    if (st) return st;
+    for (int li = 0; li < c.num_layers; li++) {
+        Layer& L = m->layers[li];
+        GemvParams g;  // q|k|v: LlmDecoderLayer.cs:167, :296-322
+        g.w_dtype = m->storage;
+        g.w = L.qkv.w;
+        g.scales = L.qkv.s;
+        g.n = L.qkv.n;
+        g.k = H;
+        g.x = m->hidden;
+        g.norm_w = L.input_norm;
+        g.eps = c.rms_norm_eps;
+        g.epilogue = EPI_QKV;
+        g.bias = L.qkv_bias;
+        g.q_out = m->q;
+        g.k_cache = L.k_cache;
+        g.v_cache = L.v_cache;
+        g.cache_dtype = m->cache_dtype;
+        g.position = m->position;
+        g.inv_freq = m->inv_freq;
+        g.rope_scale = m->rope_scale;
+        g.q_dim = m->qd;
+        g.kv_dim = m->kvd;
+        g.head_dim = c.head_dim;
+        g.rotary_dim = m->rot;
+        if ((st = launch_gemv_nk(s, g))) return st;
+
+        AttnParams a;  // :325-327
+        a.q = m->q;
+        a.q_dtype = L0H_F32;
+        a.kc = L.k_cache;
+        a.vc = L.v_cache;
+        a.cache_dtype = m->cache_dtype;
+        a.out = m->attn;
+        a.out_dtype = L0H_F32;
+        a.batch = 1;
+        a.head_dim = c.head_dim;
+        a.nh = c.num_attention_heads;
+        a.nkv = c.num_key_value_heads;
+        a.seq_len_device = m->position;
+        a.seq_len_add = 1;
+        a.max_seq_len = m->max_seq;
+        a.splits = m->attn_splits;
+        a.partials = m->attn_partials;
+        a.tickets = m->attn_tickets;
+        if ((st = launch_attention_decode(s, a))) return st;
+
+        GemvParams o;  // :333, :183
+        o.w_dtype = m->storage;
+        o.w = L.o.w;
+        o.scales = L.o.s;
+        o.n = H;
+        o.k = m->qd;
+        o.x = m->attn;
+        o.epilogue = EPI_RESIDUAL;
+        o.resid = m->hidden;
+        if ((st = launch_gemv_nk(s, o))) return st;
+
+        GemvParams gu;  // :183-189
+        gu.w_dtype = m->storage;
+        gu.w = L.gu.w;
+        gu.scales = L.gu.s;
+        gu.n = 2 * c.intermediate_size;
+        gu.k = H;
+        gu.x = m->hidden;
+        gu.norm_w = L.post_norm;
+        gu.eps = c.rms_norm_eps;
+        gu.epilogue = EPI_SWIGLU;
+        gu.y = m->act;
+        gu.y_dtype = L0H_F32;
+        if ((st = launch_gemv_nk(s, gu))) return st;
+
+        GemvParams d;  // :190-194
+        d.w_dtype = m->storage;
+        d.w = L.down.w;
+        d.scales = L.down.s;
+        d.n = H;
+        d.k = c.intermediate_size;
+        d.x = m->act;
+        d.epilogue = EPI_RESIDUAL;
+        d.resid = m->hidden;
+        if ((st = launch_gemv_nk(s, d))) return st;
+    }
+    GemvParams h;  // AppendHead: LlmModel.cs:394-395
+    h.w_dtype = m->storage;
+    h.w = m->lm.w;
+    h.scales = m->lm.s;
+    h.n = c.vocab_size;
+    h.k = H;
+    h.x = m->hidden;
+    h.norm_w = m->final_norm;
+    h.eps = c.rms_norm_eps;
+    h.epilogue = EPI_STORE;
+    h.y = m->logits;
+    h.y_dtype = L0H_F32;
+    if ((st = launch_gemv_nk(s, h))) return st;
+    ArgmaxFeed feed;  // :398, plus device-side feedback for back-to-back decode
+    feed.token = m->token;
+    feed.position = m->position;
+    feed.step = m->step;
+    feed.out_list = m->out_list;
+    feed.capacity = m->out_capacity;
+    return launch_argmax(s, m->logits, c.vocab_size, m->sampled, m->argmax_partials, m->argmax_ticket, feed);
+}
+
+int ensure_graph(l0h_model* m) {
+    if (m->step_exec) return L0H_OK;
+    hipStream_t s = m->dev->stream;
+    L0H_HIP_TRY(hipStreamSynchronize(s));
+    L0H_HIP_TRY(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    int st = enqueue_step(m, s);
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(s, &g);
+    if (st) {
+        if (g) (void)hipGraphDestroy(g);
+        return st;
+    }
+    if (e != hipSuccess) return fail(L0H_ERR_DEVICE, std::string("capture: ") + hipGetErrorString(e));
+    e = hipGraphInstantiate(&m->step_exec, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) {
+        m->step_exec = nullptr;
+        return fail(L0H_ERR_DEVICE, std::string("hipGraphInstantiate: ") + hipGetErrorString(e));
+    }
+    return L0H_OK;
+}
+
+int check_ready(l0h_model* m) {
+    if (!m) return fail(L0H_ERR_INVALID_ARG, "model is null");
+    if (m->dev->recording) return fail(L0H_ERR_INVALID_OP, "the device is recording");
+    return use_device(m->dev);
+}
+
+// One step of `token` at `position` (LlmModel.Step); the graph does the rest.
+int run_step(l0h_model* m, int token, int position) {
+    if ((unsigned)token >= (unsigned)m->cfg.vocab_size)
+        return fail(L0H_ERR_INVALID_ARG, "token id " + std::to_string(token) + " outside the vocabulary");
+    if (position < 0 || position >= m->max_seq)
+        return fail(L0H_ERR_INVALID_ARG, "position " + std::to_string(position) + " outside the cache");
+    int st = ensure_graph(m);
+    if (st) return st;
+    const int vals[4] = {token, position, 0, 0};  // token, position, sampled, step
+    if ((st = l0h_write(m->dev, m->token, 0, vals, sizeof(vals)))) return st;
+    L0H_HIP_TRY(hipGraphLaunch(m->step_exec, m->dev->stream));
+    return L0H_OK;
+}
+
+}  // namespace
+}  // namespace l0h
+
+extern "C" {
+
+int l0h_model_create(l0h_device* dev, const l0h_model_config* cfg, int precision, int cache_dtype, int max_seq_len,
+                     l0h_model** out) {
+    L0H_CHECK_ARG(out, "out is null");
+    *out = nullptr;
+    L0H_CHECK_ARG(dev && cfg, "null argument");
+    int st = use_device(dev);
+    if (st) return st;
+    const auto& c = *cfg;
+    L0H_CHECK_ARG(c.hidden_size > 0 && c.intermediate_size > 0 && c.num_layers > 0 && c.vocab_size > 0,
+                  "model dimensions must be positive");
+    if (c.num_attention_heads <= 0 || c.num_key_value_heads <= 0 || c.head_dim <= 0 ||
+        c.num_attention_heads % c.num_key_value_heads != 0)
+        return fail(L0H_ERR_INVALID_DATA, "head counts are inconsistent (HfModelConfig.EnsureSupported)");
+    if (c.head_dim % 2) return fail(L0H_ERR_INVALID_DATA, "head_dim must be even for rotary embeddings");
+    L0H_CHECK_ARG(max_seq_len > 0, "max_seq_len must be positive");
+    L0H_CHECK_ARG(cache_dtype == L0H_F16 || cache_dtype == L0H_F32, "cache dtype must be F16 or F32");
+    int storage;
+    switch (precision) {
+    case L0H_PRECISION_AUTO:
+    case L0H_PRECISION_INT8: storage = L0H_I8PC; break;
+    case L0H_PRECISION_FLOAT16: storage = L0H_F16; break;
+    case L0H_PRECISION_BFLOAT16: storage = L0H_BF16; break;
+    case L0H_PRECISION_FLOAT32: storage = L0H_F32; break;
+    default: return fail(L0H_ERR_INVALID_ARG, "unknown precision");
+    }
+    const int epc = storage == L0H_I8PC ? 16 : (storage == L0H_F32 ? 4 : 8);
+    if (c.hidden_size % epc || c.intermediate_size % epc || (c.num_attention_heads * c.head_dim) % epc)
+        return fail(L0H_ERR_UNSUPPORTED, "hidden, intermediate and q widths must be multiples of the load width");
+    if ((size_t)std::max(c.hidden_size, c.intermediate_size) * 4 > 64 * 1024)
+        return fail(L0H_ERR_UNSUPPORTED, "hidden and intermediate sizes up to 16384 are supported");
+
+    auto* m = new l0h_model();
+    m->dev = dev;
+    m->cfg = c;
+    m->storage = storage;
+    m->cache_dtype = cache_dtype;
+    m->max_seq = max_seq_len;
+    m->qd = c.num_attention_heads * c.head_dim;
+    m->kvd = c.num_key_value_heads * c.head_dim;
+    m->rot = c.head_dim;
+    m->layers.resize(c.num_layers);
+
+    // RoPE table (LlmDecoderLayer ctor, :98-104): the table form is used for every config.
+    std::vector<float> inv(c.head_dim / 2);
+    float attn_factor = 1.f;
+    st = l0h_rope_frequencies(c.head_dim, c.rope_theta, c.max_position_embeddings, c.rope_type, c.rope_factor,
+                              c.rope_original_max_position_embeddings, c.rope_beta_fast, c.rope_beta_slow,
+                              c.rope_mscale, c.rope_mscale_all_dim, c.rope_attention_factor, c.rope_low_freq_factor,
+                              c.rope_high_freq_factor, c.rope_truncate, inv.data(), &attn_factor);
+    if (st) {
+        delete m;
+        return st;
+    }
+    m->rope_scale = attn_factor;
+
+    const int H = c.hidden_size, I = c.intermediate_size;
+    const size_t kv_elems = (size_t)max_seq_len * m->kvd;
+    auto bail = [&](int code) {
+        l0h_model_destroy(m);
+        return code;
+    };
+    if ((st = alloc_t(m, inv.size(), &m->inv_freq))) return bail(st);
+    if ((st = l0h_write(dev, m->inv_freq, 0, inv.data(), inv.size() * 4))) return bail(st);
+    for (auto& L : m->layers) {
+        if ((st = alloc_proj(m, L.qkv, m->qd + 2 * m->kvd, H))) return bail(st);
+        if ((st = alloc_proj(m, L.o, H, m->qd))) return bail(st);
+        if ((st = alloc_proj(m, L.gu, 2 * I, H))) return bail(st);
+        if ((st = alloc_proj(m, L.down, H, I))) return bail(st);
+        if ((st = alloc_t(m, (size_t)H, &L.input_norm))) return bail(st);
+        if ((st = alloc_t(m, (size_t)H, &L.post_norm))) return bail(st);
+        if (c.attention_bias && (st = alloc_t(m, (size_t)(m->qd + 2 * m->kvd), &L.qkv_bias))) return bail(st);
+        if ((st = alloc_owned(m, kv_elems * dtype_size(cache_dtype), &L.k_cache))) return bail(st);
+        if ((st = alloc_owned(m, kv_elems * dtype_size(cache_dtype), &L.v_cache))) return bail(st);
+        // zeroed caches (LlmKvCache.cs:30-31), unit norms, zero bias
+        if ((st = l0h_fill_zero(dev, L.k_cache, kv_elems * dtype_size(cache_dtype)))) return bail(st);
+        if ((st = l0h_fill_zero(dev, L.v_cache, kv_elems * dtype_size(cache_dtype)))) return bail(st);
+        if ((st = launch_fill(dev->stream, L.input_norm, 1.f, H))) return bail(st);
+        if ((st = launch_fill(dev->stream, L.post_norm, 1.f, H))) return bail(st);
+        if (L.qkv_bias && (st = launch_fill(dev->stream, L.qkv_bias, 0.f, m->qd + 2 * m->kvd))) return bail(st);
+    }
+    if ((st = alloc_proj(m, m->lm, c.vocab_size, H))) return bail(st);
+    if ((st = alloc_t(m, (size_t)c.vocab_size * H, &m->embedding))) return bail(st);
+    if ((st = alloc_t(m, (size_t)H, &m->final_norm))) return bail(st);
+    if ((st = launch_fill(dev->stream, m->final_norm, 1.f, H))) return bail(st);
+    if ((st = alloc_t(m, (size_t)H, &m->hidden))) return bail(st);
+    if ((st = alloc_t(m, (size_t)m->qd, &m->q))) return bail(st);
+    if ((st = alloc_t(m, (size_t)m->qd, &m->attn))) return bail(st);
+    if ((st = alloc_t(m, (size_t)I, &m->act))) return bail(st);
+    if ((st = alloc_t(m, (size_t)c.vocab_size, &m->logits))) return bail(st);
+    if ((st = alloc_t(m, 4, &m->token))) return bail(st);
+    m->position = m->token + 1;
+    m->sampled = m->token + 2;
+    m->step = m->token + 3;
+    m->out_capacity = max_seq_len;
+    if ((st = alloc_t(m, (size_t)m->out_capacity, &m->out_list))) return bail(st);
+    m->attn_splits = attention_default_splits(1, c.num_key_value_heads, max_seq_len, dev->compute_units);
+    AttnParams a;
+    a.batch = 1;
+    a.nh = c.num_attention_heads;
+    a.nkv = c.num_key_value_heads;
+    a.head_dim = c.head_dim;
+    a.splits = m->attn_splits;
+    if ((st = alloc_owned(m, attention_partials_bytes(a), reinterpret_cast<void**>(&m->attn_partials)))) return bail(st);
+    if ((st = alloc_t(m, (size_t)c.num_key_value_heads, &m->attn_tickets))) return bail(st);
+    if ((st = l0h_fill_zero(dev, m->attn_tickets, c.num_key_value_heads * sizeof(unsigned)))) return bail(st);
+    if ((st = alloc_t(m, (size_t)argmax_blocks(c.vocab_size), &m->argmax_partials))) return bail(st);
+    if ((st = alloc_t(m, 1, &m->argmax_ticket))) return bail(st);
+    if ((st = l0h_fill_zero(dev, m->argmax_ticket, sizeof(unsigned)))) return bail(st);
+    const int zeros[4] = {0, 0, 0, 0};
+    if ((st = l0h_write(dev, m->token, 0, zeros, sizeof(zeros)))) return bail(st);
+    if ((st = l0h_synchronize(dev))) return bail(st);
+    *out = m;
+    return L0H_OK;
+}
+
+int l0h_model_init_random(l0h_model* m, uint64_t seed, float std_dev) {
+    int st = check_ready(m);
+    if (st) return st;
+    const auto& c = m->cfg;
+    hipStream_t s = m->dev->stream;
+    const int H = c.hidden_size, I = c.intermediate_size;
+    // largest HF matrix: gate/up [I, H], down [H, I], q [qd, H], o [H, qd]; lm_head is placed directly
+    const size_t tmp_elems = std::max((size_t)I * H, (size_t)m->qd * H);
+    void* tmp = nullptr;
+    uint16_t* tmp_s = nullptr;
+    if ((st = l0h_alloc(m->dev, tmp_elems * dtype_size(m->storage), &tmp))) return st;
+    if ((st = l0h_alloc(m->dev, (size_t)std::max(std::max(I, H), m->qd) * 2, reinterpret_cast<void**>(&tmp_s)))) {
+        l0h_free(m->dev, tmp);
+        return st;
+    }
+    uint64_t mat = 0;
+    auto gen = [&](void* dst, uint16_t* dst_s, int n, int k) {
+        const uint64_t sd = seed * 1000003ull + (mat++);
+        if (m->storage == L0H_I8PC) return launch_init_normal_i8pc(s, static_cast<int8_t*>(dst), dst_s, n, k, sd, std_dev);
+        return launch_init_normal(s, dst, m->storage, (size_t)n * k, sd, std_dev);
+    };
+    static const char* kNames[] = {"self_attn.q_proj.weight", "self_attn.k_proj.weight", "self_attn.v_proj.weight",
+                                   "self_attn.o_proj.weight", "mlp.gate_proj.weight",    "mlp.up_proj.weight",
+                                   "mlp.down_proj.weight"};
+    for (int li = 0; li < c.num_layers && !st; li++) {
+        for (const char* nm : kNames) {
+            Target t;
+            const std::string full = "model.layers." + std::to_string(li) + "." + nm;
+            if ((st = resolve(m, full, t))) break;
+            if ((st = gen(tmp, tmp_s, t.n, t.k))) break;
+            if ((st = place_matrix(m, t, tmp, tmp_s))) break;
+        }
+    }
+    // lm_head (identity layout); a tied head draws the same values as the embedding (LlmModel.cs:62).
+    const uint64_t lm_mat = mat;
+    if (!st) st = gen(m->lm.w, m->lm.s, c.vocab_size, H);
+    const uint64_t emb_seed = seed * 1000003ull + (c.tie_word_embeddings ? lm_mat : mat++);
+    if (!st) st = launch_init_normal(s, m->embedding, L0H_F32, (size_t)c.vocab_size * H, emb_seed, std_dev);
+    if (!st) st = l0h_synchronize(m->dev);
+    l0h_free(m->dev, tmp);
+    l0h_free(m->dev, tmp_s);
+    return st;
+}
+
+int l0h_model_set_tensor(l0h_model* m, const char* name, const float* host, size_t count, int sixteen_bit_source) {
+    (void)sixteen_bit_source;
+    int st = check_ready(m);
+    if (st) return st;
+    L0H_CHECK_ARG(name && host, "null argument");
+    Target t;
+    if ((st = resolve(m, name, t))) return st;
+    if (t.embedding) {
+        L0H_CHECK_ARG(count == (size_t)t.n * t.k, "wrong element count");
+        if ((st = l0h_write(m->dev, m->embedding, 0, host, count * 4))) return st;
+        // Tied head: lm_head is the embedding matrix (LlmModel.cs:62).
+        if (m->cfg.tie_word_embeddings) return l0h_model_set_tensor(m, "lm_head.weight", host, count, sixteen_bit_source);
+        return L0H_OK;
+    }
+    if (t.vec) {
+        L0H_CHECK_ARG(count == t.vec_count, "wrong element count");
+        if (t.vec_map.empty()) return l0h_write(m->dev, *t.vec, 0, host, count * 4);
+        for (size_t i = 0; i < count; i++)
+            if ((st = l0h_write(m->dev, *t.vec, (size_t)t.vec_map[i] * 4, &host[i], 4))) return st;
+        return L0H_OK;
+    }
+    L0H_CHECK_ARG(count == (size_t)t.n * t.k, "wrong element count");
+    // Convert on the host in HF order, upload, then scatter rows into place.
+    const size_t n = count;
+    std::vector<char> conv;
+    std::vector<uint16_t> sc;
+    if (m->storage == L0H_I8PC) {
+        conv.resize(n);
+        sc.resize(t.n);
+        quantize_rows(host, t.n, t.k, reinterpret_cast<int8_t*>(conv.data()), sc.data());
+    } else if (m->storage == L0H_F32) {
+        conv.resize(n * 4);
+        std::memcpy(conv.data(), host, n * 4);
+    } else {
+        conv.resize(n * 2);
+        auto* h = reinterpret_cast<uint16_t*>(conv.data());
+        for (size_t i = 0; i < n; i++) h[i] = m->storage == L0H_F16 ? host_f32_to_f16(host[i]) : host_f32_to_bf16(host[i]);
+    }
+    void* tmp = nullptr;
+    uint16_t* tmp_s = nullptr;
+    if ((st = l0h_alloc(m->dev, conv.size(), &tmp))) return st;
+    st = l0h_write(m->dev, tmp, 0, conv.data(), conv.size());
+    if (!st && !sc.empty()) {
+        st = l0h_alloc(m->dev, sc.size() * 2, reinterpret_cast<void**>(&tmp_s));
+        if (!st) st = l0h_write(m->dev, tmp_s, 0, sc.data(), sc.size() * 2);
+    }
+    if (!st) st = place_matrix(m, t, tmp, tmp_s);
+    l0h_free(m->dev, tmp);
+    if (tmp_s) l0h_free(m->dev, tmp_s);
+    return st;
+}
+
+int l0h_model_export_matrix(l0h_model* m, const char* name, int* storage, int* out_dim, int* in_dim, void* host_w,
+                            uint16_t* host_scales) {
+    int st = check_ready(m);
+    if (st) return st;
+    L0H_CHECK_ARG(name, "name is null");
+    Target t;
+    if ((st = resolve(m, name, t))) return st;
+    if (!t.proj) return fail(L0H_ERR_INVALID_ARG, std::string(name) + " is not a projection");
+    if (storage) *storage = m->storage;
+    if (out_dim) *out_dim = t.n;
+    if (in_dim) *in_dim = t.k;
+    if (!host_w) return L0H_OK;
+    const size_t row_bytes = (size_t)t.k * dtype_size(m->storage);
+    std::vector<char> all((size_t)t.proj->n * row_bytes);
+    if ((st = l0h_read(m->dev, t.proj->w, 0, all.data(), all.size()))) return st;
+    for (int r = 0; r < t.n; r++)
+        std::memcpy(static_cast<char*>(host_w) + (size_t)r * row_bytes, all.data() + (size_t)t.map[r] * row_bytes, row_bytes);
+    if (m->storage == L0H_I8PC && host_scales) {
+        std::vector<uint16_t> s(t.proj->n);
+        if ((st = l0h_read(m->dev, t.proj->s, 0, s.data(), s.size() * 2))) return st;
+        for (int r = 0; r < t.n; r++) host_scales[r] = s[t.map[r]];
+    }
+    return L0H_OK;
+}
+
+int l0h_model_export_vector(l0h_model* m, const char* name, float* host, size_t count) {
+    int st = check_ready(m);
+    if (st) return st;
+    L0H_CHECK_ARG(name && host, "null argument");
+    Target t;
+    if ((st = resolve(m, name, t))) return st;
+    if (t.embedding) {
+        L0H_CHECK_ARG(count == (size_t)t.n * t.k, "wrong element count");
+        return l0h_read(m->dev, m->embedding, 0, host, count * 4);
+    }
+    if (!t.vec) return fail(L0H_ERR_INVALID_ARG, std::string(name) + " is not a vector");
+    L0H_CHECK_ARG(count == t.vec_count, "wrong element count");
+    if (t.vec_map.empty()) return l0h_read(m->dev, *t.vec, 0, host, count * 4);
+    for (size_t i = 0; i < count; i++)
+        if ((st = l0h_read(m->dev, *t.vec, (size_t)t.vec_map[i] * 4, &host[i], 4))) return st;
+    return L0H_OK;
+}
+
+int l0h_model_kv_cache(l0h_model* m, int layer, void** k, void** v) {
+    L0H_CHECK_ARG(m && k && v, "null argument");
+    L0H_CHECK_ARG(layer >= 0 && layer < m->cfg.num_layers, "layer out of range");
+    *k = m->layers[layer].k_cache;
+    *v = m->layers[layer].v_cache;
+    return L0H_OK;
+}
+
+int l0h_model_logits(l0h_model* m, float** logits) {
+    L0H_CHECK_ARG(m && logits, "null argument");
+    *logits = m->logits;
+    return L0H_OK;
+}
+
+int l0h_model_projection_bytes(l0h_model* m, long long* bytes) {
+    L0H_CHECK_ARG(m && bytes, "null argument");
+    const auto& c = m->cfg;
+    const long long H = c.hidden_size, I = c.intermediate_size, qd = m->qd, kvd = m->kvd;
+    const long long per_layer_elems = (qd + 2 * kvd) * H + H * qd + 2 * I * H + H * I;
+    const long long per_layer_rows = (qd + 2 * kvd) + H + 2 * I + H;
+    const long long lm = (long long)c.vocab_size * H;
+    if (m->storage == L0H_I8PC)
+        *bytes = c.num_layers * (per_layer_elems + 2 * per_layer_rows) + lm + 2LL * c.vocab_size;
+    else
+        *bytes = (c.num_layers * per_layer_elems + lm) * dtype_size(m->storage);
+    return L0H_OK;
+}
+
+int l0h_model_position(l0h_model* m, int* position) {
+    L0H_CHECK_ARG(m && position, "null argument");
+    *position = m->pos;
+    return L0H_OK;
+}
+
+int l0h_model_reset_sequence(l0h_model* m) {
+    L0H_CHECK_ARG(m, "model is null");
+    m->pos = 0;
+    return L0H_OK;
+}
+
+int l0h_model_compute_logits(l0h_model* m, int token, int position, float* host_logits) {
+    int st = check_ready(m);
+    if (st) return st;
+    if ((st = run_step(m, token, position))) return st;
+    if (host_logits) return l0h_read(m->dev, m->logits, 0, host_logits, (size_t)m->cfg.vocab_size * 4);
+    return l0h_synchronize(m->dev);
+}
+
+int l0h_model_prefill(l0h_model* m, const int* ids, int count, float* host_logits) {
+    int st = check_ready(m);
+    if (st) return st;
+    L0H_CHECK_ARG(ids, "prompt is null");
+    L0H_CHECK_ARG(count > 0, "the prompt must contain at least one token");
+    L0H_CHECK_ARG(count <= m->max_seq, "prompt longer than the cache");
+    m->pos = 0;
+    for (int i = 0; i < count; i++)
+        if ((st = run_step(m, ids[i], i))) return st;
+    m->pos = count;
+    if (host_logits) return l0h_read(m->dev, m->logits, 0, host_logits, (size_t)m->cfg.vocab_size * 4);
+    return l0h_synchronize(m->dev);
+}
+
+int l0h_model_decode(l0h_model* m, int token, float* host_logits) {
+    int st = check_ready(m);
+    if (st) return st;
+    if (m->pos >= m->max_seq) return fail(L0H_ERR_INVALID_OP, "the KV cache is full");
+    if ((st = run_step(m, token, m->pos))) return st;
+    m->pos++;
+    if (host_logits) return l0h_read(m->dev, m->logits, 0, host_logits, (size_t)m->cfg.vocab_size * 4);
+    return l0h_synchronize(m->dev);
+}
+
+int l0h_model_decode_greedy_device(l0h_model* m, int token, int steps, int* host_out) {
+    int st = check_ready(m);
+    if (st) return st;
+    L0H_CHECK_ARG(steps >= 0, "steps must not be negative");
+    if (m->pos + steps > m->max_seq) return fail(L0H_ERR_INVALID_ARG, "decode would run past the cache");
+    if (steps == 0) return L0H_OK;
+    if ((st = run_step(m, token, m->pos))) return st;  // writes token, position, step = 0
+    for (int i = 1; i < steps; i++) L0H_HIP_TRY(hipGraphLaunch(m->step_exec, m->dev->stream));
+    m->pos += steps;
+    if (host_out) return l0h_read(m->dev, m->out_list, 0, host_out, (size_t)steps * 4);
+    return l0h_synchronize(m->dev);
+}
+
+int l0h_model_generate_greedy(l0h_model* m, const int* prompt, int prompt_len, int max_new, const int* stop,
+                              int n_stop, int* out, int* n_out) {
+    int st = check_ready(m);
+    if (st) return st;
+    L0H_CHECK_ARG(prompt && n_out && (out || max_new == 0), "null argument");
+    L0H_CHECK_ARG(max_new >= 0, "maxNewTokens must not be negative");
+    L0H_CHECK_ARG(prompt_len > 0, "the prompt must contain at least one token");
+    if (prompt_len + max_new > m->max_seq)
+        return fail(L0H_ERR_INVALID_ARG, "prompt plus new tokens exceeds the cache");
+    *n_out = 0;
+    if (max_new == 0) return L0H_OK;
+    const int saved = m->pos;
+    for (int i = 0; i < prompt_len; i++)
+        if ((st = run_step(m, prompt[i], i))) return st;
+    // The last prompt step chose token 0 of the output (out_list[0]) and advanced the device
+    // position; the remaining steps replay the graph with the token fed back on the device.
+    for (int i = 1; i < max_new; i++) L0H_HIP_TRY(hipGraphLaunch(m->step_exec, m->dev->stream));
+    std::vector<int> toks(max_new);
+    if ((st = l0h_read(m->dev, m->out_list, 0, toks.data(), (size_t)max_new * 4))) return st;
+    int n = 0;
+    for (int i = 0; i < max_new; i++) {
+        out[n++] = toks[i];
+        bool is_stop = false;
+        for (int j = 0; j < n_stop && stop; j++) is_stop |= toks[i] == stop[j];
+        if (is_stop) break;
+    }
+    *n_out = n;
+    m->pos = saved;  // GenerateGreedy leaves Position alone (LlmModel.cs:156-193)
+    return L0H_OK;
+}
+
+int l0h_model_destroy(l0h_model* m) {
+    if (!m) return L0H_OK;
+    (void)use_device(m->dev);
+    if (m->step_exec) (void)hipGraphExecDestroy(m->step_exec);
+    for (void* p : m->owned) l0h_free(m->dev, p);
+    delete m;
+    return L0H_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,394 @@
+"""GPU parity of every kernel on the path, through the C ABI, against the oracle on identical
+seeded inputs. Integer/byte work is compared bit for bit; floating point to the tolerances
+written in each test (fp32 accumulation; fp16/bf16 outputs within 1e-2 relative)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import l0llm_amd as l0
+from oracle import pyoracle as orc
+from tests.helpers import bf16_bits, dequant, rel_err, stored
+
+pytestmark = pytest.mark.gpu
+
+
+def up(device, a):
+    return device.alloc_shared(np.ascontiguousarray(a))
+
+
+# ---- weight-streaming GEMV, [N, K] layout ------------------------------------------------------
+
+GEMV_SHAPES = [
+    (4864, 896),    # Qwen2.5-0.5B up-proj: config 1
+    (1152, 896),    # fused QKV 896 -> 1152
+    (896, 4864),    # down-proj
+    (6144, 4096),   # Llama-3.1-8B fused QKV
+    (4096, 14336),  # Llama-3.1-8B down-proj
+    (100, 48),      # small
+    (30, 17),       # odd shape: generic path
+]
+
+
+@pytest.mark.parametrize("n,k", GEMV_SHAPES)
+@pytest.mark.parametrize("storage", [l0.I8PC, l0.F16, l0.BF16, l0.F32])
+def test_gemv_nk_matches_oracle(device, suite, storage, n, k):
+    rng = np.random.default_rng(n * 7 + k + storage)
+    w = rng.normal(0, 0.02, (n, k)).astype(np.float32)
+    x = rng.normal(0, 1, k).astype(np.float32)
+    dt, ws, s = stored(storage, w)
+    want = orc.gemv_nk(dt, ws, x, s)[0]
+    wb, xb, yb = up(device, ws), up(device, x), device.alloc(n * 4)
+    sb = up(device, s) if s is not None else None
+    suite.gemv_nk(storage, 1, n, k, xb, l0.F32, wb, sb, yb, l0.F32)
+    y = yb.read(np.float32, n)
+    assert rel_err(y, want) < 2e-5, rel_err(y, want)
+    for b in (wb, xb, yb, sb):
+        if b is not None:
+            b.free()
+
+
+def test_gemv_int8_config1_fp16_io(device, suite):
+    """x fp16 [1,896] ~N(0,1); W int8 [4864,896] uniform in [-127,127]; fp16 scales U[1e-3,1e-2]; fp16 y."""
+    rng = np.random.default_rng(101)
+    n, k = 4864, 896
+    q = rng.integers(-127, 128, (n, k)).astype(np.int8)
+    s = rng.uniform(1e-3, 1e-2, n).astype(np.float16)
+    x = rng.normal(0, 1, k).astype(np.float16)
+    want = orc.gemv_nk(orc.I8PC, q, x.astype(np.float32), s)[0]
+    qb, sb, xb, yb = up(device, q), up(device, s), up(device, x), device.alloc(n * 2)
+    suite.gemv_nk(l0.I8PC, 1, n, k, xb, l0.F16, qb, sb, yb, l0.F16)
+    y = yb.read(np.float16, n).astype(np.float32)
+    assert np.max(np.abs(y - want) / np.maximum(np.abs(want), 1e-2)) < 1e-2
+    assert rel_err(y, want) < 1e-3
+
+
+@pytest.mark.parametrize("rows", [2, 3, 5, 8])
+@pytest.mark.parametrize("storage", [l0.I8PC, l0.F16])
+def test_gemv_rows_read_weights_once_per_chunk(device, suite, storage, rows):
+    rng = np.random.default_rng(rows)
+    n, k = 1152, 896
+    w = rng.normal(0, 0.02, (n, k)).astype(np.float32)
+    x = rng.normal(0, 1, (rows, k)).astype(np.float32)
+    dt, ws, s = stored(storage, w)
+    want = orc.gemv_nk(dt, ws, x, s)
+    wb, xb, yb = up(device, ws), up(device, x), device.alloc(rows * n * 4)
+    sb = up(device, s) if s is not None else None
+    suite.gemv_nk(storage, rows, n, k, xb, l0.F32, wb, sb, yb, l0.F32)
+    assert rel_err(yb.read(np.float32, rows * n).reshape(rows, n), want) < 2e-5
+
+
+# ---- LlmMatrix (reference operator surface) ---------------------------------------------------
+
+HF = np.array([[1, 2], [3, 4], [5, 6], [7, 8]], dtype=np.float32)
+
+
+@pytest.mark.parametrize("precision,expect_half", [(l0.PRECISION_AUTO, True), (l0.PRECISION_FLOAT32, False),
+                                                   (l0.PRECISION_FLOAT16, True), (l0.PRECISION_BFLOAT16, False)])
+def test_matrix_known_answer(device, precision, expect_half):  # LlmMatrixTests.cs:99-130 (BF16 source)
+    with l0.LlmMatrix.from_hugging_face(device, HF, True, 4, 2, precision) as m:
+        assert m.is_half == expect_half and m.in_dim == 2 and m.out_dim == 4
+        x, y = up(device, np.array([1, 10], np.float32)), device.alloc(16)
+        m.project(device, x, y)
+        np.testing.assert_array_equal(y.read(np.float32, 4), [21, 43, 65, 87])
+
+
+def test_matrix_auto_keeps_float32_when_values_do_not_fit_half(device):  # LlmMatrixTests.cs:131-146
+    hf = np.array([1, 2, 3, 4, 5, 6, 7, 1e30], np.float32)
+    with l0.LlmMatrix.from_hugging_face(device, hf, True, 4, 2, l0.PRECISION_AUTO) as m:
+        assert not m.is_half
+    with pytest.raises(l0.InvalidDataError):
+        l0.LlmMatrix.from_hugging_face(device, hf, True, 4, 2, l0.PRECISION_FLOAT16)
+
+
+@pytest.mark.parametrize("out_dim,in_dim,half", [(64, 48, True), (64, 48, False), (30, 17, True), (30, 17, False)])
+def test_matrix_upload_project_matches_cpu_loop(device, out_dim, in_dim, half):  # LlmMatrixTests.cs:47-82
+    rng = np.random.default_rng(out_dim + in_dim)
+    w = ((rng.random(in_dim * out_dim) * 2 - 1) * 0.1).astype(np.float32)  # [in, out]
+    x = ((rng.random(in_dim) * 2 - 1)).astype(np.float32)
+    with l0.LlmMatrix.upload(device, w, in_dim, out_dim, half) as m:
+        assert m.is_half == (half and out_dim % 4 == 0)
+        xb, yb = up(device, x), device.alloc(out_dim * 4)
+        m.project(device, xb, yb)
+        wk = w.reshape(in_dim, out_dim)
+        if m.is_half:
+            wk = wk.astype(np.float16).astype(np.float32)
+        expected = x.astype(np.float64) @ wk.astype(np.float64)
+        assert np.max(np.abs(expected - yb.read(np.float32, out_dim))) < 1e-4
+
+
+def test_matrix_int8_storage_and_fallbacks(device):  # LlmMatrixInt8Tests.cs:46-75
+    rng = np.random.default_rng(1)
+    hf = ((rng.random(64 * 96) * 2 - 1) * 0.3).astype(np.float32)
+    with l0.LlmMatrix.from_hugging_face(device, hf, True, 64, 96, l0.PRECISION_INT8) as m:
+        assert m.is_int8 and not m.is_half
+        assert m.size_in_bytes == 64 * 96 + 64 * 2
+    for o, i in ((30, 64), (64, 50)):
+        with l0.LlmMatrix.from_hugging_face(device, rng.random(o * i).astype(np.float32), True, o, i,
+                                            l0.PRECISION_INT8) as m:
+            assert not m.is_int8
+
+
+@pytest.mark.parametrize("rows", [1, 5])
+def test_matrix_int8_within_quantization_error(device, rows):  # LlmMatrixInt8Tests.cs:80-119
+    rng = np.random.default_rng(3)
+    hf = ((rng.random(96 * 160) * 2 - 1) * 0.2).astype(np.float32).reshape(96, 160)
+    x = ((rng.random(rows * 160) * 2 - 1) * 1.5).astype(np.float32).reshape(rows, 160)
+    with l0.LlmMatrix.from_hugging_face(device, hf, True, 96, 160, l0.PRECISION_INT8) as m:
+        xb, yb = up(device, x), device.alloc(rows * 96 * 4)
+        m.project_any(device, rows, xb, yb)
+        y = yb.read(np.float32, rows * 96).reshape(rows, 96)
+        truth = x.astype(np.float64) @ hf.T.astype(np.float64)
+        assert np.sqrt(np.sum((y - truth) ** 2) / np.sum(truth**2)) < 0.02
+        wq, ws = m.data()
+        q = device_read(device, wq, np.int8, 96 * 160).reshape(96, 160)
+        s = device_read(device, ws, np.uint16, 96)
+        oq, os_ = orc.quantize_i8pc(hf)
+        np.testing.assert_array_equal(q, oq)
+        np.testing.assert_array_equal(s, os_)
+        assert rel_err(y, orc.gemv_nk(orc.I8PC, oq, x, os_)) < 2e-5
+
+
+def device_read(device, ptr, dtype, count):
+    b = l0.Buffer(device, count * np.dtype(dtype).itemsize, ptr=ptr, owned=False)
+    return b.read(dtype, count)
+
+
+@pytest.mark.parametrize("rows", [1, 6])
+def test_project_shared_equals_separate(device, rows):  # LlmMatrixInt8Tests.cs:124-149
+    rng = np.random.default_rng(99)
+    outs = [64, 32, 16, 8]
+    ms = [l0.LlmMatrix.from_hugging_face(device, rng.random(o * 128).astype(np.float32) * 0.5 - 0.25, True, o, 128,
+                                         l0.PRECISION_INT8) for o in outs]
+    xb = up(device, rng.random(rows * 128).astype(np.float32) * 2 - 1)
+    shared = [device.alloc(rows * o * 4) for o in outs]
+    separate = [device.alloc(rows * o * 4) for o in outs]
+    l0.LlmMatrix.project_shared(device, rows, xb, list(zip(ms, shared)))
+    for m, sb, pb, o in zip(ms, shared, separate, outs):
+        m.project_any(device, rows, xb, pb)
+        np.testing.assert_array_equal(sb.read(np.float32, rows * o), pb.read(np.float32, rows * o))
+        m.dispose()
+
+
+# ---- reference-layout Gemv / Gemm --------------------------------------------------------------
+
+@pytest.mark.parametrize("n,k,rows,wdt", [(4864, 896, 1, l0.F16), (30, 17, 1, l0.F32), (64, 48, 3, l0.F16),
+                                          (1000, 300, 2, l0.F32)])
+def test_gemv_kn_matches_oracle(device, suite, n, k, rows, wdt):
+    rng = np.random.default_rng(n + k)
+    w = rng.normal(0, 0.05, (k, n)).astype(np.float32)
+    ws = w.astype(np.float16).view(np.uint16) if wdt == l0.F16 else w
+    x = rng.normal(0, 1, (rows, k)).astype(np.float32)
+    want = orc.gemv_kn(wdt, ws, x)
+    wb, xb, yb = up(device, ws), up(device, x), device.alloc(rows * n * 4)
+    suite.gemv_execute_rows(rows, n, k, xb, wb, yb, w_dtype=wdt)
+    assert np.max(np.abs(yb.read(np.float32).reshape(rows, n) - want)) < 1e-4
+
+
+def test_gemm_execute_fp32(device, suite):
+    rng = np.random.default_rng(5)
+    m, n, k = 7, 30, 50
+    w = rng.normal(0, 0.1, (k, n)).astype(np.float32)
+    x = rng.normal(0, 1, (m, k)).astype(np.float32)
+    wb, xb, yb = up(device, w), up(device, x), device.alloc(m * n * 4)
+    suite.gemm_execute(m, n, k, xb, wb, yb)
+    np.testing.assert_allclose(yb.read(np.float32).reshape(m, n), x.astype(np.float64) @ w, atol=1e-5)
+
+
+# ---- element-wise ------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("n,rows,resid", [(896, 1, False), (4096, 1, True), (896, 5, True), (64, 14, False)])
+def test_rmsnorm_matches_oracle(device, suite, n, rows, resid):
+    rng = np.random.default_rng(n + rows)
+    x = rng.normal(0, 30, (rows, n)).astype(np.float32)
+    r = rng.normal(0, 1, (rows, n)).astype(np.float32)
+    w = rng.normal(1, 0.1, n).astype(np.float32)
+    want_x, want = orc.rmsnorm(x, w, 1e-6, residual=r if resid else None)
+    xb, rb, wb, ob = up(device, x), up(device, r), up(device, w), device.alloc(x.nbytes)
+    suite.rmsnorm_execute(xb, rb if resid else None, wb, ob, 1e-6, n, rows, resid)
+    assert rel_err(ob.read().reshape(rows, n), want) < 1e-5
+    np.testing.assert_array_equal(xb.read().reshape(rows, n), want_x)
+    suite.rmsnorm_execute(xb, None, wb, xb, 1e-6, n, rows, False)  # in place (QK-norm form)
+    assert rel_err(xb.read().reshape(rows, n), orc.rmsnorm(want_x, w, 1e-6)[1]) < 1e-5
+
+
+def test_swiglu_add_bias(device, suite):
+    rng = np.random.default_rng(6)
+    g, u = rng.normal(0, 3, 14336).astype(np.float32), rng.normal(0, 1, 14336).astype(np.float32)
+    gb, ub = up(device, g), up(device, u)
+    suite.swiglu_execute(gb, ub, g.size)
+    assert rel_err(gb.read(), orc.swiglu(g, u)) < 1e-6
+    ab = up(device, g)
+    suite.add_execute(ab, ub, g.size)
+    np.testing.assert_array_equal(ab.read(), g + u)
+    x = rng.normal(0, 1, (3, 1152)).astype(np.float32)
+    b = rng.normal(0, 1, 1152).astype(np.float32)
+    xb, bb = up(device, x), up(device, b)
+    suite.bias_add_execute(xb, bb, 1152, 3)
+    np.testing.assert_array_equal(xb.read().reshape(3, 1152), x + b)
+
+
+@pytest.mark.parametrize("hd,nh,nkv,theta,positions", [(64, 14, 2, 1e6, [0, 1, 37, 300]),
+                                                       (128, 32, 8, 5e5, [2047, 4095, 32767])])
+def test_rope_matches_oracle(device, suite, hd, nh, nkv, theta, positions):
+    rng = np.random.default_rng(hd)
+    T = len(positions)
+    q = rng.normal(0, 1, (T, nh * hd)).astype(np.float32)
+    k = rng.normal(0, 1, (T, nkv * hd)).astype(np.float32)
+    pos = np.array(positions, np.int32)
+    qb, kb, pb = up(device, q), up(device, k), up(device, pos)
+    suite.rope_execute(qb, kb, pb, hd, nh, nkv, theta, T)
+    wq, wk = orc.rope_theta(q, k, pos, hd, nh, nkv, theta)
+    assert np.max(np.abs(qb.read().reshape(T, -1) - wq)) < 5e-5
+    assert np.max(np.abs(kb.read().reshape(T, -1) - wk)) < 5e-5
+    inv, _ = orc.rope_frequencies(hd, theta, 131072, "llama3", factor=8.0, original_max=8192)
+    qb2, kb2, ib = up(device, q), up(device, k), up(device, inv)
+    suite.rope_execute_with_frequencies(qb2, kb2, pb, ib, hd, nh, nkv, 0.9, T, hd)
+    wq, wk = orc.rope_table(q, k, pos, inv, hd, nh, nkv, 0.9)
+    assert np.max(np.abs(qb2.read().reshape(T, -1) - wq)) < 5e-5
+    assert np.max(np.abs(kb2.read().reshape(T, -1) - wk)) < 5e-5
+
+
+@pytest.mark.parametrize("cache", [l0.F32, l0.F16])
+def test_kv_store_bit_exact(device, suite, cache):
+    rng = np.random.default_rng(7)
+    kv, max_seq, pos0, T = 1024, 64, 13, 5
+    k = rng.normal(0, 1, (T, kv)).astype(np.float32)
+    v = rng.normal(0, 1, (T, kv)).astype(np.float32)
+    item = 4 if cache == l0.F32 else 2
+    kc, vc = device.alloc(max_seq * kv * item), device.alloc(max_seq * kv * item)
+    kc.zero()
+    vc.zero()
+    suite.kv_cache_store_execute_rows(up(device, k), up(device, v), kc, vc, pos0, kv, T, cache_dtype=cache)
+    okc = np.zeros(max_seq * kv * item, np.uint8)
+    ovc = np.zeros(max_seq * kv * item, np.uint8)
+    orc.kv_store(k, v, okc, ovc, cache, pos0, kv, T)
+    np.testing.assert_array_equal(kc.read(np.uint8), okc)
+    np.testing.assert_array_equal(vc.read(np.uint8), ovc)
+
+
+# ---- attention ---------------------------------------------------------------------------------
+
+ATTN = [(64, 14, 2, 37, l0.F32), (64, 14, 2, 1, l0.F16), (128, 32, 8, 512, l0.F16), (128, 32, 8, 4096, l0.F16),
+        (128, 32, 8, 2049, l0.F32), (128, 8, 8, 300, l0.F16)]
+
+
+@pytest.mark.parametrize("hd,nh,nkv,seq,cache", ATTN)
+def test_attention_decode_matches_oracle(device, suite, hd, nh, nkv, seq, cache):
+    rng = np.random.default_rng(seq + hd)
+    max_seq = seq + 3
+    kf = rng.normal(0, 1, (max_seq, nkv * hd)).astype(np.float32)
+    vf = rng.normal(0, 1, (max_seq, nkv * hd)).astype(np.float32)
+    q = rng.normal(0, 1, nh * hd).astype(np.float32)
+    kc, vc = (kf, vf) if cache == l0.F32 else (kf.astype(np.float16).view(np.uint16), vf.astype(np.float16).view(np.uint16))
+    want = orc.attention_decode(q, kc, vc, cache, hd, nh, nkv, seq, max_seq)
+    ob = device.alloc(nh * hd * 4)
+    suite.attention_execute(up(device, q), up(device, kc), up(device, vc), ob, hd, nh, nkv, seq, max_seq, cache_dtype=cache)
+    out = ob.read()
+    assert rel_err(out, want) < 1e-4, rel_err(out, want)
+    # replayed: the in-kernel split merge resets its counters
+    suite.attention_execute(up(device, q), up(device, kc), up(device, vc), ob, hd, nh, nkv, seq, max_seq, cache_dtype=cache)
+    np.testing.assert_array_equal(ob.read(), out)
+
+
+@pytest.mark.parametrize("batch,seq", [(8, 512), (1, 32768)])
+def test_attention_decode_batched_fp16(device, suite, batch, seq):
+    """GQA 32q/8kv/128, fp16 q/K/V, fp16 out, fp32 softmax."""
+    rng = np.random.default_rng(batch * seq)
+    hd, nh, nkv = 128, 32, 8
+    kf = rng.normal(0, 1, (batch, seq, nkv * hd)).astype(np.float16)
+    vf = rng.normal(0, 1, (batch, seq, nkv * hd)).astype(np.float16)
+    q = rng.normal(0, 1, (batch, nh * hd)).astype(np.float16)
+    ob = device.alloc(batch * nh * hd * 2)
+    suite.attention_decode(up(device, q), l0.F16, up(device, kf.view(np.uint16)), up(device, vf.view(np.uint16)),
+                           l0.F16, ob, l0.F16, batch, hd, nh, nkv, seq, seq)
+    out = ob.read(np.float16).astype(np.float32).reshape(batch, -1)
+    for b in range(batch):
+        want = orc.attention_decode(q[b].astype(np.float32), kf[b].view(np.uint16), vf[b].view(np.uint16), l0.F16,
+                                    hd, nh, nkv, seq, seq)
+        assert np.max(np.abs(out[b] - want)) <= 1e-2 * np.max(np.abs(want)), b
+
+
+def test_attention_prefill_matches_oracle(device, suite):
+    rng = np.random.default_rng(8)
+    hd, nh, nkv, pos0, T, max_seq = 64, 14, 2, 9, 8, 32
+    kc = rng.normal(0, 1, (max_seq, nkv * hd)).astype(np.float32)
+    vc = rng.normal(0, 1, (max_seq, nkv * hd)).astype(np.float32)
+    q = rng.normal(0, 1, (T, nh * hd)).astype(np.float32)
+    ob = device.alloc(T * nh * hd * 4)
+    suite.attention_execute_prefill(up(device, q), up(device, kc), up(device, vc), ob, hd, nh, nkv, pos0, T, max_seq)
+    want = orc.attention_prefill(q, kc, vc, orc.F32, hd, nh, nkv, pos0, T, max_seq)
+    assert rel_err(ob.read(), want) < 1e-4
+
+
+# ---- embedding, copy, greedy pick --------------------------------------------------------------
+
+def test_embedding_copy_sampling(device, suite):
+    rng = np.random.default_rng(9)
+    vocab, h = 128256, 64
+    table = rng.normal(0, 1, (vocab, h)).astype(np.float32)
+    ids = np.array([5, 128255, 0], np.int32)
+    ob = device.alloc(3 * h * 4)
+    suite.embedding_execute(up(device, ids), up(device, table), ob, h, 3 * h)
+    np.testing.assert_array_equal(ob.read(), orc.embedding(ids, table, h, 3 * h))
+    cb = device.alloc(h * 4)
+    suite.copy_execute(ob, cb, 2 * h, h)
+    np.testing.assert_array_equal(cb.read(), table[0])
+    logits = rng.normal(0, 1, vocab).astype(np.float32)
+    sb = device.alloc(4)
+    for tie in (None, (100, 90000), (127000, 5)):
+        lg = logits.copy()
+        if tie:
+            lg[list(tie)] = 50.0
+        suite.sampling_execute(up(device, lg), sb, 0.0, 0.0, vocab)
+        assert int(sb.read(np.int32)[0]) == orc.argmax(lg)
+    with pytest.raises(l0.UnsupportedError):
+        suite.sampling_execute(up(device, logits), sb, 0.7, 0.5, vocab)
+
+
+# ---- recording (one graph per recorded list) ---------------------------------------------------
+
+def test_recording_matches_eager_and_replays(device, suite):
+    rng = np.random.default_rng(10)
+    n, k = 1152, 896
+    q, s = orc.quantize_i8pc(rng.normal(0, 0.02, (n, k)).astype(np.float32))
+    x = rng.normal(0, 1, k).astype(np.float32)
+    w = rng.normal(1, 0.1, k).astype(np.float32)
+    qb, sb, xb, wb = up(device, q), up(device, s), up(device, x), up(device, w)
+    nb, yb = device.alloc(k * 4), device.alloc(n * 4)
+    suite.rmsnorm_execute(xb, None, wb, nb, 1e-6, k, 1, False)
+    suite.gemv_nk(l0.I8PC, 1, n, k, nb, l0.F32, qb, sb, yb, l0.F32)
+    eager = yb.read()
+    for _ in range(3):
+        yb.zero()
+        device.begin_recording()
+        assert device.is_recording
+        suite.rmsnorm_execute(xb, None, wb, nb, 1e-6, k, 1, False)
+        suite.gemv_nk(l0.I8PC, 1, n, k, nb, l0.F32, qb, sb, yb, l0.F32)
+        device.end_recording()
+        np.testing.assert_array_equal(yb.read(), eager)
+    device.begin_recording()
+    with pytest.raises(l0.InvalidOperationError):
+        yb.read()
+    device.abort_recording()
+    assert not device.is_recording
+
+
+# ---- MFMA prefill GEMM -------------------------------------------------------------------------
+
+@pytest.mark.parametrize("m,n,k", [(64, 256, 512), (128, 3072, 2048), (512, 2048, 2048), (100, 200, 128),
+                                   (128, 64, 8192), (33, 40, 70)])
+@pytest.mark.parametrize("dtype", [l0.BF16, l0.F16])
+def test_gemm_nk_matches_oracle(device, suite, m, n, k, dtype):
+    rng = np.random.default_rng(m + n + k)
+    x = rng.normal(0, 1, (m, k)).astype(np.float32)
+    w = rng.normal(0, 0.02, (n, k)).astype(np.float32)
+    if dtype == l0.BF16:
+        xs, ws = bf16_bits(x), bf16_bits(w)
+    else:
+        xs, ws = x.astype(np.float16).view(np.uint16), w.astype(np.float16).view(np.uint16)
+    xf = dequant(dtype, xs, None).astype(np.float32)
+    want = orc.gemv_nk(dtype, ws, xf)
+    yb = device.alloc(m * n * 4)
+    suite.gemm_nk(dtype, m, n, k, up(device, xs), up(device, ws), yb, l0.F32)
+    assert rel_err(yb.read().reshape(m, n), want) < 2e-5

@@ -1,0 +1,184 @@
+"""GPU parity of the whole decode step (LlmModel / LlmDecoderLayer restated as the fused step
+graph) against the oracle and against Hugging Face transformers logits."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import l0llm_amd as l0
+from oracle import pyoracle as orc
+from tests.helpers import PROJECTIONS, load_hf, rel_err, rope_table_for
+
+pytestmark = pytest.mark.gpu
+
+STORAGE = {l0.PRECISION_FLOAT32: l0.F32, l0.PRECISION_FLOAT16: l0.F16, l0.PRECISION_BFLOAT16: l0.BF16,
+           l0.PRECISION_INT8: l0.I8PC}
+
+
+def hf_config(cfg: dict) -> l0.HfConfig:
+    rp = cfg["rope"]
+    scaling = None
+    if rp.get("rope_type", "default") != "default":
+        scaling = l0.RopeScaling(type=rp["rope_type"], factor=rp.get("factor", 1.0),
+                                 original_max_position_embeddings=rp.get("original_max_position_embeddings"),
+                                 low_freq_factor=rp.get("low_freq_factor", 1.0),
+                                 high_freq_factor=rp.get("high_freq_factor", 4.0))
+    return l0.HfConfig(hidden_size=cfg["hidden_size"], intermediate_size=cfg["intermediate_size"],
+                       num_layers=cfg["num_layers"], num_attention_heads=cfg["num_attention_heads"],
+                       num_key_value_heads=cfg["num_key_value_heads"], head_dim=cfg["head_dim"],
+                       vocab_size=cfg["vocab_size"], max_position_embeddings=cfg["max_position_embeddings"],
+                       rms_norm_eps=cfg["rms_norm_eps"], rope_theta=cfg["rope_theta"],
+                       attention_bias=cfg["attention_bias"], tie_word_embeddings=cfg["tie_word_embeddings"],
+                       rope_scaling=scaling)
+
+
+def load_model(device, d, precision, cache, max_seq=64):
+    m = l0.LlmModel(device, hf_config(d["cfg"]), precision=precision, cache_dtype=cache, max_seq_len=max_seq)
+    for name, w in d["weights"].items():
+        m.set_tensor(name, w)
+    return m
+
+
+def exported_oracle(m: l0.LlmModel, cfg: dict, cache: int, max_seq: int) -> orc.Model:
+    """Oracle over the weights exactly as the device stores them (read back through the ABI)."""
+    H, L = cfg["hidden_size"], cfg["num_layers"]
+    w = {"model.embed_tokens.weight": m.export_vector("model.embed_tokens.weight", cfg["vocab_size"] * H),
+         "model.norm.weight": m.export_vector("model.norm.weight", H)}
+    st, lm, s = m.export_matrix("lm_head.weight")
+    w["lm_head.weight"] = (st, lm, s)
+    for i in range(L):
+        p = f"model.layers.{i}."
+        for n in PROJECTIONS:
+            w[p + n] = m.export_matrix(p + n)
+        w[p + "input_layernorm.weight"] = m.export_vector(p + "input_layernorm.weight", H)
+        w[p + "post_attention_layernorm.weight"] = m.export_vector(p + "post_attention_layernorm.weight", H)
+        if cfg.get("attention_bias"):
+            for n, width in (("q", cfg["num_attention_heads"]), ("k", cfg["num_key_value_heads"]),
+                             ("v", cfg["num_key_value_heads"])):
+                w[p + f"self_attn.{n}_proj.bias"] = m.export_vector(p + f"self_attn.{n}_proj.bias", width * cfg["head_dim"])
+    inv, att = rope_table_for(cfg)
+    return orc.Model(cfg, w, inv, att, cache, max_seq)
+
+
+@pytest.mark.parametrize("name", ["llama", "qwen2"])
+def test_fp32_model_matches_transformers(device, name):
+    """fp32 weights, fp32 cache: logits at every prompt position and the greedy continuation."""
+    d = load_hf(name)
+    with load_model(device, d, l0.PRECISION_FLOAT32, l0.F32) as m:
+        for t, tok in enumerate(d["prompt"]):
+            lg = m.compute_logits(tok, t)
+            assert rel_err(lg, d["prompt_logits"][t]) < 1e-4, t
+        out = m.generate_greedy(d["prompt"], len(d["generated"]))
+        assert out == d["generated"]
+
+
+@pytest.mark.parametrize("precision", [l0.PRECISION_INT8, l0.PRECISION_FLOAT16, l0.PRECISION_BFLOAT16])
+@pytest.mark.parametrize("name", ["llama", "qwen2"])
+def test_quantized_model_matches_oracle(device, name, precision):
+    """Stored weights equal the oracle's conversion; logits match the oracle step by step."""
+    d = load_hf(name)
+    cfg = d["cfg"]
+    with load_model(device, d, precision, l0.F16) as m:
+        from tests.helpers import stored
+        st, w, s = m.export_matrix("model.layers.1.self_attn.q_proj.weight")
+        ost, ow, os_ = stored(STORAGE[precision], d["weights"]["model.layers.1.self_attn.q_proj.weight"])
+        assert st == ost
+        np.testing.assert_array_equal(w.view(np.uint8), np.ascontiguousarray(ow).view(np.uint8))
+        if s is not None:
+            np.testing.assert_array_equal(s, os_)
+        om = exported_oracle(m, cfg, orc.F16, 64)
+        seq = list(d["prompt"])
+        for t in range(len(seq) + 6):
+            tok = seq[t]
+            lg = m.compute_logits(tok, t)
+            onext, olg = om.step(tok, t)
+            assert rel_err(lg, olg) < 2e-3, t
+            if t >= len(d["prompt"]) - 1:
+                nxt = int(np.argmax(lg))
+                if nxt != onext:
+                    assert orc.top2_margin(olg) < 1e-3, (t, nxt, onext)
+                seq.append(onext)
+
+
+def test_prefill_matches_sequential_decode(device):  # Qwen25PrefillTests.cs:41-75
+    d = load_hf("qwen2")
+    with load_model(device, d, l0.PRECISION_INT8, l0.F16) as m:
+        prompt = d["prompt"][:7]
+        seq = None
+        for i, t in enumerate(prompt):
+            seq = m.compute_logits(t, i)
+        nxt = int(np.argmax(seq))
+        seq_after = m.compute_logits(nxt, len(prompt))
+        batched = m.prefill(prompt)
+        assert m.position == len(prompt)
+        after = m.decode(nxt)
+        assert m.position == len(prompt) + 1
+        assert int(np.argmax(batched)) == nxt
+        assert np.max(np.abs(seq - batched)) < 2e-3
+        assert np.max(np.abs(seq_after - after)) < 2e-3
+
+
+def test_generate_greedy_matches_step_loop_and_stops(device):
+    d = load_hf("llama")
+    with load_model(device, d, l0.PRECISION_INT8, l0.F16) as m:
+        gen = m.generate_greedy(d["prompt"], 10)
+        assert len(gen) == 10
+        logits = m.prefill(d["prompt"])
+        loop = [int(np.argmax(logits))]
+        while len(loop) < 10:
+            loop.append(int(np.argmax(m.decode(loop[-1]))))
+        assert gen == loop
+        m.prefill(d["prompt"])
+        dev_loop = m.decode_greedy_device(loop[0], 9)
+        assert [loop[0]] + dev_loop.tolist() == loop
+        stop = gen[3]
+        cut = m.generate_greedy(d["prompt"], 10, stop_token_ids=[stop])
+        assert cut == gen[: gen.index(stop) + 1]
+        with pytest.raises(l0.InvalidArgumentError):
+            m.generate_greedy(d["prompt"], 100)
+        with pytest.raises(l0.InvalidArgumentError):
+            m.compute_logits(d["cfg"]["vocab_size"], 0)
+
+
+def _random_model(device, hf: l0.HfConfig, max_seq: int, seed: int) -> l0.LlmModel:
+    m = l0.LlmModel(device, hf, precision=l0.PRECISION_INT8, cache_dtype=l0.F16, max_seq_len=max_seq)
+    m.init_random(seed, 0.02)
+    return m
+
+
+def _as_cfg(hf: l0.HfConfig) -> dict:
+    return dict(vocab_size=hf.vocab_size, hidden_size=hf.hidden_size, intermediate_size=hf.intermediate_size,
+                num_layers=hf.num_layers, num_attention_heads=hf.num_attention_heads,
+                num_key_value_heads=hf.num_key_value_heads, head_dim=hf.head_dim,
+                max_position_embeddings=hf.max_position_embeddings, rms_norm_eps=hf.rms_norm_eps,
+                rope_theta=hf.rope_theta, tie_word_embeddings=hf.tie_word_embeddings,
+                attention_bias=hf.attention_bias, rope={"rope_type": "default", "rope_theta": hf.rope_theta})
+
+
+QWEN05 = l0.HfConfig(hidden_size=896, intermediate_size=4864, num_layers=4, num_attention_heads=14,
+                     num_key_value_heads=2, head_dim=64, vocab_size=151936, max_position_embeddings=32768,
+                     rms_norm_eps=1e-6, rope_theta=1e6, attention_bias=True, tie_word_embeddings=True)
+LLAMA8B = l0.HfConfig(hidden_size=4096, intermediate_size=14336, num_layers=32, num_attention_heads=32,
+                      num_key_value_heads=8, head_dim=128, vocab_size=128256, max_position_embeddings=131072,
+                      rms_norm_eps=1e-5, rope_theta=500000.0)
+
+
+@pytest.mark.parametrize("hf,steps", [(QWEN05, 6), (LLAMA8B, 4)], ids=["qwen2.5-0.5b-4layers", "llama3.1-8b"])
+def test_random_int8_model_matches_oracle(device, hf, steps):
+    """Int8 per-channel random-init model at the real shapes: the device's weights are read
+    back and the oracle runs the same steps; logits agree and greedy ids agree unless the
+    oracle's own top-2 gap is below the accumulation noise."""
+    max_seq = 16
+    with _random_model(device, hf, max_seq, seed=599) as m:
+        cfg = _as_cfg(hf)
+        om = exported_oracle(m, cfg, orc.F16, max_seq)
+        rng = np.random.default_rng(599)
+        tok = int(rng.integers(0, hf.vocab_size))
+        for t in range(steps):
+            lg = m.compute_logits(tok, t)
+            onext, olg = om.step(tok, t)
+            assert rel_err(lg, olg) < 2e-3, t
+            gnext = int(np.argmax(lg))
+            if gnext != onext:
+                assert orc.top2_margin(olg) < 1e-3 * np.max(np.abs(olg)), (t, gnext, onext)
+            tok = onext
