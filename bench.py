@@ -1,0 +1,192 @@
+#!/usr/bin/env python3
+"""Decode throughput of a Llama-3.1-8B-shaped int8 weight-only model on one MI355X.
+
+Workload: 32 layers, hidden 4096, intermediate 14336, 32 q / 8 kv heads, head_dim 128, vocab
+128256, RMSNorm eps 1e-5, RoPE theta 5e5; random-init weights N(0, 0.02) stored as int8 with one
+fp16 scale per output row; fp16 KV cache. Batch 1: a 2048-token prompt of seeded random ids is
+prefilled, then greedy decode. A step is one generated token (all 32 layers, lm_head, argmax);
+the timed region is `--steps` back-to-back steps at positions 2048.. with every input resident
+in HBM, bracketed by device synchronisation.
+
+The JSON line also carries:
+  roofline      the int8 weight-streaming GEMV (the dominant kernel: q|k|v, O, gate|up, down and
+                lm_head launches): algorithmic bytes / HIP-event duration per launch, measured
+                live on the model's stream over `--profile-steps` eager steps, against 8 TB/s
+  kernels       the same per kernel kind
+  cpu_baseline  the CPU oracle (fp64-accumulating C) running the same model's decode steps on the
+                host cores, for a bounded sample of `--cpu-tokens` tokens
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "int8 decode GEMV HBM GB/s (% of peak); 8B-shape decode tokens/s at 1 GPU"
+GEMV_KINDS = ("qkv", "o_proj", "gate_up", "down", "lm_head")
+PROJECTIONS = ("self_attn.q_proj.weight", "self_attn.k_proj.weight", "self_attn.v_proj.weight",
+               "self_attn.o_proj.weight", "mlp.gate_proj.weight", "mlp.up_proj.weight", "mlp.down_proj.weight")
+
+
+def llama8b():
+    import l0llm_amd as l0
+    return l0.HfConfig(hidden_size=4096, intermediate_size=14336, num_layers=32, num_attention_heads=32,
+                       num_key_value_heads=8, head_dim=128, vocab_size=128256, max_position_embeddings=131072,
+                       rms_norm_eps=1e-5, rope_theta=500000.0)
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def kernel_table(samples: list[list[dict]]) -> dict:
+    agg: dict[str, dict] = {}
+    for step in samples:
+        for e in step:
+            a = agg.setdefault(e["kind"], dict(launches=0, us=0.0, bytes=0.0))
+            a["launches"] += 1
+            a["us"] += e["us"]
+            a["bytes"] += e["bytes"]
+    out = {}
+    for k, a in agg.items():
+        gbs = a["bytes"] / (a["us"] * 1e-6) / 1e9 if a["us"] > 0 else 0.0
+        out[k] = dict(launches_per_step=a["launches"] // len(samples), avg_us=round(a["us"] / a["launches"], 3),
+                      bytes_per_launch=round(a["bytes"] / a["launches"]), gbs=round(gbs, 1),
+                      frac=round(gbs / HBM_PEAK_GBS, 4))
+    return out
+
+
+def cpu_baseline(model, cfg, tokens: int, position: int) -> dict:
+    from oracle import pyoracle as orc
+
+    H = cfg.hidden_size
+    w = {"model.embed_tokens.weight": model.export_vector("model.embed_tokens.weight", cfg.vocab_size * H),
+         "model.norm.weight": model.export_vector("model.norm.weight", H),
+         "lm_head.weight": model.export_matrix("lm_head.weight")}
+    for i in range(cfg.num_layers):
+        p = f"model.layers.{i}."
+        for n in PROJECTIONS:
+            w[p + n] = model.export_matrix(p + n)
+        for n in ("input_layernorm.weight", "post_attention_layernorm.weight"):
+            w[p + n] = model.export_vector(p + n, H)
+    inv, att = orc.rope_frequencies(cfg.head_dim, cfg.rope_theta, cfg.max_position_embeddings)
+    c = dict(vocab_size=cfg.vocab_size, hidden_size=H, intermediate_size=cfg.intermediate_size,
+             num_layers=cfg.num_layers, num_attention_heads=cfg.num_attention_heads,
+             num_key_value_heads=cfg.num_key_value_heads, head_dim=cfg.head_dim, rms_norm_eps=cfg.rms_norm_eps)
+    om = orc.Model(c, w, inv, att, orc.F16, position + tokens + 1)
+    tok = 1
+    om.step(tok, position)  # page in the weights once
+    t0 = time.perf_counter()
+    for i in range(tokens):
+        tok, _ = om.step(tok, position + 1 + i)
+    dt = time.perf_counter() - t0
+    return dict(value=round(tokens / dt, 4), unit="tokens/s", cores=orc.num_threads(), kind="port",
+                sample=f"{tokens} decode tokens of the same int8 model (all 32 layers + lm_head + argmax) at "
+                       f"positions {position + 1}..{position + tokens}, fp64-accumulating C oracle, "
+                       f"{orc.num_threads()} OpenMP threads")
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128, help="timed decode steps (generated tokens)")
+    ap.add_argument("--warmup", type=int, default=8, help="untimed decode steps before the timed region")
+    ap.add_argument("--ctx", type=int, default=2048, help="prefilled KV-cache length")
+    ap.add_argument("--profile-steps", type=int, default=3)
+    ap.add_argument("--cpu-tokens", type=int, default=2, help="tokens in the CPU baseline sample (0: skip)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one MI355X: the path runs on a single GPU (no sharding or collectives "
+              "in this build); run it with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import l0llm_amd as l0
+
+    cfg = llama8b()
+    dev = l0.Device(0)
+    max_seq = args.ctx + args.steps + args.profile_steps + 8
+    log(f"device {dev.name}; building the model (max_seq {max_seq})")
+    model = l0.LlmModel(dev, cfg, precision=l0.PRECISION_INT8, cache_dtype=l0.F16, max_seq_len=max_seq)
+    model.init_random(500, 0.02)
+    prompt = np.random.default_rng(599).integers(0, cfg.vocab_size, args.ctx).astype(np.int32)
+
+    # Warm up the captured step graph on a short prompt, then prefill the full context.
+    logits = model.prefill(prompt[:8])
+    if args.warmup:
+        model.decode_greedy_device(int(np.argmax(logits)), args.warmup)
+    t0 = time.perf_counter()
+    logits = model.prefill(prompt)
+    log(f"prefilled {args.ctx} tokens in {time.perf_counter() - t0:.2f} s")
+    first = int(np.argmax(logits))
+
+    dev.synchronize()
+    t0 = time.perf_counter()
+    toks = model.decode_greedy_device(first, args.steps)
+    dev.synchronize()
+    dt = time.perf_counter() - t0
+    tps = args.steps / dt
+    log(f"decoded {args.steps} tokens in {dt * 1e3:.2f} ms: {tps:.1f} tokens/s; first ids {toks[:8].tolist()}")
+
+    pos = model.position
+    samples = [model.profile_step(int(toks[-1]), pos + i) for i in range(args.profile_steps)]
+    table = kernel_table(samples)
+    gemv_us = sum(table[k]["avg_us"] * table[k]["launches_per_step"] for k in GEMV_KINDS)
+    gemv_bytes = sum(table[k]["bytes_per_launch"] * table[k]["launches_per_step"] for k in GEMV_KINDS)
+    launches = sum(table[k]["launches_per_step"] for k in GEMV_KINDS)
+    achieved = gemv_bytes / (gemv_us * 1e-6) / 1e9
+    step_bytes = sum(t["bytes_per_launch"] * t["launches_per_step"] for t in table.values())
+    traffic = None
+    tf = ROOT / "profiles" / "gemv_i8_traffic.json"
+    if tf.exists():
+        traffic = json.loads(tf.read_text()).get("hbm_bytes_per_launch")
+    log(f"int8 GEMV: {achieved:.0f} GB/s over {launches} launches/step ({gemv_us:.0f} us/step)")
+
+    cpu = None
+    if args.cpu_tokens > 0:
+        log("CPU baseline: exporting the model and running the oracle")
+        cpu = cpu_baseline(model, cfg, args.cpu_tokens, pos + args.profile_steps)
+        log(f"CPU baseline {cpu['value']} tokens/s on {cpu['cores']} threads")
+
+    line = {
+        "metric": METRIC,
+        "value": round(tps, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dt * 1e3 / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic: random-init N(0,0.02) weights quantized to int8 per output row, seeded random prompt ids",
+        "config": {"workload": f"llama3.1-8b-shaped int8 weight-only greedy decode, batch 1, "
+                               f"{args.ctx}-token prefilled KV cache (fp16), {args.steps} generated tokens",
+                   "layers": 32, "hidden": 4096, "intermediate": 14336, "heads": 32, "kv_heads": 8,
+                   "head_dim": 128, "vocab": 128256, "batch": 1, "ctx": args.ctx},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": "gemv_nk_kernel<I8PC> (q|k|v, O, gate|up, down, lm_head)",
+                     "bytes_per_launch": round(gemv_bytes / launches), "avg_us_per_launch": round(gemv_us / launches, 3)},
+        "step_roofline": {"bytes_per_step": round(step_bytes), "ideal_tokens_per_s": round(HBM_PEAK_GBS * 1e9 / step_bytes, 1),
+                          "frac": round(tps * step_bytes / (HBM_PEAK_GBS * 1e9), 4)},
+        "kernels": table,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    model.dispose()
+    dev.close()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

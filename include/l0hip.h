@@ -328,6 +328,29 @@ int l0h_model_generate_greedy(l0h_model* model, const int* host_prompt, int prom
  * back to back and the sampled token fed back on the device (no host round trip per token);
  * starts from `token` at Position and advances Position. host_out receives the tokens. */
 int l0h_model_decode_greedy_device(l0h_model* model, int token, int steps, int* host_out);
+/* Kernel kinds of one decode step. */
+#define L0H_KERNEL_EMBEDDING 0
+#define L0H_KERNEL_QKV 1       /* input RMSNorm + q|k|v GEMV + bias + RoPE + KV store */
+#define L0H_KERNEL_ATTENTION 2
+#define L0H_KERNEL_O_PROJ 3    /* O GEMV + residual */
+#define L0H_KERNEL_GATE_UP 4   /* post-attention RMSNorm + gate|up GEMV + SwiGLU */
+#define L0H_KERNEL_DOWN 5      /* down GEMV + residual */
+#define L0H_KERNEL_LM_HEAD 6   /* final RMSNorm + lm_head GEMV */
+#define L0H_KERNEL_ARGMAX 7
+
+typedef struct {
+    int kind;            /* L0H_KERNEL_* */
+    int layer;           /* decoder layer, -1 for model-level kernels */
+    float microseconds;  /* HIP-event time of the launch on the model's stream */
+    double bytes;        /* algorithmic HBM bytes of the launch (weights, scales, activations, cache) */
+} l0h_kernel_timing;
+
+/* One decode step of `token` at `position` run eagerly, kernel by kernel, with a HIP event pair
+ * around every launch (the eager per-stage mode of LlmDecoderLayer.Probe, LlmDecoderLayer.cs:113-119,
+ * LlmModel.cs:415-417). Same kernels and results as the graph step. Writes up to `capacity`
+ * entries to host_out and the number of launches to count. */
+int l0h_model_profile_step(l0h_model* model, int token, int position, l0h_kernel_timing* host_out,
+                           int capacity, int* count);
 /* LlmModel.Dispose (LlmModel.cs:308). */
 int l0h_model_destroy(l0h_model* model);
 

@@ -132,7 +132,7 @@ def _ctype(param: str):
 def _load() -> ctypes.CDLL:
     if not LIB_PATH.exists():
         raise ImportError(
-            f"{LIB_PATH} is missing: build it with `python -m l0llm_amd.build` (hipcc, gfx950). "
+            f"{LIB_PATH} is missing: build it with `python l0llm_amd/build.py` (hipcc, gfx950). "
             "There is no CPU fallback.")
     lib = ctypes.CDLL(str(LIB_PATH))
     for name, (ret, params) in declared_functions().items():

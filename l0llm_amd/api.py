@@ -404,6 +404,16 @@ class HfConfig:
                            s.low_freq_factor, s.high_freq_factor, int(s.truncate))
 
 
+KERNEL_KINDS = ("embedding", "qkv", "attention", "o_proj", "gate_up", "down", "lm_head", "argmax")
+
+
+class KernelTiming(ctypes.Structure):
+    """l0h_kernel_timing."""
+
+    _fields_ = [("kind", ctypes.c_int), ("layer", ctypes.c_int), ("microseconds", ctypes.c_float),
+                ("bytes", ctypes.c_double)]
+
+
 class LlmModel:
     """LlmModel (LlmModel.cs): a decoder resident on the device, one sequence at a time."""
 
@@ -492,6 +502,15 @@ class LlmModel:
                                             max_new_tokens, stop.ctypes.data_as(ctypes.c_void_p),
                                             len(stop_token_ids), out.ctypes.data_as(ctypes.c_void_p), ctypes.byref(n)))
         return out[: n.value].tolist()
+
+    def profile_step(self, token: int, position: int) -> list[dict]:
+        """One eager decode step with a HIP-event pair around every launch: kind, layer, us, bytes."""
+        cap = 8 * self.config.num_layers + 16
+        buf = (KernelTiming * cap)()
+        n = ctypes.c_int()
+        check(lib.l0h_model_profile_step(self.handle, token, position, buf, cap, ctypes.byref(n)))
+        return [dict(kind=KERNEL_KINDS[e.kind], layer=e.layer, us=e.microseconds, bytes=e.bytes)
+                for e in buf[: n.value]]
 
     def decode_greedy_device(self, token: int, steps: int) -> np.ndarray:
         out = np.empty(max(steps, 1), dtype=np.int32)

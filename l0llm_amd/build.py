@@ -1,5 +1,6 @@
 """Builds libl0hip.so (gfx950) in-tree with hipcc: one object per source, compiled in
-parallel, linked into l0llm_amd/libl0hip.so. Run as `python -m l0llm_amd.build`."""
+parallel, linked into l0llm_amd/libl0hip.so. Run as `python l0llm_amd/build.py` (this file does
+not import the package, whose import loads the library being rebuilt)."""
 from __future__ import annotations
 
 import concurrent.futures as cf

@@ -27,14 +27,15 @@ __device__ __forceinline__ float dpp_src(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, false));
 }
 
-// Sum over the LPP lanes that share a position (a quad pair or a full 16-lane row).
+// Sum over the LPP lanes that share a position (2, 4 or 8 lanes of a row, or the full
+// 16-lane row), left in every lane of the group.
 template <int LPP>
 __device__ __forceinline__ float group_sum(float v) {
     v += dpp_src<0xB1, 0xf>(v);  // quad_perm [1,0,3,2]
-    v += dpp_src<0x4E, 0xf>(v);  // quad_perm [2,3,0,1]
+    if constexpr (LPP >= 4) v += dpp_src<0x4E, 0xf>(v);  // quad_perm [2,3,0,1]
     if constexpr (LPP == 8) {
         v += dpp_src<0x141, 0xf>(v);  // row_half_mirror: quad 0 <-> quad 1
-    } else {
+    } else if constexpr (LPP == 16) {
         v += dpp_src<0x124, 0xf>(v);  // row_ror:4
         v += dpp_src<0x128, 0xf>(v);  // row_ror:8
     }
@@ -147,7 +148,7 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(const AttnParams p,
 #pragma unroll
                     for (int d = 0; d < 8; d++) s = fmaf(qr[h][d], kf[d], s);
                     s = group_sum<LPP>(s);
-                    if (lg == h && t < n) s_scores[h * kChunkMax + t] = s;
+                    if (lg == h % LPP && t < n) s_scores[h * kChunkMax + t] = s;
                 }
             }
         }
@@ -280,8 +281,8 @@ int launch_hd(hipStream_t s, const AttnParams& p, int seq_len_step, size_t cache
 }
 
 int launch_any(hipStream_t s, const AttnParams& p, int seq_len_step, size_t cache_batch_stride) {
-    if (p.head_dim != 64 && p.head_dim != 128)
-        return fail(L0H_ERR_UNSUPPORTED, "attention supports head_dim 64 and 128");
+    if (p.head_dim != 16 && p.head_dim != 32 && p.head_dim != 64 && p.head_dim != 128)
+        return fail(L0H_ERR_UNSUPPORTED, "attention supports head_dim 16, 32, 64 and 128");
     if (p.nkv <= 0 || p.nh % p.nkv != 0 || p.nh / p.nkv > kGroupMax)
         return fail(L0H_ERR_UNSUPPORTED, "attention needs n_heads a multiple of n_kv_heads, at most 8 per group");
     if (p.cache_dtype != L0H_F16 && p.cache_dtype != L0H_F32)
@@ -289,8 +290,12 @@ int launch_any(hipStream_t s, const AttnParams& p, int seq_len_step, size_t cach
     if (p.splits < 1 || (size_t)p.max_seq_len > (size_t)p.splits * kChunkMax)
         return fail(L0H_ERR_INVALID_ARG, "too few splits for the sequence length");
     if (!p.partials || !p.tickets) return fail(L0H_ERR_INVALID_ARG, "attention workspace missing");
-    return p.head_dim == 64 ? launch_hd<64>(s, p, seq_len_step, cache_batch_stride)
-                            : launch_hd<128>(s, p, seq_len_step, cache_batch_stride);
+    switch (p.head_dim) {
+    case 16: return launch_hd<16>(s, p, seq_len_step, cache_batch_stride);
+    case 32: return launch_hd<32>(s, p, seq_len_step, cache_batch_stride);
+    case 64: return launch_hd<64>(s, p, seq_len_step, cache_batch_stride);
+    default: return launch_hd<128>(s, p, seq_len_step, cache_batch_stride);
+    }
 }
 
 }  // namespace

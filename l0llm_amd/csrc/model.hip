@@ -224,10 +224,61 @@ int place_matrix(l0h_model* m, const Target& t, const void* dev_w, const uint16_
     return st;
 }
 
-int enqueue_step(l0h_model* m, hipStream_t s) {
+// Event pairs around each launch of an eagerly run step (profiling); null when capturing.
+struct StepTimer {
+    hipStream_t s = nullptr;
+    int position = 0;
+    std::vector<l0h_kernel_timing> entries;
+    std::vector<hipEvent_t> events;
+    int begin(int kind, int layer, double bytes) {
+        hipEvent_t a, b;
+        L0H_HIP_TRY(hipEventCreate(&a));
+        L0H_HIP_TRY(hipEventCreate(&b));
+        events.push_back(a);
+        events.push_back(b);
+        entries.push_back(l0h_kernel_timing{kind, layer, 0.f, bytes});
+        L0H_HIP_TRY(hipEventRecord(a, s));
+        return L0H_OK;
+    }
+    int end() {
+        L0H_HIP_TRY(hipEventRecord(events.back(), s));
+        return L0H_OK;
+    }
+    int collect() {
+        L0H_HIP_TRY(hipStreamSynchronize(s));
+        for (size_t i = 0; i < entries.size(); i++) {
+            float ms = 0.f;
+            L0H_HIP_TRY(hipEventElapsedTime(&ms, events[2 * i], events[2 * i + 1]));
+            entries[i].microseconds = ms * 1000.f;
+        }
+        return L0H_OK;
+    }
+    ~StepTimer() {
+        for (auto e : events) (void)hipEventDestroy(e);
+    }
+};
+
+// Algorithmic HBM bytes of a weight-streaming GEMV launch: weights (+ int8 scales) + the
+// activation bytes it reads and writes.
+double gemv_bytes(const l0h_model* m, int n, int k, double act_bytes) {
+    double b = (double)n * k * dtype_size(m->storage);
+    if (m->storage == L0H_I8PC) b += 2.0 * n;
+    return b + act_bytes;
+}
+
+int enqueue_step(l0h_model* m, hipStream_t s, StepTimer* t = nullptr) {
     const auto& c = m->cfg;
-    const int H = c.hidden_size;
-    int st = launch_embedding(s, m->token, m->embedding, m->hidden, H, (size_t)H);  // LlmModel.cs:424
+    const int H = c.hidden_size, I = c.intermediate_size;
+    const double cache_item = dtype_size(m->cache_dtype);
+    auto timed = [&](int kind, int layer, double bytes, auto&& launch) -> int {
+        int r;
+        if (t && (r = t->begin(kind, layer, bytes))) return r;
+        if ((r = launch())) return r;
+        return t ? t->end() : L0H_OK;
+    };
+    int st = timed(L0H_KERNEL_EMBEDDING, -1, 8.0 * H, [&] {
+        return launch_embedding(s, m->token, m->embedding, m->hidden, H, (size_t)H);  // LlmModel.cs:424
+    });
     if (st) return st;
     for (int li = 0; li < c.num_layers; li++) {
         Layer& L = m->layers[li];
@@ -253,7 +304,9 @@ int enqueue_step(l0h_model* m, hipStream_t s) {
         g.kv_dim = m->kvd;
         g.head_dim = c.head_dim;
         g.rotary_dim = m->rot;
-        if ((st = launch_gemv_nk(s, g))) return st;
+        const double qkv_out = 4.0 * m->qd + 2.0 * m->kvd * cache_item;
+        if ((st = timed(L0H_KERNEL_QKV, li, gemv_bytes(m, g.n, H, 8.0 * H + qkv_out), [&] { return launch_gemv_nk(s, g); })))
+            return st;
 
         AttnParams a;  // :325-327
         a.q = m->q;
@@ -273,7 +326,9 @@ int enqueue_step(l0h_model* m, hipStream_t s) {
         a.splits = m->attn_splits;
         a.partials = m->attn_partials;
         a.tickets = m->attn_tickets;
-        if ((st = launch_attention_decode(s, a))) return st;
+        const double attn_bytes = t ? 2.0 * (t->position + 1) * m->kvd * cache_item + 8.0 * m->qd : 0.0;
+        if ((st = timed(L0H_KERNEL_ATTENTION, li, attn_bytes, [&] { return launch_attention_decode(s, a); })))
+            return st;
 
         GemvParams o;  // :333, :183
         o.w_dtype = m->storage;
@@ -284,7 +339,8 @@ int enqueue_step(l0h_model* m, hipStream_t s) {
         o.x = m->attn;
         o.epilogue = EPI_RESIDUAL;
         o.resid = m->hidden;
-        if ((st = launch_gemv_nk(s, o))) return st;
+        if ((st = timed(L0H_KERNEL_O_PROJ, li, gemv_bytes(m, H, m->qd, 4.0 * m->qd + 8.0 * H), [&] { return launch_gemv_nk(s, o); })))
+            return st;
 
         GemvParams gu;  // :183-189
         gu.w_dtype = m->storage;
@@ -298,7 +354,8 @@ int enqueue_step(l0h_model* m, hipStream_t s) {
         gu.epilogue = EPI_SWIGLU;
         gu.y = m->act;
         gu.y_dtype = L0H_F32;
-        if ((st = launch_gemv_nk(s, gu))) return st;
+        if ((st = timed(L0H_KERNEL_GATE_UP, li, gemv_bytes(m, 2 * I, H, 8.0 * H + 4.0 * I), [&] { return launch_gemv_nk(s, gu); })))
+            return st;
 
         GemvParams d;  // :190-194
         d.w_dtype = m->storage;
@@ -309,7 +366,8 @@ int enqueue_step(l0h_model* m, hipStream_t s) {
         d.x = m->act;
         d.epilogue = EPI_RESIDUAL;
         d.resid = m->hidden;
-        if ((st = launch_gemv_nk(s, d))) return st;
+        if ((st = timed(L0H_KERNEL_DOWN, li, gemv_bytes(m, H, I, 4.0 * I + 8.0 * H), [&] { return launch_gemv_nk(s, d); })))
+            return st;
     }
     GemvParams h;  // AppendHead: LlmModel.cs:394-395
     h.w_dtype = m->storage;
@@ -323,14 +381,18 @@ int enqueue_step(l0h_model* m, hipStream_t s) {
     h.epilogue = EPI_STORE;
     h.y = m->logits;
     h.y_dtype = L0H_F32;
-    if ((st = launch_gemv_nk(s, h))) return st;
+    if ((st = timed(L0H_KERNEL_LM_HEAD, -1, gemv_bytes(m, c.vocab_size, H, 8.0 * H + 4.0 * c.vocab_size),
+                    [&] { return launch_gemv_nk(s, h); })))
+        return st;
     ArgmaxFeed feed;  // :398, plus device-side feedback for back-to-back decode
     feed.token = m->token;
     feed.position = m->position;
     feed.step = m->step;
     feed.out_list = m->out_list;
     feed.capacity = m->out_capacity;
-    return launch_argmax(s, m->logits, c.vocab_size, m->sampled, m->argmax_partials, m->argmax_ticket, feed);
+    return timed(L0H_KERNEL_ARGMAX, -1, 4.0 * c.vocab_size, [&] {
+        return launch_argmax(s, m->logits, c.vocab_size, m->sampled, m->argmax_partials, m->argmax_ticket, feed);
+    });
 }
 
 int ensure_graph(l0h_model* m) {
@@ -747,6 +809,24 @@ int l0h_model_generate_greedy(l0h_model* m, const int* prompt, int prompt_len, i
     }
     *n_out = n;
     m->pos = saved;  // GenerateGreedy leaves Position alone (LlmModel.cs:156-193)
+    return L0H_OK;
+}
+
+int l0h_model_profile_step(l0h_model* m, int token, int position, l0h_kernel_timing* out, int capacity, int* count) {
+    int st = check_ready(m);
+    if (st) return st;
+    L0H_CHECK_ARG(count && (out || capacity == 0), "null argument");
+    if ((unsigned)token >= (unsigned)m->cfg.vocab_size) return fail(L0H_ERR_INVALID_ARG, "token id outside the vocabulary");
+    if (position < 0 || position >= m->max_seq) return fail(L0H_ERR_INVALID_ARG, "position outside the cache");
+    const int vals[4] = {token, position, 0, 0};
+    if ((st = l0h_write(m->dev, m->token, 0, vals, sizeof(vals)))) return st;
+    StepTimer t;
+    t.s = m->dev->stream;
+    t.position = position;
+    if ((st = enqueue_step(m, t.s, &t))) return st;
+    if ((st = t.collect())) return st;
+    *count = (int)t.entries.size();
+    for (int i = 0; i < std::min(capacity, *count); i++) out[i] = t.entries[i];
     return L0H_OK;
 }
 

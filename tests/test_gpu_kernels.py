@@ -270,7 +270,8 @@ def test_kv_store_bit_exact(device, suite, cache):
 # ---- attention ---------------------------------------------------------------------------------
 
 ATTN = [(64, 14, 2, 37, l0.F32), (64, 14, 2, 1, l0.F16), (128, 32, 8, 512, l0.F16), (128, 32, 8, 4096, l0.F16),
-        (128, 32, 8, 2049, l0.F32), (128, 8, 8, 300, l0.F16)]
+        (128, 32, 8, 2049, l0.F32), (128, 8, 8, 300, l0.F16), (16, 4, 2, 50, l0.F16), (32, 8, 2, 100, l0.F32),
+        (64, 16, 2, 700, l0.F16)]
 
 
 @pytest.mark.parametrize("hd,nh,nkv,seq,cache", ATTN)
