@@ -11,7 +11,7 @@ in HBM, bracketed by device synchronisation.
 The JSON line also carries:
   roofline      the int8 weight-streaming GEMV (the dominant kernel: q|k|v, O, gate|up, down and
                 lm_head launches): algorithmic bytes / HIP-event duration per launch, measured
-                live on the model's stream over `--profile-steps` eager steps, against 8 TB/s
+                live on the model's stream (back-to-back launches over all layers), against 8 TB/s
   kernels       the same per kernel kind
   cpu_baseline  the CPU oracle (fp64-accumulating C) running the same model's decode steps on the
                 host cores, for a bounded sample of `--cpu-tokens` tokens
@@ -48,20 +48,18 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def kernel_table(samples: list[list[dict]]) -> dict:
-    agg: dict[str, dict] = {}
-    for step in samples:
-        for e in step:
-            a = agg.setdefault(e["kind"], dict(launches=0, us=0.0, bytes=0.0))
-            a["launches"] += 1
-            a["us"] += e["us"]
-            a["bytes"] += e["bytes"]
+KINDS = ("embedding", "qkv", "attention", "o_proj", "gate_up", "down", "lm_head", "argmax")
+
+
+def kernel_table(model, position: int, rounds: int) -> dict:
+    """Per kernel kind: HIP-event time of back-to-back launches on the model's stream (every
+    layer once per round, so weights stream from HBM), divided per launch."""
     out = {}
-    for k, a in agg.items():
-        gbs = a["bytes"] / (a["us"] * 1e-6) / 1e9 if a["us"] > 0 else 0.0
-        out[k] = dict(launches_per_step=a["launches"] // len(samples), avg_us=round(a["us"] / a["launches"], 3),
-                      bytes_per_launch=round(a["bytes"] / a["launches"]), gbs=round(gbs, 1),
-                      frac=round(gbs / HBM_PEAK_GBS, 4))
+    for kind in KINDS:
+        r = model.profile_kernel(kind, position, rounds if kind in GEMV_KINDS + ("attention",) else 4 * rounds)
+        gbs = r["bytes"] / (r["us"] * 1e-6) / 1e9 if r["us"] > 0 else 0.0
+        out[kind] = dict(launches_per_step=r["launches"], avg_us=round(r["us"], 3), bytes_per_launch=round(r["bytes"]),
+                         gbs=round(gbs, 1), frac=round(gbs / HBM_PEAK_GBS, 4))
     return out
 
 
@@ -101,7 +99,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=128, help="timed decode steps (generated tokens)")
     ap.add_argument("--warmup", type=int, default=8, help="untimed decode steps before the timed region")
     ap.add_argument("--ctx", type=int, default=2048, help="prefilled KV-cache length")
-    ap.add_argument("--profile-steps", type=int, default=3)
+    ap.add_argument("--profile-rounds", type=int, default=4,
+                    help="passes over all layers when timing each kernel kind for the roofline")
     ap.add_argument("--cpu-tokens", type=int, default=2, help="tokens in the CPU baseline sample (0: skip)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -113,7 +112,7 @@ def main() -> int:
 
     cfg = llama8b()
     dev = l0.Device(0)
-    max_seq = args.ctx + args.steps + args.profile_steps + 8
+    max_seq = args.ctx + args.steps + args.cpu_tokens + 8
     log(f"device {dev.name}; building the model (max_seq {max_seq})")
     model = l0.LlmModel(dev, cfg, precision=l0.PRECISION_INT8, cache_dtype=l0.F16, max_seq_len=max_seq)
     model.init_random(500, 0.02)
@@ -137,8 +136,7 @@ def main() -> int:
     log(f"decoded {args.steps} tokens in {dt * 1e3:.2f} ms: {tps:.1f} tokens/s; first ids {toks[:8].tolist()}")
 
     pos = model.position
-    samples = [model.profile_step(int(toks[-1]), pos + i) for i in range(args.profile_steps)]
-    table = kernel_table(samples)
+    table = kernel_table(model, pos, args.profile_rounds)
     gemv_us = sum(table[k]["avg_us"] * table[k]["launches_per_step"] for k in GEMV_KINDS)
     gemv_bytes = sum(table[k]["bytes_per_launch"] * table[k]["launches_per_step"] for k in GEMV_KINDS)
     launches = sum(table[k]["launches_per_step"] for k in GEMV_KINDS)
@@ -153,7 +151,7 @@ def main() -> int:
     cpu = None
     if args.cpu_tokens > 0:
         log("CPU baseline: exporting the model and running the oracle")
-        cpu = cpu_baseline(model, cfg, args.cpu_tokens, pos + args.profile_steps)
+        cpu = cpu_baseline(model, cfg, args.cpu_tokens, pos)
         log(f"CPU baseline {cpu['value']} tokens/s on {cpu['cores']} threads")
 
     line = {

@@ -351,6 +351,12 @@ typedef struct {
  * entries to host_out and the number of launches to count. */
 int l0h_model_profile_step(l0h_model* model, int token, int position, l0h_kernel_timing* host_out,
                            int capacity, int* count);
+/* Average duration of one kernel kind of the decode step at `position`: `rounds` passes, each
+ * launching the kind for every layer (per-layer kinds) or once, back to back between one HIP
+ * event pair, so the event cost is amortised and every layer's weights come from HBM. Reports the
+ * microseconds and algorithmic bytes per launch and the launches per step. */
+int l0h_model_profile_kernel(l0h_model* model, int kind, int position, int rounds, float* avg_us,
+                             double* bytes, int* launches);
 /* LlmModel.Dispose (LlmModel.cs:308). */
 int l0h_model_destroy(l0h_model* model);
 

@@ -512,6 +512,13 @@ class LlmModel:
         return [dict(kind=KERNEL_KINDS[e.kind], layer=e.layer, us=e.microseconds, bytes=e.bytes)
                 for e in buf[: n.value]]
 
+    def profile_kernel(self, kind: str, position: int, rounds: int = 4) -> dict:
+        """Back-to-back launches of one kernel kind (every layer per round): avg us, bytes, launches/step."""
+        us, b, n = ctypes.c_float(), ctypes.c_double(), ctypes.c_int()
+        check(lib.l0h_model_profile_kernel(self.handle, KERNEL_KINDS.index(kind), position, rounds, ctypes.byref(us),
+                                           ctypes.byref(b), ctypes.byref(n)))
+        return dict(kind=kind, us=us.value, bytes=b.value, launches=n.value)
+
     def decode_greedy_device(self, token: int, steps: int) -> np.ndarray:
         out = np.empty(max(steps, 1), dtype=np.int32)
         check(lib.l0h_model_decode_greedy_device(self.handle, token, steps, out.ctypes.data_as(ctypes.c_void_p)))

@@ -21,6 +21,7 @@ constexpr int kBlock = 256;
 constexpr int kGroupMax = 8;   // q heads per kv head
 constexpr int kChunkMax = 1024;  // positions per block (scores staged in LDS)
 constexpr int kUnroll = 4;
+constexpr int kMaxSplitsMerge = 256;  // splits whose merge weights are staged in LDS
 
 template <int CTRL, int ROW_MASK>
 __device__ __forceinline__ float dpp_src(float v) {
@@ -245,23 +246,50 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(const AttnParams p,
     if (!s_last) return;
     __threadfence();
 
-    // Last block of this (batch, kv head): log-sum-exp merge of the splits.
+    // Last block of this (batch, kv head): log-sum-exp merge of the splits. The other blocks
+    // published their partials with a release fence before taking a ticket; the acquire fence
+    // above makes them visible to plain loads, which can all be in flight at once.
     const float* all = p.partials + ((size_t)b * p.nkv + g) * p.splits * (size_t)G * (HD + 2);
     const size_t stride = (size_t)G * (HD + 2);
+    __shared__ float s_scale[kGroupMax][kMaxSplitsMerge];
+    __shared__ float s_den[kGroupMax];
+    const bool staged = p.splits <= kMaxSplitsMerge;
+    if (staged) {
+        // Per head: M = max m_s, scale_s = exp2(m_s - M), den = sum scale_s * l_s (wave h).
+        for (int h = wave; h < G; h += 4) {
+            float M = -INFINITY;
+            for (int s = lane; s < p.splits; s += 64) M = fmaxf(M, all[s * stride + G * HD + h]);
+            M = wave_max(M);
+            float den = 0.f;
+            for (int s = lane; s < p.splits; s += 64) {
+                const float ms = all[s * stride + G * HD + h];
+                const float w = ms == -INFINITY ? 0.f : exp2f(ms - M);
+                s_scale[h][s] = w;
+                den = fmaf(w, all[s * stride + G * HD + G + h], den);
+            }
+            den = wave_sum(den);
+            if (lane == 0) s_den[h] = den;
+        }
+        __syncthreads();
+    }
     for (int idx = threadIdx.x; idx < G * HD; idx += kBlock) {
         const int h = idx / HD, d = idx - h * HD;
-        float M = -INFINITY;
-        for (int s = 0; s < p.splits; s++)
-            M = fmaxf(M, __hip_atomic_load(all + s * stride + G * HD + h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
         float num = 0.f, den = 0.f;
-        if (M != -INFINITY) {
-            for (int s = 0; s < p.splits; s++) {
-                const float* ps = all + s * stride;
-                const float ms = __hip_atomic_load(ps + G * HD + h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                if (ms == -INFINITY) continue;
-                const float w = exp2f(ms - M);
-                num = fmaf(w, __hip_atomic_load(ps + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), num);
-                den = fmaf(w, __hip_atomic_load(ps + G * HD + G + h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), den);
+        if (staged) {
+            for (int s = 0; s < p.splits; s++) num = fmaf(s_scale[h][s], all[s * stride + idx], num);
+            den = s_den[h];
+        } else {
+            float M = -INFINITY;
+            for (int s = 0; s < p.splits; s++) M = fmaxf(M, all[s * stride + G * HD + h]);
+            if (M != -INFINITY) {
+                for (int s = 0; s < p.splits; s++) {
+                    const float* ps = all + s * stride;
+                    const float ms = ps[G * HD + h];
+                    if (ms == -INFINITY) continue;
+                    const float w = exp2f(ms - M);
+                    num = fmaf(w, ps[idx], num);
+                    den = fmaf(w, ps[G * HD + G + h], den);
+                }
             }
         }
         const float o = den > 0.f ? num / den : 0.f;

@@ -7,6 +7,8 @@
 // in LDS as fp32 (with the RMSNorm prologue applied there when fused), dequantisation happens in
 // registers (int8 per-row scale folded in after the reduction), accumulation is fp32, and the
 // cross-lane sum uses DPP (quad_perm, row mirrors, row_bcast15/31).
+#include <cstdlib>
+
 #include "kernels.h"
 
 namespace l0h {
@@ -163,7 +165,27 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p) {
     const int K = p.k, N = p.n;
     const int C = K / EPC;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int row0 = (blockIdx.x * kWaves + wave) * R;
+    // Persistent waves: wave w of block b owns row groups (b * kWaves + w) + i * (all waves).
+    const int wave_stride = gridDim.x * kWaves * R;
+    int row0 = (blockIdx.x * kWaves + wave) * R;
+
+    auto row_ptr = [&](int row) {
+        return reinterpret_cast<const uint4*>(static_cast<const char*>(p.w) +
+                                              (size_t)min(row, N - 1) * K * WTraits<WT>::kBytes);
+    };
+    uint4 wv[U][R];
+    auto load_batch = [&](int r0, int c0) {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int c = c0 + 64 * u;
+#pragma unroll
+            for (int r = 0; r < R; r++) wv[u][r] = c < C ? ld_nt16(row_ptr(r0 + r) + c) : make_uint4(0u, 0u, 0u, 0u);
+        }
+    };
+    // The first batch of weight loads goes out before the activations are staged, so the
+    // prologue overlaps their HBM latency.
+    bool prefetched = row0 < N && lane < C;
+    if (prefetched) load_batch(row0, lane);
 
     // Stage activations (and RMSNorm) in LDS.
     if constexpr (XLDS) {
@@ -221,7 +243,9 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p) {
             __syncthreads();
         }
     }
-    if (row0 >= N) return;  // whole wave out of range; no barrier follows
+    const float* xg = static_cast<const float*>(p.x);
+    // No barrier below this point: waves run their row groups independently.
+    for (; row0 < N; row0 += wave_stride) {
 
     float acc[MR][R];
 #pragma unroll
@@ -229,28 +253,9 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p) {
 #pragma unroll
         for (int r = 0; r < R; r++) acc[mr][r] = 0.f;
 
-    const uint4* wp[R];
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-        const int row = min(row0 + r, N - 1);
-        wp[r] = reinterpret_cast<const uint4*>(static_cast<const char*>(p.w) +
-                                               (size_t)row * K * WTraits<WT>::kBytes);
-    }
-    const float* xg = static_cast<const float*>(p.x);
-
     for (int c0 = lane; c0 < C; c0 += 64 * U) {
-        uint4 wv[U][R];
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-            const int c = c0 + 64 * u;
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                if (c < C)
-                    wv[u][r] = ld_nt16(wp[r] + c);
-                else
-                    wv[u][r] = make_uint4(0u, 0u, 0u, 0u);
-            }
-        }
+        if (!prefetched) load_batch(row0, c0);
+        prefetched = false;
 #pragma unroll
         for (int u = 0; u < U; u++) {
             const int c = c0 + 64 * u;
@@ -336,6 +341,8 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p) {
             }
         }
     }
+    prefetched = false;
+    }  // row groups
 }
 
 // Any shape: one wave per (activation row, output row), scalar loads. STORE / RESIDUAL only.
@@ -371,7 +378,8 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_generic_kernel(const GemvParam
 template <int WT, int R, int U, int MR, bool XLDS>
 int launch_fast(hipStream_t s, const GemvParams& p) {
     const unsigned rows_per_block = kWaves * R;
-    const unsigned grid = ceil_div(p.n, rows_per_block);
+    unsigned grid = ceil_div(p.n, rows_per_block);
+    if (p.max_blocks > 0) grid = std::min<unsigned>(grid, (unsigned)p.max_blocks);
     const size_t shmem = XLDS ? (size_t)MR * p.k * sizeof(float) : 0;
     auto kern = gemv_nk_kernel<WT, R, U, MR, XLDS>;
     if (shmem > 64 * 1024) {
@@ -394,15 +402,48 @@ int dispatch_mr(hipStream_t s, const GemvParams& p, int mr) {
     return fits ? launch_fast<WT, R, U, 8, true>(s, p) : launch_fast<WT, R, U, 8, false>(s, p);
 }
 
+// Rows per wave (R) and 16-byte chunks in flight per row per lane (U) for the one-row int8
+// kernel: R * U loads of 1 KiB per wave are outstanding. L0H_GEMV_RU="RU" selects another
+// instantiation (for tuning sweeps); the default is the measured best.
+int int8_ru_choice() {
+    static const int v = [] {
+        const char* e = std::getenv("L0H_GEMV_RU");
+        return e ? std::atoi(e) : 0;
+    }();
+    return v;
+}
+
 template <int WT>
 int dispatch_wt(hipStream_t s, const GemvParams& p, int mr) {
+    if constexpr (WT == L0H_I8PC) {
+        if (mr == 1 && (size_t)p.k * sizeof(float) <= kLdsBudget) {
+            switch (int8_ru_choice()) {
+            case 24: return launch_fast<WT, 2, 4, 1, true>(s, p);
+            case 28: return launch_fast<WT, 2, 8, 1, true>(s, p);
+            case 42: return launch_fast<WT, 4, 2, 1, true>(s, p);
+            case 48: return launch_fast<WT, 4, 8, 1, true>(s, p);
+            case 82: return launch_fast<WT, 8, 2, 1, true>(s, p);
+            case 84: return launch_fast<WT, 8, 4, 1, true>(s, p);
+            default: break;
+            }
+        }
+    }
     // Rows per wave and chunks in flight, chosen per weight width.
-    if constexpr (WT == L0H_I8PC) return dispatch_mr<WT, 4, 2>(s, p, mr);
-    else if constexpr (WT == L0H_F32) return dispatch_mr<WT, 4, 4>(s, p, mr);
-    else return dispatch_mr<WT, 4, 2>(s, p, mr);
+    if constexpr (WT == L0H_F32) return dispatch_mr<WT, 4, 4>(s, p, mr);
+    else return dispatch_mr<WT, 4, 4>(s, p, mr);
 }
 
 }  // namespace
+
+int gemv_max_blocks(int compute_units) {
+    // L0H_GEMV_BLOCKS_PER_CU overrides the default (0: one block per row group, no cap).
+    static const int per_cu = [] {
+        const char* e = std::getenv("L0H_GEMV_BLOCKS_PER_CU");
+        const int v = e ? std::atoi(e) : 2;
+        return v >= 0 ? v : 2;
+    }();
+    return per_cu == 0 ? 0 : std::max(1, compute_units) * per_cu;
+}
 
 int launch_gemv_nk(hipStream_t s, const GemvParams& p0) {
     const int epc = p0.w_dtype == L0H_I8PC ? 16 : (p0.w_dtype == L0H_F32 ? 4 : 8);

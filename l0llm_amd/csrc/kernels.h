@@ -43,7 +43,13 @@ struct GemvParams {
     const float* inv_freq = nullptr;
     float rope_scale = 1.f;
     int q_dim = 0, kv_dim = 0, head_dim = 0, rotary_dim = 0;
+    // Grid cap: 0 launches one block per group of rows; otherwise at most this many blocks
+    // loop over the row groups (activations staged once per block).
+    int max_blocks = 0;
 };
+
+// Persistent-grid size for weight-streaming kernels on a device with `compute_units` CUs.
+int gemv_max_blocks(int compute_units);
 
 int launch_gemv_nk(hipStream_t s, const GemvParams& p);
 

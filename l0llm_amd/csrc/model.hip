@@ -80,6 +80,7 @@ struct l0h_model {
     unsigned* argmax_ticket = nullptr;
     int attn_splits = 1;
     hipGraphExec_t step_exec = nullptr;
+    bool eager = false;  // L0H_EAGER_STEP=1: enqueue the step's kernels instead of replaying the graph
     int pos = 0;  // LlmModel.Position
     std::vector<void*> owned;
 };
@@ -266,24 +267,38 @@ double gemv_bytes(const l0h_model* m, int n, int k, double act_bytes) {
     return b + act_bytes;
 }
 
-int enqueue_step(l0h_model* m, hipStream_t s, StepTimer* t = nullptr) {
+// Algorithmic HBM bytes of one launch of `kind` at `position`: weights (+ int8 scales), the
+// activations it reads and writes, and for attention the K and V rows of slots 0..position.
+double op_bytes(const l0h_model* m, int kind, int position) {
     const auto& c = m->cfg;
-    const int H = c.hidden_size, I = c.intermediate_size;
-    const double cache_item = dtype_size(m->cache_dtype);
-    auto timed = [&](int kind, int layer, double bytes, auto&& launch) -> int {
-        int r;
-        if (t && (r = t->begin(kind, layer, bytes))) return r;
-        if ((r = launch())) return r;
-        return t ? t->end() : L0H_OK;
-    };
-    int st = timed(L0H_KERNEL_EMBEDDING, -1, 8.0 * H, [&] {
-        return launch_embedding(s, m->token, m->embedding, m->hidden, H, (size_t)H);  // LlmModel.cs:424
-    });
-    if (st) return st;
-    for (int li = 0; li < c.num_layers; li++) {
+    const double H = c.hidden_size, I = c.intermediate_size, qd = m->qd, kvd = m->kvd;
+    const double ci = dtype_size(m->cache_dtype);
+    switch (kind) {
+    case L0H_KERNEL_EMBEDDING: return 8.0 * H;
+    case L0H_KERNEL_QKV: return gemv_bytes(m, m->qd + 2 * m->kvd, c.hidden_size, 8.0 * H + 4.0 * qd + 2.0 * kvd * ci);
+    case L0H_KERNEL_ATTENTION: return 2.0 * (position + 1) * kvd * ci + 8.0 * qd;
+    case L0H_KERNEL_O_PROJ: return gemv_bytes(m, c.hidden_size, m->qd, 4.0 * qd + 8.0 * H);
+    case L0H_KERNEL_GATE_UP: return gemv_bytes(m, 2 * c.intermediate_size, c.hidden_size, 8.0 * H + 4.0 * I);
+    case L0H_KERNEL_DOWN: return gemv_bytes(m, c.hidden_size, c.intermediate_size, 4.0 * I + 8.0 * H);
+    case L0H_KERNEL_LM_HEAD: return gemv_bytes(m, c.vocab_size, c.hidden_size, 8.0 * H + 4.0 * c.vocab_size);
+    default: return 4.0 * c.vocab_size;  // argmax reads the logits
+    }
+}
+
+bool per_layer_kind(int kind) { return kind >= L0H_KERNEL_QKV && kind <= L0H_KERNEL_DOWN; }
+
+// Enqueues one kernel of the decode step (layer li for the per-layer kinds).
+int launch_op(l0h_model* m, hipStream_t s, int kind, int li) {
+    const auto& c = m->cfg;
+    const int H = c.hidden_size;
+    GemvParams g;
+    g.w_dtype = m->storage;
+    g.max_blocks = gemv_max_blocks(m->dev->compute_units);
+    switch (kind) {
+    case L0H_KERNEL_EMBEDDING:  // LlmModel.cs:424
+        return launch_embedding(s, m->token, m->embedding, m->hidden, H, (size_t)H);
+    case L0H_KERNEL_QKV: {  // LlmDecoderLayer.cs:167, :296-322
         Layer& L = m->layers[li];
-        GemvParams g;  // q|k|v: LlmDecoderLayer.cs:167, :296-322
-        g.w_dtype = m->storage;
         g.w = L.qkv.w;
         g.scales = L.qkv.s;
         g.n = L.qkv.n;
@@ -304,11 +319,11 @@ int enqueue_step(l0h_model* m, hipStream_t s, StepTimer* t = nullptr) {
         g.kv_dim = m->kvd;
         g.head_dim = c.head_dim;
         g.rotary_dim = m->rot;
-        const double qkv_out = 4.0 * m->qd + 2.0 * m->kvd * cache_item;
-        if ((st = timed(L0H_KERNEL_QKV, li, gemv_bytes(m, g.n, H, 8.0 * H + qkv_out), [&] { return launch_gemv_nk(s, g); })))
-            return st;
-
-        AttnParams a;  // :325-327
+        return launch_gemv_nk(s, g);
+    }
+    case L0H_KERNEL_ATTENTION: {  // LlmDecoderLayer.cs:325-327
+        Layer& L = m->layers[li];
+        AttnParams a;
         a.q = m->q;
         a.q_dtype = L0H_F32;
         a.kc = L.k_cache;
@@ -326,73 +341,81 @@ int enqueue_step(l0h_model* m, hipStream_t s, StepTimer* t = nullptr) {
         a.splits = m->attn_splits;
         a.partials = m->attn_partials;
         a.tickets = m->attn_tickets;
-        const double attn_bytes = t ? 2.0 * (t->position + 1) * m->kvd * cache_item + 8.0 * m->qd : 0.0;
-        if ((st = timed(L0H_KERNEL_ATTENTION, li, attn_bytes, [&] { return launch_attention_decode(s, a); })))
-            return st;
-
-        GemvParams o;  // :333, :183
-        o.w_dtype = m->storage;
-        o.w = L.o.w;
-        o.scales = L.o.s;
-        o.n = H;
-        o.k = m->qd;
-        o.x = m->attn;
-        o.epilogue = EPI_RESIDUAL;
-        o.resid = m->hidden;
-        if ((st = timed(L0H_KERNEL_O_PROJ, li, gemv_bytes(m, H, m->qd, 4.0 * m->qd + 8.0 * H), [&] { return launch_gemv_nk(s, o); })))
-            return st;
-
-        GemvParams gu;  // :183-189
-        gu.w_dtype = m->storage;
-        gu.w = L.gu.w;
-        gu.scales = L.gu.s;
-        gu.n = 2 * c.intermediate_size;
-        gu.k = H;
-        gu.x = m->hidden;
-        gu.norm_w = L.post_norm;
-        gu.eps = c.rms_norm_eps;
-        gu.epilogue = EPI_SWIGLU;
-        gu.y = m->act;
-        gu.y_dtype = L0H_F32;
-        if ((st = timed(L0H_KERNEL_GATE_UP, li, gemv_bytes(m, 2 * I, H, 8.0 * H + 4.0 * I), [&] { return launch_gemv_nk(s, gu); })))
-            return st;
-
-        GemvParams d;  // :190-194
-        d.w_dtype = m->storage;
-        d.w = L.down.w;
-        d.scales = L.down.s;
-        d.n = H;
-        d.k = c.intermediate_size;
-        d.x = m->act;
-        d.epilogue = EPI_RESIDUAL;
-        d.resid = m->hidden;
-        if ((st = timed(L0H_KERNEL_DOWN, li, gemv_bytes(m, H, I, 4.0 * I + 8.0 * H), [&] { return launch_gemv_nk(s, d); })))
-            return st;
+        return launch_attention_decode(s, a);
     }
-    GemvParams h;  // AppendHead: LlmModel.cs:394-395
-    h.w_dtype = m->storage;
-    h.w = m->lm.w;
-    h.scales = m->lm.s;
-    h.n = c.vocab_size;
-    h.k = H;
-    h.x = m->hidden;
-    h.norm_w = m->final_norm;
-    h.eps = c.rms_norm_eps;
-    h.epilogue = EPI_STORE;
-    h.y = m->logits;
-    h.y_dtype = L0H_F32;
-    if ((st = timed(L0H_KERNEL_LM_HEAD, -1, gemv_bytes(m, c.vocab_size, H, 8.0 * H + 4.0 * c.vocab_size),
-                    [&] { return launch_gemv_nk(s, h); })))
-        return st;
-    ArgmaxFeed feed;  // :398, plus device-side feedback for back-to-back decode
-    feed.token = m->token;
-    feed.position = m->position;
-    feed.step = m->step;
-    feed.out_list = m->out_list;
-    feed.capacity = m->out_capacity;
-    return timed(L0H_KERNEL_ARGMAX, -1, 4.0 * c.vocab_size, [&] {
+    case L0H_KERNEL_O_PROJ: {  // LlmDecoderLayer.cs:333, residual half of :183
+        Layer& L = m->layers[li];
+        g.w = L.o.w;
+        g.scales = L.o.s;
+        g.n = H;
+        g.k = m->qd;
+        g.x = m->attn;
+        g.epilogue = EPI_RESIDUAL;
+        g.resid = m->hidden;
+        return launch_gemv_nk(s, g);
+    }
+    case L0H_KERNEL_GATE_UP: {  // LlmDecoderLayer.cs:183-189
+        Layer& L = m->layers[li];
+        g.w = L.gu.w;
+        g.scales = L.gu.s;
+        g.n = 2 * c.intermediate_size;
+        g.k = H;
+        g.x = m->hidden;
+        g.norm_w = L.post_norm;
+        g.eps = c.rms_norm_eps;
+        g.epilogue = EPI_SWIGLU;
+        g.y = m->act;
+        g.y_dtype = L0H_F32;
+        return launch_gemv_nk(s, g);
+    }
+    case L0H_KERNEL_DOWN: {  // LlmDecoderLayer.cs:190-194
+        Layer& L = m->layers[li];
+        g.w = L.down.w;
+        g.scales = L.down.s;
+        g.n = H;
+        g.k = c.intermediate_size;
+        g.x = m->act;
+        g.epilogue = EPI_RESIDUAL;
+        g.resid = m->hidden;
+        return launch_gemv_nk(s, g);
+    }
+    case L0H_KERNEL_LM_HEAD:  // AppendHead: LlmModel.cs:394-395
+        g.w = m->lm.w;
+        g.scales = m->lm.s;
+        g.n = c.vocab_size;
+        g.k = H;
+        g.x = m->hidden;
+        g.norm_w = m->final_norm;
+        g.eps = c.rms_norm_eps;
+        g.epilogue = EPI_STORE;
+        g.y = m->logits;
+        g.y_dtype = L0H_F32;
+        return launch_gemv_nk(s, g);
+    default: {  // LlmModel.cs:398, plus device-side feedback for back-to-back decode
+        ArgmaxFeed feed;
+        feed.token = m->token;
+        feed.position = m->position;
+        feed.step = m->step;
+        feed.out_list = m->out_list;
+        feed.capacity = m->out_capacity;
         return launch_argmax(s, m->logits, c.vocab_size, m->sampled, m->argmax_partials, m->argmax_ticket, feed);
-    });
+    }
+    }
+}
+
+int enqueue_step(l0h_model* m, hipStream_t s, StepTimer* t = nullptr) {
+    auto run = [&](int kind, int li) -> int {
+        int r;
+        if (t && (r = t->begin(kind, li, op_bytes(m, kind, t->position)))) return r;
+        if ((r = launch_op(m, s, kind, li))) return r;
+        return t ? t->end() : L0H_OK;
+    };
+    int st = run(L0H_KERNEL_EMBEDDING, -1);
+    for (int li = 0; li < m->cfg.num_layers && !st; li++)
+        for (int kind = L0H_KERNEL_QKV; kind <= L0H_KERNEL_DOWN && !st; kind++) st = run(kind, li);
+    if (!st) st = run(L0H_KERNEL_LM_HEAD, -1);
+    if (!st) st = run(L0H_KERNEL_ARGMAX, -1);
+    return st;
 }
 
 int ensure_graph(l0h_model* m) {
@@ -417,6 +440,14 @@ int ensure_graph(l0h_model* m) {
     return L0H_OK;
 }
 
+// One step with whatever token/position the device holds: the captured graph, or the same
+// kernels enqueued one by one in eager mode.
+int launch_step(l0h_model* m) {
+    if (m->eager) return enqueue_step(m, m->dev->stream);
+    L0H_HIP_TRY(hipGraphLaunch(m->step_exec, m->dev->stream));
+    return L0H_OK;
+}
+
 int check_ready(l0h_model* m) {
     if (!m) return fail(L0H_ERR_INVALID_ARG, "model is null");
     if (m->dev->recording) return fail(L0H_ERR_INVALID_OP, "the device is recording");
@@ -429,12 +460,11 @@ int run_step(l0h_model* m, int token, int position) {
         return fail(L0H_ERR_INVALID_ARG, "token id " + std::to_string(token) + " outside the vocabulary");
     if (position < 0 || position >= m->max_seq)
         return fail(L0H_ERR_INVALID_ARG, "position " + std::to_string(position) + " outside the cache");
-    int st = ensure_graph(m);
+    int st = m->eager ? L0H_OK : ensure_graph(m);
     if (st) return st;
     const int vals[4] = {token, position, 0, 0};  // token, position, sampled, step
     if ((st = l0h_write(m->dev, m->token, 0, vals, sizeof(vals)))) return st;
-    L0H_HIP_TRY(hipGraphLaunch(m->step_exec, m->dev->stream));
-    return L0H_OK;
+    return launch_step(m);
 }
 
 }  // namespace
@@ -479,6 +509,8 @@ int l0h_model_create(l0h_device* dev, const l0h_model_config* cfg, int precision
     m->storage = storage;
     m->cache_dtype = cache_dtype;
     m->max_seq = max_seq_len;
+    const char* eager_env = std::getenv("L0H_EAGER_STEP");
+    m->eager = eager_env && std::atoi(eager_env) != 0;
     m->qd = c.num_attention_heads * c.head_dim;
     m->kvd = c.num_key_value_heads * c.head_dim;
     m->rot = c.head_dim;
@@ -775,7 +807,8 @@ int l0h_model_decode_greedy_device(l0h_model* m, int token, int steps, int* host
     if (m->pos + steps > m->max_seq) return fail(L0H_ERR_INVALID_ARG, "decode would run past the cache");
     if (steps == 0) return L0H_OK;
     if ((st = run_step(m, token, m->pos))) return st;  // writes token, position, step = 0
-    for (int i = 1; i < steps; i++) L0H_HIP_TRY(hipGraphLaunch(m->step_exec, m->dev->stream));
+    for (int i = 1; i < steps; i++)
+        if ((st = launch_step(m))) return st;
     m->pos += steps;
     if (host_out) return l0h_read(m->dev, m->out_list, 0, host_out, (size_t)steps * 4);
     return l0h_synchronize(m->dev);
@@ -797,7 +830,8 @@ int l0h_model_generate_greedy(l0h_model* m, const int* prompt, int prompt_len, i
         if ((st = run_step(m, prompt[i], i))) return st;
     // The last prompt step chose token 0 of the output (out_list[0]) and advanced the device
     // position; the remaining steps replay the graph with the token fed back on the device.
-    for (int i = 1; i < max_new; i++) L0H_HIP_TRY(hipGraphLaunch(m->step_exec, m->dev->stream));
+    for (int i = 1; i < max_new; i++)
+        if ((st = launch_step(m))) return st;
     std::vector<int> toks(max_new);
     if ((st = l0h_read(m->dev, m->out_list, 0, toks.data(), (size_t)max_new * 4))) return st;
     int n = 0;
@@ -828,6 +862,38 @@ int l0h_model_profile_step(l0h_model* m, int token, int position, l0h_kernel_tim
     *count = (int)t.entries.size();
     for (int i = 0; i < std::min(capacity, *count); i++) out[i] = t.entries[i];
     return L0H_OK;
+}
+
+int l0h_model_profile_kernel(l0h_model* m, int kind, int position, int rounds, float* avg_us, double* bytes,
+                             int* launches) {
+    int st = check_ready(m);
+    if (st) return st;
+    L0H_CHECK_ARG(avg_us && bytes && launches, "null argument");
+    L0H_CHECK_ARG(kind >= L0H_KERNEL_EMBEDDING && kind <= L0H_KERNEL_ARGMAX, "unknown kernel kind");
+    L0H_CHECK_ARG(rounds > 0, "rounds must be positive");
+    if (position < 0 || position >= m->max_seq) return fail(L0H_ERR_INVALID_ARG, "position outside the cache");
+    const int vals[4] = {0, position, 0, 0};
+    if ((st = l0h_write(m->dev, m->token, 0, vals, sizeof(vals)))) return st;
+    const int n = per_layer_kind(kind) ? m->cfg.num_layers : 1;
+    hipStream_t s = m->dev->stream;
+    hipEvent_t a, b;
+    L0H_HIP_TRY(hipEventCreate(&a));
+    L0H_HIP_TRY(hipEventCreate(&b));
+    L0H_HIP_TRY(hipEventRecord(a, s));
+    for (int r = 0; r < rounds && !st; r++)
+        for (int li = 0; li < n && !st; li++) st = launch_op(m, s, kind, per_layer_kind(kind) ? li : -1);
+    if (!st) {
+        L0H_HIP_TRY(hipEventRecord(b, s));
+        L0H_HIP_TRY(hipEventSynchronize(b));
+        float ms = 0.f;
+        L0H_HIP_TRY(hipEventElapsedTime(&ms, a, b));
+        *avg_us = ms * 1000.f / (float)(rounds * n);
+        *bytes = op_bytes(m, kind, position);
+        *launches = n;
+    }
+    (void)hipEventDestroy(a);
+    (void)hipEventDestroy(b);
+    return st;
 }
 
 int l0h_model_destroy(l0h_model* m) {
