@@ -6,10 +6,10 @@
 // Layout: cache [batch, max_seq, n_kv * head_dim] (LlmKvCache.cs:5-8). A lane owns 8 dims of a
 // row (one 16-byte fp16 load), head_dim/8 lanes cover a row, so a wave instruction reads 4
 // (head_dim 128) or 8 (head_dim 64) positions of 256/128 contiguous bytes. Scores and
-// probabilities are staged in LDS, softmax is fp32 in the log2 domain, and the last block of
-// each (batch, kv head) to finish merges the splits' (max, sum, acc) partials with a
-// log-sum-exp combine, so one launch produces the output. The completion counter resets itself,
-// so the kernel can be replayed inside a graph.
+// probabilities are staged in LDS, softmax is fp32 in the log2 domain, and each block writes its
+// (max, sum, acc) partial; a second small kernel merges the splits with a log-sum-exp combine.
+// The kernel boundary publishes the partials, so no block waits on another and no device-scope
+// fence is needed (on gfx950 such a fence writes back the L2).
 #include "kernels.h"
 
 #include <cmath>
@@ -21,7 +21,7 @@ constexpr int kBlock = 256;
 constexpr int kGroupMax = 8;   // q heads per kv head
 constexpr int kChunkMax = 1024;  // positions per block (scores staged in LDS)
 constexpr int kUnroll = 4;
-constexpr int kMaxSplitsMerge = 256;  // splits whose merge weights are staged in LDS
+constexpr int kMergeBlock = 256;
 
 template <int CTRL, int ROW_MASK>
 __device__ __forceinline__ float dpp_src(float v) {
@@ -100,7 +100,6 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(const AttnParams p,
     __shared__ float s_scores[kGroupMax * kChunkMax];
     __shared__ float s_acc[4][kGroupMax][HD];
     __shared__ float s_m[kGroupMax], s_l[kGroupMax];
-    __shared__ bool s_last;
 
     const int split = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
     const int G = p.nh / p.nkv;
@@ -127,6 +126,16 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(const AttnParams p,
     }
     const T* kbase = static_cast<const T*>(p.kc) + (size_t)b * cache_batch_stride + (size_t)g * HD + lg * 8;
     const T* vbase = static_cast<const T*>(p.vc) + (size_t)b * cache_batch_stride + (size_t)g * HD + lg * 8;
+
+    // The first batch of V rows is requested together with the K rows, so a chunk that fits one
+    // batch (the decode case) costs a single HBM round trip.
+    CacheRow<CT> vpre[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; u++) {
+        const int t = grp + u * NG;
+        if (t < n) vpre[u].load(vbase + (size_t)(lo + t) * kv_dim);
+        else vpre[u].zero();
+    }
 
     // Phase A: scores of this block's positions into LDS.
     for (int t0 = grp; t0 < n; t0 += NG * kUnroll) {
@@ -186,7 +195,8 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(const AttnParams p,
 #pragma unroll
         for (int u = 0; u < kUnroll; u++) {
             const int t = t0 + u * NG;
-            if (t < n) vr[u].load(vbase + (size_t)(lo + t) * kv_dim);
+            if (t0 == grp) vr[u] = vpre[u];
+            else if (t < n) vr[u].load(vbase + (size_t)(lo + t) * kv_dim);
             else vr[u].zero();
         }
 #pragma unroll
@@ -238,64 +248,63 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(const AttnParams p,
         part[G * HD + threadIdx.x] = n > 0 ? s_m[threadIdx.x] : -INFINITY;
         part[G * HD + G + threadIdx.x] = n > 0 ? s_l[threadIdx.x] : 0.f;
     }
-    __threadfence();
-    __syncthreads();
-    unsigned* ticket = p.tickets + (size_t)b * p.nkv + g;
-    if (threadIdx.x == 0) s_last = atomicAdd(ticket, 1u) == (unsigned)(p.splits - 1);
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
+}
 
-    // Last block of this (batch, kv head): log-sum-exp merge of the splits. The other blocks
-    // published their partials with a release fence before taking a ticket; the acquire fence
-    // above makes them visible to plain loads, which can all be in flight at once.
-    const float* all = p.partials + ((size_t)b * p.nkv + g) * p.splits * (size_t)G * (HD + 2);
+// Log-sum-exp merge of the splits' partials: one block per (q head of the group, kv head,
+// batch). Wave w folds splits w, w+4, ... against its own running max (lane owns dims lane,
+// lane+64), then the four wave results are combined in a fixed order, so the output does not
+// depend on timing.
+template <int HD>
+__global__ __launch_bounds__(kMergeBlock) void attn_merge_kernel(const AttnParams p) {
+    constexpr int kWavesM = kMergeBlock / 64;
+    constexpr int DPL = (HD + 63) / 64;  // dims per lane
+    __shared__ float s_num[kWavesM][HD];
+    __shared__ float s_wm[kWavesM], s_wden[kWavesM];
+    const int h = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int G = p.nh / p.nkv;
     const size_t stride = (size_t)G * (HD + 2);
-    __shared__ float s_scale[kGroupMax][kMaxSplitsMerge];
-    __shared__ float s_den[kGroupMax];
-    const bool staged = p.splits <= kMaxSplitsMerge;
-    if (staged) {
-        // Per head: M = max m_s, scale_s = exp2(m_s - M), den = sum scale_s * l_s (wave h).
-        for (int h = wave; h < G; h += 4) {
-            float M = -INFINITY;
-            for (int s = lane; s < p.splits; s += 64) M = fmaxf(M, all[s * stride + G * HD + h]);
-            M = wave_max(M);
-            float den = 0.f;
-            for (int s = lane; s < p.splits; s += 64) {
-                const float ms = all[s * stride + G * HD + h];
-                const float w = ms == -INFINITY ? 0.f : exp2f(ms - M);
-                s_scale[h][s] = w;
-                den = fmaf(w, all[s * stride + G * HD + G + h], den);
-            }
-            den = wave_sum(den);
-            if (lane == 0) s_den[h] = den;
+    const float* all = p.partials + ((size_t)b * p.nkv + g) * p.splits * stride;
+    float M = -INFINITY;
+    for (int s = wave; s < p.splits; s += kWavesM) M = fmaxf(M, all[s * stride + G * HD + h]);
+    float num[DPL], den = 0.f;
+#pragma unroll
+    for (int j = 0; j < DPL; j++) num[j] = 0.f;
+    if (M != -INFINITY) {
+#pragma unroll 4
+        for (int s = wave; s < p.splits; s += kWavesM) {
+            const float* ps = all + s * stride;
+            const float ms = ps[G * HD + h];
+            const float w = ms == -INFINITY ? 0.f : exp2f(ms - M);
+            den = fmaf(w, ps[G * HD + G + h], den);
+#pragma unroll
+            for (int j = 0; j < DPL; j++)
+                if (lane + 64 * j < HD) num[j] = fmaf(w, ps[h * HD + lane + 64 * j], num[j]);
         }
-        __syncthreads();
     }
-    for (int idx = threadIdx.x; idx < G * HD; idx += kBlock) {
-        const int h = idx / HD, d = idx - h * HD;
-        float num = 0.f, den = 0.f;
-        if (staged) {
-            for (int s = 0; s < p.splits; s++) num = fmaf(s_scale[h][s], all[s * stride + idx], num);
-            den = s_den[h];
-        } else {
-            float M = -INFINITY;
-            for (int s = 0; s < p.splits; s++) M = fmaxf(M, all[s * stride + G * HD + h]);
-            if (M != -INFINITY) {
-                for (int s = 0; s < p.splits; s++) {
-                    const float* ps = all + s * stride;
-                    const float ms = ps[G * HD + h];
-                    if (ms == -INFINITY) continue;
-                    const float w = exp2f(ms - M);
-                    num = fmaf(w, ps[idx], num);
-                    den = fmaf(w, ps[G * HD + G + h], den);
-                }
+#pragma unroll
+    for (int j = 0; j < DPL; j++)
+        if (lane + 64 * j < HD) s_num[wave][lane + 64 * j] = num[j];
+    if (lane == 0) {
+        s_wm[wave] = M;
+        s_wden[wave] = den;
+    }
+    __syncthreads();
+    float Mt = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWavesM; w++) Mt = fmaxf(Mt, s_wm[w]);
+    for (int d = threadIdx.x; d < HD; d += kMergeBlock) {
+        float n = 0.f, dd = 0.f;
+        if (Mt != -INFINITY) {
+#pragma unroll
+            for (int w = 0; w < kWavesM; w++) {
+                const float sc = s_wm[w] == -INFINITY ? 0.f : exp2f(s_wm[w] - Mt);
+                n = fmaf(sc, s_num[w][d], n);
+                dd = fmaf(sc, s_wden[w], dd);
             }
         }
-        const float o = den > 0.f ? num / den : 0.f;
-        store_act(p.out, p.out_dtype, (size_t)b * p.nh * HD + (size_t)(g * G + h) * HD + d, o);
+        store_act(p.out, p.out_dtype, (size_t)b * p.nh * HD + (size_t)(g * G + h) * HD + d, dd > 0.f ? n / dd : 0.f);
     }
-    if (threadIdx.x == 0) *ticket = 0u;
 }
 
 template <int HD>
@@ -305,7 +314,10 @@ int launch_hd(hipStream_t s, const AttnParams& p, int seq_len_step, size_t cache
         attn_decode_kernel<HD, L0H_F16><<<grid, kBlock, 0, s>>>(p, seq_len_step, cache_batch_stride);
     else
         attn_decode_kernel<HD, L0H_F32><<<grid, kBlock, 0, s>>>(p, seq_len_step, cache_batch_stride);
-    return launch_status("attention");
+    int st = launch_status("attention");
+    if (st) return st;
+    attn_merge_kernel<HD><<<dim3(p.nh / p.nkv, p.nkv, p.batch), kMergeBlock, 0, s>>>(p);
+    return launch_status("attention merge");
 }
 
 int launch_any(hipStream_t s, const AttnParams& p, int seq_len_step, size_t cache_batch_stride) {
@@ -317,7 +329,7 @@ int launch_any(hipStream_t s, const AttnParams& p, int seq_len_step, size_t cach
         return fail(L0H_ERR_INVALID_ARG, "cache dtype must be F16 or F32");
     if (p.splits < 1 || (size_t)p.max_seq_len > (size_t)p.splits * kChunkMax)
         return fail(L0H_ERR_INVALID_ARG, "too few splits for the sequence length");
-    if (!p.partials || !p.tickets) return fail(L0H_ERR_INVALID_ARG, "attention workspace missing");
+    if (!p.partials) return fail(L0H_ERR_INVALID_ARG, "attention workspace missing");
     switch (p.head_dim) {
     case 16: return launch_hd<16>(s, p, seq_len_step, cache_batch_stride);
     case 32: return launch_hd<32>(s, p, seq_len_step, cache_batch_stride);

@@ -112,8 +112,12 @@ __device__ __forceinline__ void store_cache(void* cache, int dt, size_t idx, flo
         static_cast<float*>(cache)[idx] = v;
 }
 
-// Epilogue for the RoPE-paired rows (r0, r0+1) of the fused q|k|v matrix.
-__device__ __forceinline__ void qkv_pair(const GemvParams& p, int row, float v0, float v1, int pos) {
+constexpr int kMaxRotaryHalf = 128;  // cos/sin table entries per block (rotary_dim <= 256)
+
+// Epilogue for the RoPE-paired rows (r0, r0+1) of the fused q|k|v matrix; cs/sn hold
+// cos/sin(pos * inv_freq[i]) * scale for this launch's position.
+__device__ __forceinline__ void qkv_pair(const GemvParams& p, int row, float v0, float v1, int pos,
+                                         const float* cs_tab, const float* sn_tab) {
     const int hd = p.head_dim, rot = p.rotary_dim;
     if (row >= p.q_dim + p.kv_dim) {  // v rows: natural order
         const int off = row - p.q_dim - p.kv_dim;
@@ -131,11 +135,7 @@ __device__ __forceinline__ void qkv_pair(const GemvParams& p, int row, float v0,
         const int i = j >> 1;
         d0 = i;
         d1 = i + (rot >> 1);
-        const float angle = (float)pos * p.inv_freq[i];
-        float sn, cs;
-        sincosf(angle, &sn, &cs);
-        cs *= p.rope_scale;
-        sn *= p.rope_scale;
+        const float cs = cs_tab[i], sn = sn_tab[i];
         o0 = v0 * cs - v1 * sn;
         o1 = v1 * cs + v0 * sn;
     } else {
@@ -154,13 +154,17 @@ __device__ __forceinline__ void qkv_pair(const GemvParams& p, int row, float v0,
     }
 }
 
-// R rows per wave, U chunks in flight per row per lane, MR activation rows, XLDS: x staged in LDS.
-template <int WT, int R, int U, int MR, bool XLDS>
+// R rows per wave, U chunks in flight per row per lane, MR activation rows, XLDS: x staged in
+// LDS, EPI: EPI_STORE (store or residual, chosen at run time), EPI_SWIGLU or EPI_QKV.
+template <int WT, int R, int U, int MR, bool XLDS, int EPI>
 __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p) {
     extern __shared__ float4 smem4[];
     float* xs = reinterpret_cast<float*>(smem4);  // [MR, K] when XLDS
     __shared__ float red[kWaves];
     __shared__ float xsum_s[MR];
+    __shared__ float rope_cs[EPI == EPI_QKV ? kMaxRotaryHalf : 1];
+    __shared__ float rope_sn[EPI == EPI_QKV ? kMaxRotaryHalf : 1];
+    int pos = 0;
     constexpr int EPC = WTraits<WT>::kElems;
     const int K = p.k, N = p.n;
     const int C = K / EPC;
@@ -173,19 +177,65 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p) {
         return reinterpret_cast<const uint4*>(static_cast<const char*>(p.w) +
                                               (size_t)min(row, N - 1) * K * WTraits<WT>::kBytes);
     };
-    uint4 wv[U][R];
-    auto load_batch = [&](int r0, int c0) {
+    uint4 wa[U][R], wb[U][R];  // double buffer: item i computes from one while item i+1 loads
+    auto load_into = [&](uint4 (&w)[U][R], int r0, int c0) {
 #pragma unroll
         for (int u = 0; u < U; u++) {
             const int c = c0 + 64 * u;
 #pragma unroll
-            for (int r = 0; r < R; r++) wv[u][r] = c < C ? ld_nt16(row_ptr(r0 + r) + c) : make_uint4(0u, 0u, 0u, 0u);
+            for (int r = 0; r < R; r++) w[u][r] = c < C ? ld_nt16(row_ptr(r0 + r) + c) : make_uint4(0u, 0u, 0u, 0u);
         }
     };
+    const int nb = (C + 64 * U - 1) / (64 * U);  // batches per row group, the same for every lane
     // The first batch of weight loads goes out before the activations are staged, so the
     // prologue overlaps their HBM latency.
-    bool prefetched = row0 < N && lane < C;
-    if (prefetched) load_batch(row0, lane);
+    // Per-row values the epilogue needs (int8 scale, bias, residual), fetched with the row group's
+    // first weight batch so the epilogue issues no dependent global load. A lane holds the values
+    // of the rows it finalizes: row r0 + r for lane mr * R + r (store / residual), or rows
+    // r0 + 2j and r0 + 2j + 1 for lane j (SwiGLU and q|k|v pairs).
+    struct Side {
+        float s0 = 1.f, s1 = 1.f, b0 = 0.f, b1 = 0.f, res = 0.f;
+    };
+    auto load_side = [&](int r0) {
+        Side sd;
+        if constexpr (EPI == EPI_STORE) {
+            const int r = lane % R, mr = lane / R;
+            if (mr < MR) {
+                const int row = min(r0 + r, N - 1);
+                if constexpr (WT == L0H_I8PC) sd.s0 = __half2float(__ushort_as_half(p.scales[row]));
+                if (p.bias) sd.b0 = p.bias[row];
+                if (p.epilogue == EPI_RESIDUAL) sd.res = p.resid[(size_t)mr * N + row];
+            }
+        } else if (lane < R / 2) {
+            const int row = min(r0 + 2 * lane, N - 2);
+            if constexpr (WT == L0H_I8PC) {
+                sd.s0 = __half2float(__ushort_as_half(p.scales[row]));
+                sd.s1 = __half2float(__ushort_as_half(p.scales[row + 1]));
+            }
+            if (p.bias) {
+                sd.b0 = p.bias[row];
+                sd.b1 = p.bias[row + 1];
+            }
+        }
+        return sd;
+    };
+    Side side_cur, side_next;
+    if (row0 < N) {
+        load_into(wa, row0, lane);
+        side_cur = load_side(row0);
+    }
+
+    if constexpr (EPI == EPI_QKV) {
+        pos = *p.position;
+        // cos/sin of this position for every rotated pair, once per block (accurate sincos of
+        // the fp32 product pos * inv_freq[i]); published by the staging barrier below.
+        for (int i = threadIdx.x; i < p.rotary_dim / 2; i += kBlock) {
+            float sn, cs;
+            sincosf((float)pos * p.inv_freq[i], &sn, &cs);
+            rope_cs[i] = cs * p.rope_scale;
+            rope_sn[i] = sn * p.rope_scale;
+        }
+    }
 
     // Stage activations (and RMSNorm) in LDS.
     if constexpr (XLDS) {
@@ -244,18 +294,16 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p) {
         }
     }
     const float* xg = static_cast<const float*>(p.x);
-    // No barrier below this point: waves run their row groups independently.
-    for (; row0 < N; row0 += wave_stride) {
-
+    // Pipelined stream over this wave's (row group, batch) items: the loads of item i+1 are issued
+    // before item i is computed, across row-group boundaries, so every HBM round trip overlaps
+    // compute. No barrier below this point: waves run independently.
     float acc[MR][R];
 #pragma unroll
     for (int mr = 0; mr < MR; mr++)
 #pragma unroll
         for (int r = 0; r < R; r++) acc[mr][r] = 0.f;
 
-    for (int c0 = lane; c0 < C; c0 += 64 * U) {
-        if (!prefetched) load_batch(row0, c0);
-        prefetched = false;
+    auto compute = [&](const uint4 (&w)[U][R], int c0) {
 #pragma unroll
         for (int u = 0; u < U; u++) {
             const int c = c0 + 64 * u;
@@ -274,75 +322,84 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p) {
                         xv[4 * q + 3] = t.w;
                     }
 #pragma unroll
-                    for (int r = 0; r < R; r++) chunk_fma<WT>(wv[u][r], xv, acc[mr][r]);
+                    for (int r = 0; r < R; r++) chunk_fma<WT>(w[u][r], xv, acc[mr][r]);
                 }
             }
         }
-    }
+    };
 
-    // Reduce across the wave; every lane gets every row's sum.
-    float sums[MR][R];
+    // Wave reduction and epilogue of the row group starting at r0; resets the accumulators.
+    auto finish = [&](int r0, const Side& sd) {
+        float sums[MR][R];
 #pragma unroll
-    for (int mr = 0; mr < MR; mr++)
+        for (int mr = 0; mr < MR; mr++)
 #pragma unroll
-        for (int r = 0; r < R; r++) sums[mr][r] = wave_sum(acc[mr][r]);
-
-    if constexpr (WT == L0H_I8PC) {
+            for (int r = 0; r < R; r++) {
+                sums[mr][r] = wave_sum(acc[mr][r]);
+                acc[mr][r] = 0.f;
+            }
+        if constexpr (EPI == EPI_STORE) {
 #pragma unroll
-        for (int r = 0; r < R; r++) {
-            const int row = min(row0 + r, N - 1);
-            const float sc = __half2float(__ushort_as_half(p.scales[row]));
+            for (int mr = 0; mr < MR; mr++)
 #pragma unroll
-            for (int mr = 0; mr < MR; mr++) sums[mr][r] = (sums[mr][r] - 128.0f * xsum_s[mr]) * sc;
-        }
-    }
-
-    if (p.epilogue == EPI_STORE || p.epilogue == EPI_RESIDUAL) {
+                for (int r = 0; r < R; r++) {
+                    const int row = r0 + r;
+                    if (lane == mr * R + r && row < N) {
+                        float v = sums[mr][r];
+                        if constexpr (WT == L0H_I8PC) v = (v - 128.0f * xsum_s[mr]) * sd.s0;
+                        v += sd.b0;
+                        if (p.epilogue == EPI_STORE)
+                            store_act(p.y, p.y_dtype, (size_t)mr * N + row, v);
+                        else
+                            p.resid[(size_t)mr * N + row] = sd.res + v;
+                    }
+                }
+        } else {
 #pragma unroll
-        for (int r = 0; r < R; r++) {
-            const int row = row0 + r;
-            if (lane == r && row < N) {
-#pragma unroll
-                for (int mr = 0; mr < MR; mr++) {
-                    float v = sums[mr][r];
-                    if (p.bias) v += p.bias[row];
-                    if (p.epilogue == EPI_STORE)
-                        store_act(p.y, p.y_dtype, (size_t)mr * N + row, v);
+            for (int j = 0; j < R / 2; j++) {
+                const int row = r0 + 2 * j;
+                if (lane == j && row + 1 < N) {
+                    float v0 = sums[0][2 * j], v1 = sums[0][2 * j + 1];
+                    if constexpr (WT == L0H_I8PC) {
+                        v0 = (v0 - 128.0f * xsum_s[0]) * sd.s0;
+                        v1 = (v1 - 128.0f * xsum_s[0]) * sd.s1;
+                    }
+                    v0 += sd.b0;
+                    v1 += sd.b1;
+                    if constexpr (EPI == EPI_SWIGLU)
+                        store_act(p.y, p.y_dtype, (size_t)(row >> 1), silu(v0) * v1);
                     else
-                        p.resid[(size_t)mr * N + row] += v;
+                        qkv_pair(p, row, v0, v1, pos, rope_cs, rope_sn);
                 }
             }
         }
-    } else if (p.epilogue == EPI_SWIGLU) {
-#pragma unroll
-        for (int j = 0; j < R / 2; j++) {
-            const int row = row0 + 2 * j;
-            if (lane == j && row + 1 < N) {
-                float g = sums[0][2 * j], u = sums[0][2 * j + 1];
-                if (p.bias) {
-                    g += p.bias[row];
-                    u += p.bias[row + 1];
-                }
-                store_act(p.y, p.y_dtype, (size_t)(row >> 1), silu(g) * u);
-            }
+    };
+
+    int b = 0;  // batch of the current row group
+    auto step = [&](uint4 (&cur)[U][R], uint4 (&nxt)[U][R]) -> bool {
+        int n_row0 = row0, n_b = b + 1;
+        if (n_b == nb) {
+            n_b = 0;
+            n_row0 += wave_stride;
         }
-    } else {  // EPI_QKV
-        const int pos = *p.position;
-#pragma unroll
-        for (int j = 0; j < R / 2; j++) {
-            const int row = row0 + 2 * j;
-            if (lane == j && row + 1 < N) {
-                float v0 = sums[0][2 * j], v1 = sums[0][2 * j + 1];
-                if (p.bias) {
-                    v0 += p.bias[row];
-                    v1 += p.bias[row + 1];
-                }
-                qkv_pair(p, row, v0, v1, pos);
-            }
+        const bool more = n_row0 < N;
+        if (more) {
+            load_into(nxt, n_row0, lane + 64 * U * n_b);
+            if (n_b == 0) side_next = load_side(n_row0);
+        }
+        compute(cur, lane + 64 * U * b);
+        if (b == nb - 1) {
+            finish(row0, side_cur);
+            side_cur = side_next;
+        }
+        row0 = n_row0;
+        b = n_b;
+        return more;
+    };
+    if (row0 < N) {
+        while (step(wa, wb) && step(wb, wa)) {
         }
     }
-    prefetched = false;
-    }  // row groups
 }
 
 // Any shape: one wave per (activation row, output row), scalar loads. STORE / RESIDUAL only.
@@ -375,13 +432,13 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_generic_kernel(const GemvParam
     }
 }
 
-template <int WT, int R, int U, int MR, bool XLDS>
+template <int WT, int R, int U, int MR, bool XLDS, int EPI = EPI_STORE>
 int launch_fast(hipStream_t s, const GemvParams& p) {
     const unsigned rows_per_block = kWaves * R;
     unsigned grid = ceil_div(p.n, rows_per_block);
     if (p.max_blocks > 0) grid = std::min<unsigned>(grid, (unsigned)p.max_blocks);
     const size_t shmem = XLDS ? (size_t)MR * p.k * sizeof(float) : 0;
-    auto kern = gemv_nk_kernel<WT, R, U, MR, XLDS>;
+    auto kern = gemv_nk_kernel<WT, R, U, MR, XLDS, EPI>;
     if (shmem > 64 * 1024) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem);
@@ -393,10 +450,20 @@ int launch_fast(hipStream_t s, const GemvParams& p) {
 
 constexpr size_t kLdsBudget = 64 * 1024;
 
+// One activation row with x in LDS: the fused epilogues live here.
+template <int WT, int R, int U>
+int dispatch_one(hipStream_t s, const GemvParams& p) {
+    switch (p.epilogue) {
+    case EPI_SWIGLU: return launch_fast<WT, R, U, 1, true, EPI_SWIGLU>(s, p);
+    case EPI_QKV: return launch_fast<WT, R, U, 1, true, EPI_QKV>(s, p);
+    default: return launch_fast<WT, R, U, 1, true, EPI_STORE>(s, p);
+    }
+}
+
 template <int WT, int R, int U>
 int dispatch_mr(hipStream_t s, const GemvParams& p, int mr) {
     const bool fits = (size_t)mr * p.k * sizeof(float) <= kLdsBudget;
-    if (mr == 1) return fits ? launch_fast<WT, R, U, 1, true>(s, p) : launch_fast<WT, R, U, 1, false>(s, p);
+    if (mr == 1) return fits ? dispatch_one<WT, R, U>(s, p) : launch_fast<WT, R, U, 1, false>(s, p);
     if (mr == 2) return fits ? launch_fast<WT, R, U, 2, true>(s, p) : launch_fast<WT, R, U, 2, false>(s, p);
     if (mr == 4) return fits ? launch_fast<WT, R, U, 4, true>(s, p) : launch_fast<WT, R, U, 4, false>(s, p);
     return fits ? launch_fast<WT, R, U, 8, true>(s, p) : launch_fast<WT, R, U, 8, false>(s, p);
@@ -418,19 +485,18 @@ int dispatch_wt(hipStream_t s, const GemvParams& p, int mr) {
     if constexpr (WT == L0H_I8PC) {
         if (mr == 1 && (size_t)p.k * sizeof(float) <= kLdsBudget) {
             switch (int8_ru_choice()) {
-            case 24: return launch_fast<WT, 2, 4, 1, true>(s, p);
-            case 28: return launch_fast<WT, 2, 8, 1, true>(s, p);
-            case 42: return launch_fast<WT, 4, 2, 1, true>(s, p);
-            case 48: return launch_fast<WT, 4, 8, 1, true>(s, p);
-            case 82: return launch_fast<WT, 8, 2, 1, true>(s, p);
-            case 84: return launch_fast<WT, 8, 4, 1, true>(s, p);
+            case 22: return dispatch_one<WT, 2, 2>(s, p);
+            case 42: return dispatch_one<WT, 4, 2>(s, p);
+            case 44: return dispatch_one<WT, 4, 4>(s, p);
+            case 82: return dispatch_one<WT, 8, 2>(s, p);
             default: break;
             }
         }
     }
     // Rows per wave and chunks in flight, chosen per weight width.
-    if constexpr (WT == L0H_F32) return dispatch_mr<WT, 4, 4>(s, p, mr);
-    else return dispatch_mr<WT, 4, 4>(s, p, mr);
+    // (R, U) = (2, 4): 2 rows per wave, 4 x 1 KiB loads per row in flight, double-buffered
+    // (the fastest of the measured shapes at the Llama-3.1-8B decode sizes).
+    return dispatch_mr<WT, 2, 4>(s, p, mr);
 }
 
 }  // namespace
@@ -439,8 +505,8 @@ int gemv_max_blocks(int compute_units) {
     // L0H_GEMV_BLOCKS_PER_CU overrides the default (0: one block per row group, no cap).
     static const int per_cu = [] {
         const char* e = std::getenv("L0H_GEMV_BLOCKS_PER_CU");
-        const int v = e ? std::atoi(e) : 2;
-        return v >= 0 ? v : 2;
+        const int v = e ? std::atoi(e) : 4;
+        return v >= 0 ? v : 4;
     }();
     return per_cu == 0 ? 0 : std::max(1, compute_units) * per_cu;
 }

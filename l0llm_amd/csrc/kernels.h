@@ -103,7 +103,6 @@ struct AttnParams {
     int max_seq_len = 0;
     int splits = 1;  // sequence partitions per (batch, kv head)
     float* partials = nullptr;  // [batch, nkv, splits, group, head_dim + 2]
-    unsigned* tickets = nullptr;  // [batch * nkv]
 };
 int attention_default_splits(int batch, int nkv, int max_len, int compute_units);
 size_t attention_partials_bytes(const AttnParams& p);

@@ -75,7 +75,6 @@ struct l0h_model {
     int out_capacity = 0;
     // workspaces
     float* attn_partials = nullptr;
-    unsigned* attn_tickets = nullptr;
     unsigned long long* argmax_partials = nullptr;
     unsigned* argmax_ticket = nullptr;
     int attn_splits = 1;
@@ -340,7 +339,6 @@ int launch_op(l0h_model* m, hipStream_t s, int kind, int li) {
         a.max_seq_len = m->max_seq;
         a.splits = m->attn_splits;
         a.partials = m->attn_partials;
-        a.tickets = m->attn_tickets;
         return launch_attention_decode(s, a);
     }
     case L0H_KERNEL_O_PROJ: {  // LlmDecoderLayer.cs:333, residual half of :183
@@ -577,8 +575,6 @@ int l0h_model_create(l0h_device* dev, const l0h_model_config* cfg, int precision
     a.head_dim = c.head_dim;
     a.splits = m->attn_splits;
     if ((st = alloc_owned(m, attention_partials_bytes(a), reinterpret_cast<void**>(&m->attn_partials)))) return bail(st);
-    if ((st = alloc_t(m, (size_t)c.num_key_value_heads, &m->attn_tickets))) return bail(st);
-    if ((st = l0h_fill_zero(dev, m->attn_tickets, c.num_key_value_heads * sizeof(unsigned)))) return bail(st);
     if ((st = alloc_t(m, (size_t)argmax_blocks(c.vocab_size), &m->argmax_partials))) return bail(st);
     if ((st = alloc_t(m, 1, &m->argmax_ticket))) return bail(st);
     if ((st = l0h_fill_zero(dev, m->argmax_ticket, sizeof(unsigned)))) return bail(st);

@@ -17,10 +17,9 @@ int attention_run(l0h_device* dev, AttnParams p, bool prefill, int pos0, int tok
     }
     p.splits = attention_default_splits(p.batch, p.nkv, p.max_seq_len, dev->compute_units);
     const size_t bytes = attention_partials_bytes(p);
-    int st = ensure_workspace(dev, bytes, (size_t)p.batch * p.nkv);
+    int st = ensure_workspace(dev, bytes, 0);
     if (st) return st;
     p.partials = static_cast<float*>(dev->workspace);
-    p.tickets = dev->tickets;
     return prefill ? launch_attention_prefill(dev->stream, p, pos0, tokens) : launch_attention_decode(dev->stream, p);
 }
 

@@ -287,7 +287,7 @@ def test_attention_decode_matches_oracle(device, suite, hd, nh, nkv, seq, cache)
     suite.attention_execute(up(device, q), up(device, kc), up(device, vc), ob, hd, nh, nkv, seq, max_seq, cache_dtype=cache)
     out = ob.read()
     assert rel_err(out, want) < 1e-4, rel_err(out, want)
-    # replayed: the in-kernel split merge resets its counters
+    # replayed: the merge is fixed-order, so results repeat bit for bit
     suite.attention_execute(up(device, q), up(device, kc), up(device, vc), ob, hd, nh, nkv, seq, max_seq, cache_dtype=cache)
     np.testing.assert_array_equal(ob.read(), out)
 
