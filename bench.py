@@ -63,6 +63,26 @@ def kernel_table(model, position: int, rounds: int) -> dict:
     return out
 
 
+def hbm_copy_probe(dev, mib: int = 1024, reps: int = 10) -> dict:
+    """Achievable HBM rate on this box: Copy.Execute (a 16-byte grid-stride copy kernel) over two
+    buffers of `mib` MiB, far larger than the 256 MB Infinity Cache; bytes = read + write."""
+    import l0llm_amd as l0
+
+    n = mib * (1 << 20) // 4
+    suite = l0.LlmKernelSuite(dev)
+    with dev.alloc(4 * n) as a, dev.alloc(4 * n) as b:
+        a.zero()
+        suite.copy_execute(a, b, 0, n)
+        dev.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            suite.copy_execute(a, b, 0, n)
+        dev.synchronize()
+        dt = (time.perf_counter() - t0) / reps
+    return dict(kernel="copy16_kernel", bytes_per_launch=8 * n, avg_us=round(dt * 1e6, 1),
+                gbs=round(8 * n / dt / 1e9, 1))
+
+
 def cpu_baseline(model, cfg, tokens: int, position: int) -> dict:
     from oracle import pyoracle as orc
 
@@ -102,7 +122,12 @@ def main() -> int:
     ap.add_argument("--profile-rounds", type=int, default=4,
                     help="passes over all layers when timing each kernel kind for the roofline")
     ap.add_argument("--cpu-tokens", type=int, default=2, help="tokens in the CPU baseline sample (0: skip)")
+    ap.add_argument("--eager-step", action="store_true",
+                    help="enqueue the decode step's kernels one by one instead of replaying its HIP graph "
+                         "(same kernels; for profilers that cannot trace graph launches)")
     args = ap.parse_args()
+    if args.eager_step:
+        os.environ["L0H_EAGER_STEP"] = "1"  # read by the library when the model is created
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: the path runs on a single GPU (no sharding or collectives "
               "in this build); run it with --gpus 1.", file=sys.stderr)
@@ -112,6 +137,8 @@ def main() -> int:
 
     cfg = llama8b()
     dev = l0.Device(0)
+    copy = hbm_copy_probe(dev)
+    log(f"HBM copy probe: {copy['gbs']} GB/s ({copy['bytes_per_launch']} bytes in {copy['avg_us']} us)")
     max_seq = args.ctx + args.steps + args.cpu_tokens + 8
     log(f"device {dev.name}; building the model (max_seq {max_seq})")
     model = l0.LlmModel(dev, cfg, precision=l0.PRECISION_INT8, cache_dtype=l0.F16, max_seq_len=max_seq)
@@ -170,7 +197,8 @@ def main() -> int:
         "config": {"workload": f"llama3.1-8b-shaped int8 weight-only greedy decode, batch 1, "
                                f"{args.ctx}-token prefilled KV cache (fp16), {args.steps} generated tokens",
                    "layers": 32, "hidden": 4096, "intermediate": 14336, "heads": 32, "kv_heads": 8,
-                   "head_dim": 128, "vocab": 128256, "batch": 1, "ctx": args.ctx},
+                   "head_dim": 128, "vocab": 128256, "batch": 1, "ctx": args.ctx,
+                   "step": "eager launches" if args.eager_step else "HIP graph replay"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": "gemv_nk_kernel<I8PC> (q|k|v, O, gate|up, down, lm_head)",
@@ -178,6 +206,7 @@ def main() -> int:
         "step_roofline": {"bytes_per_step": round(step_bytes), "ideal_tokens_per_s": round(HBM_PEAK_GBS * 1e9 / step_bytes, 1),
                           "frac": round(tps * step_bytes / (HBM_PEAK_GBS * 1e9), 4)},
         "kernels": table,
+        "hbm_copy_probe": copy,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -1,15 +1,21 @@
 // GQA decode attention over the KV cache for gfx950 (Attention.Execute / ExecutePrefill,
 // LlmDecoderLayer.cs:325-327, :369-371).
 //
-// Split-K over the sequence ("flash decoding"): block (split, kv head, batch) reads its slice
-// of the K and V rows of one kv head once and serves all the q heads of that group from it.
+// Split-K over the sequence ("flash decoding"): block (split, kv head, batch) reads its slice of
+// the K and V rows of one kv head once and serves all the q heads of that group from it.
 // Layout: cache [batch, max_seq, n_kv * head_dim] (LlmKvCache.cs:5-8). A lane owns 8 dims of a
-// row (one 16-byte fp16 load), head_dim/8 lanes cover a row, so a wave instruction reads 4
-// (head_dim 128) or 8 (head_dim 64) positions of 256/128 contiguous bytes. Scores and
-// probabilities are staged in LDS, softmax is fp32 in the log2 domain, and each block writes its
-// (max, sum, acc) partial; a second small kernel merges the splits with a log-sum-exp combine.
-// The kernel boundary publishes the partials, so no block waits on another and no device-scope
-// fence is needed (on gfx950 such a fence writes back the L2).
+// row (one 16-byte fp16 load, two for fp32), head_dim / 8 lanes cover a row, so a wave
+// instruction reads 64 / (head_dim / 8) positions of contiguous bytes. Each group of lanes that
+// shares a position slot keeps an online softmax (running max, sum and P.V accumulator, fp32,
+// log2 domain) over its positions; the slots of a block are combined at the end (lane shuffles,
+// then LDS across waves) into one (max, sum, acc) partial per q head. A second small kernel
+// merges the splits' partials with a log-sum-exp combine in a fixed order, so the result does
+// not depend on timing.
+//
+// Every load is unconditional (positions past the slice are clamped to valid rows and masked in
+// the softmax), the next step's K and V rows are requested before the current step is computed,
+// and all control flow is wave-uniform, so the in-order memory counter only ever waits for the
+// rows being computed.
 #include "kernels.h"
 
 #include <cmath>
@@ -18,18 +24,19 @@ namespace l0h {
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kGroupMax = 8;   // q heads per kv head
-constexpr int kChunkMax = 1024;  // positions per block (scores staged in LDS)
-constexpr int kUnroll = 4;
+constexpr int kWaves = kBlock / 64;
+constexpr int kGroupMax = 8;  // q heads per kv head
+constexpr int kUnroll = 4;    // positions per slot per step
 constexpr int kMergeBlock = 256;
+constexpr int kMaxSplits = 256;
 
 template <int CTRL, int ROW_MASK>
 __device__ __forceinline__ float dpp_src(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, false));
 }
 
-// Sum over the LPP lanes that share a position (2, 4 or 8 lanes of a row, or the full
-// 16-lane row), left in every lane of the group.
+// Sum over the LPP lanes that share a position (2, 4 or 8 lanes of a row, or the full 16-lane
+// row), left in every lane of the group.
 template <int LPP>
 __device__ __forceinline__ float group_sum(float v) {
     v += dpp_src<0xB1, 0xf>(v);  // quad_perm [1,0,3,2]
@@ -43,18 +50,6 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    return v;
-}
-
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
-
 template <int CT>
 struct CacheRow;
 template <>
@@ -62,7 +57,6 @@ struct CacheRow<L0H_F16> {
     using T = uint16_t;
     uint4 raw;
     __device__ __forceinline__ void load(const T* p) { raw = ld_nt16(p); }
-    __device__ __forceinline__ void zero() { raw = make_uint4(0u, 0u, 0u, 0u); }
     __device__ __forceinline__ void get(float* f) const {
         const uint32_t d[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
@@ -76,248 +70,322 @@ struct CacheRow<L0H_F16> {
 template <>
 struct CacheRow<L0H_F32> {
     using T = float;
-    float4 a, b;
+    uint4 a, b;
     __device__ __forceinline__ void load(const T* p) {
-        uint4 t0 = ld_nt16(p);
-        a = make_float4(__uint_as_float(t0.x), __uint_as_float(t0.y), __uint_as_float(t0.z), __uint_as_float(t0.w));
-        uint4 t1 = ld_nt16(p + 4);
-        b = make_float4(__uint_as_float(t1.x), __uint_as_float(t1.y), __uint_as_float(t1.z), __uint_as_float(t1.w));
+        a = ld_nt16(p);
+        b = ld_nt16(p + 4);
     }
-    __device__ __forceinline__ void zero() { a = b = make_float4(0.f, 0.f, 0.f, 0.f); }
     __device__ __forceinline__ void get(float* f) const {
-        f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
-        f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+        f[0] = __uint_as_float(a.x); f[1] = __uint_as_float(a.y); f[2] = __uint_as_float(a.z); f[3] = __uint_as_float(a.w);
+        f[4] = __uint_as_float(b.x); f[5] = __uint_as_float(b.y); f[6] = __uint_as_float(b.z); f[7] = __uint_as_float(b.w);
     }
 };
 
-template <int HD, int CT>
-__global__ __launch_bounds__(kBlock) void attn_decode_kernel(const AttnParams p, int seq_len_step,
-                                                             size_t cache_batch_stride) {
+// 8 consecutive activation values (fp32 or fp16) as fp32.
+template <int QT>
+__device__ __forceinline__ void load8(const void* base, size_t idx, float* f) {
+    if constexpr (QT == L0H_F32) {
+        const uint4* p = reinterpret_cast<const uint4*>(static_cast<const float*>(base) + idx);
+        const uint4 a = p[0], b = p[1];
+        f[0] = __uint_as_float(a.x); f[1] = __uint_as_float(a.y); f[2] = __uint_as_float(a.z); f[3] = __uint_as_float(a.w);
+        f[4] = __uint_as_float(b.x); f[5] = __uint_as_float(b.y); f[6] = __uint_as_float(b.z); f[7] = __uint_as_float(b.w);
+    } else {
+        const uint4 a = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + idx);
+        const uint32_t d[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            float2 t = __half22float2(__builtin_bit_cast(__half2, d[j]));
+            f[2 * j] = t.x;
+            f[2 * j + 1] = t.y;
+        }
+    }
+}
+
+// Sequence length of batch entry b, and this split's slice [lo, lo + n) of it. Slices are whole
+// steps (NG * kUnroll positions) so a block's slots stay in step.
+template <int NG>
+__device__ __forceinline__ void split_range(const AttnParams& p, int seq_len_step, int b, int split, int& lo, int& n) {
+    int len = (p.seq_len_device ? *p.seq_len_device + p.seq_len_add : p.seq_len) + b * seq_len_step;
+    len = max(0, min(len, p.max_seq_len));
+    constexpr int kStep = NG * kUnroll;
+    int chunk = (len + p.splits - 1) / p.splits;
+    chunk = (chunk + kStep - 1) / kStep * kStep;
+    lo = split * chunk;
+    n = max(0, min(len, lo + chunk) - lo);
+}
+
+// QT: q dtype, G: q heads per kv head rounded up to a power of two (heads >= p.nh / p.nkv are
+// computed on clamped inputs and not written).
+template <int HD, int CT, int QT, int G>
+__global__ __launch_bounds__(kBlock) void attn_split_kernel(const AttnParams p, int seq_len_step,
+                                                            size_t cache_batch_stride) {
     constexpr int LPP = HD / 8;     // lanes per position
-    constexpr int PPW = 64 / LPP;   // positions per wave instruction
-    constexpr int NG = 4 * PPW;     // lane groups per block
+    constexpr int PPW = 64 / LPP;   // position slots per wave
+    constexpr int NG = kWaves * PPW;  // position slots per block
+    constexpr int U = kUnroll;
     using T = typename CacheRow<CT>::T;
-    __shared__ float s_scores[kGroupMax * kChunkMax];
-    __shared__ float s_acc[4][kGroupMax][HD];
-    __shared__ float s_m[kGroupMax], s_l[kGroupMax];
+    __shared__ float s_m[kWaves][G], s_l[kWaves][G];
+    __shared__ float s_acc[kWaves][G][HD];
 
     const int split = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
-    const int G = p.nh / p.nkv;
+    const int gsize = p.nh / p.nkv;
     const int kv_dim = p.nkv * HD;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lg = lane % LPP;
-    const int grp = wave * PPW + lane / LPP;
+    const int slot = wave * PPW + lane / LPP;
+    int lo, n;
+    split_range<NG>(p, seq_len_step, b, split, lo, n);
 
-    int len = (p.seq_len_device ? *p.seq_len_device + p.seq_len_add : p.seq_len) + b * seq_len_step;
-    len = min(len, p.max_seq_len);
-    const int chunk = (len + p.splits - 1) / p.splits;
-    const int lo = split * chunk;
-    const int n = max(0, min(len, lo + chunk) - lo);
-
-    // q for this lane's 8 dims of every head of the group, scaled by log2(e) / sqrt(HD).
-    float qr[kGroupMax][8];
+    // q: this lane's 8 dims of every head of the group, scaled by log2(e) / sqrt(HD).
+    float qr[G][8];
     const float qscale = 1.4426950408889634f / sqrtf((float)HD);
 #pragma unroll
-    for (int h = 0; h < kGroupMax; h++) {
+    for (int h = 0; h < G; h++) {
+        const int hh = min(h, gsize - 1);
+        load8<QT>(p.q, (size_t)b * p.nh * HD + (size_t)(g * gsize + hh) * HD + lg * 8, qr[h]);
 #pragma unroll
-        for (int d = 0; d < 8; d++)
-            qr[h][d] = h < G ? load_act(p.q, p.q_dtype, (size_t)b * p.nh * HD + (size_t)(g * G + h) * HD + lg * 8 + d) * qscale
-                             : 0.f;
+        for (int d = 0; d < 8; d++) qr[h][d] *= qscale;
     }
     const T* kbase = static_cast<const T*>(p.kc) + (size_t)b * cache_batch_stride + (size_t)g * HD + lg * 8;
     const T* vbase = static_cast<const T*>(p.vc) + (size_t)b * cache_batch_stride + (size_t)g * HD + lg * 8;
+    const int last = p.max_seq_len - 1;
 
-    // The first batch of V rows is requested together with the K rows, so a chunk that fits one
-    // batch (the decode case) costs a single HBM round trip.
-    CacheRow<CT> vpre[kUnroll];
+    CacheRow<CT> ka[U], va[U], kb[U], vb[U];
+    auto load = [&](CacheRow<CT> (&k)[U], CacheRow<CT> (&v)[U], int step) {
 #pragma unroll
-    for (int u = 0; u < kUnroll; u++) {
-        const int t = grp + u * NG;
-        if (t < n) vpre[u].load(vbase + (size_t)(lo + t) * kv_dim);
-        else vpre[u].zero();
-    }
-
-    // Phase A: scores of this block's positions into LDS.
-    for (int t0 = grp; t0 < n; t0 += NG * kUnroll) {
-        CacheRow<CT> kr[kUnroll];
-#pragma unroll
-        for (int u = 0; u < kUnroll; u++) {
-            const int t = t0 + u * NG;
-            if (t < n) kr[u].load(kbase + (size_t)(lo + t) * kv_dim);
-            else kr[u].zero();
+        for (int u = 0; u < U; u++) {
+            const int t = min(lo + step * NG * U + u * NG + slot, last);
+            k[u].load(kbase + (size_t)t * kv_dim);
         }
 #pragma unroll
-        for (int u = 0; u < kUnroll; u++) {
-            const int t = t0 + u * NG;
-            float kf[8];
-            kr[u].get(kf);
-#pragma unroll
-            for (int h = 0; h < kGroupMax; h++) {
-                if (h < G) {
-                    float s = 0.f;
-#pragma unroll
-                    for (int d = 0; d < 8; d++) s = fmaf(qr[h][d], kf[d], s);
-                    s = group_sum<LPP>(s);
-                    if (lg == h % LPP && t < n) s_scores[h * kChunkMax + t] = s;
-                }
-            }
+        for (int u = 0; u < U; u++) {
+            const int t = min(lo + step * NG * U + u * NG + slot, last);
+            v[u].load(vbase + (size_t)t * kv_dim);
         }
-    }
-    __syncthreads();
+    };
 
-    // Phase B: per-head max and exp (wave w handles heads w, w+4).
-    for (int h = wave; h < G; h += 4) {
-        float m = -INFINITY;
-        for (int t = lane; t < n; t += 64) m = fmaxf(m, s_scores[h * kChunkMax + t]);
-        m = wave_max(m);
-        float l = 0.f;
-        for (int t = lane; t < n; t += 64) {
-            const float e = exp2f(s_scores[h * kChunkMax + t] - m);
-            s_scores[h * kChunkMax + t] = e;
-            l += e;
-        }
-        l = wave_sum(l);
-        if (lane == 0) {
-            s_m[h] = m;
-            s_l[h] = l;
-        }
-    }
-    __syncthreads();
-
-    // Phase C: P . V per lane group, then across the groups of the wave.
-    float acc[kGroupMax][8];
+    float m[G], l[G], acc[G][8];
 #pragma unroll
-    for (int h = 0; h < kGroupMax; h++)
+    for (int h = 0; h < G; h++) {
+        m[h] = -INFINITY;
+        l[h] = 0.f;
 #pragma unroll
         for (int d = 0; d < 8; d++) acc[h][d] = 0.f;
-    for (int t0 = grp; t0 < n; t0 += NG * kUnroll) {
-        CacheRow<CT> vr[kUnroll];
+    }
+    auto compute = [&](const CacheRow<CT> (&k)[U], const CacheRow<CT> (&v)[U], int step) {
+        float sc[U][G];
 #pragma unroll
-        for (int u = 0; u < kUnroll; u++) {
-            const int t = t0 + u * NG;
-            if (t0 == grp) vr[u] = vpre[u];
-            else if (t < n) vr[u].load(vbase + (size_t)(lo + t) * kv_dim);
-            else vr[u].zero();
-        }
+        for (int u = 0; u < U; u++) {
+            const bool valid = step * NG * U + u * NG + slot < n;
+            float kf[8];
+            k[u].get(kf);
 #pragma unroll
-        for (int u = 0; u < kUnroll; u++) {
-            const int t = t0 + u * NG;
-            if (t < n) {
-                float vf[8];
-                vr[u].get(vf);
+            for (int h = 0; h < G; h++) {
+                float s = 0.f;
 #pragma unroll
-                for (int h = 0; h < kGroupMax; h++) {
-                    if (h < G) {
-                        const float pr = s_scores[h * kChunkMax + t];
-#pragma unroll
-                        for (int d = 0; d < 8; d++) acc[h][d] = fmaf(pr, vf[d], acc[h][d]);
-                    }
-                }
+                for (int d = 0; d < 8; d++) s = fmaf(qr[h][d], kf[d], s);
+                s = group_sum<LPP>(s);
+                sc[u][h] = valid ? s : -INFINITY;
             }
         }
-    }
+        float vf[U][8];
 #pragma unroll
-    for (int h = 0; h < kGroupMax; h++) {
-        if (h < G) {
+        for (int u = 0; u < U; u++) v[u].get(vf[u]);
+#pragma unroll
+        for (int h = 0; h < G; h++) {
+            float mx = m[h];
+#pragma unroll
+            for (int u = 0; u < U; u++) mx = fmaxf(mx, sc[u][h]);
+            const float ref = mx == -INFINITY ? 0.f : mx;  // no valid position yet: keep zeros
+            const float c = exp2f(m[h] - ref);
+            float pr[U];
+#pragma unroll
+            for (int u = 0; u < U; u++) pr[u] = exp2f(sc[u][h] - ref);
+            float lsum = l[h] * c;
+#pragma unroll
+            for (int u = 0; u < U; u++) lsum += pr[u];
+            l[h] = lsum;
 #pragma unroll
             for (int d = 0; d < 8; d++) {
-                float v = acc[h][d];
+                float a = acc[h][d] * c;
 #pragma unroll
-                for (int off = LPP; off < 64; off <<= 1) v += __shfl_xor(v, off, 64);
-                acc[h][d] = v;
+                for (int u = 0; u < U; u++) a = fmaf(pr[u], vf[u][d], a);
+                acc[h][d] = a;
             }
+            m[h] = mx;
+        }
+    };
+
+    // Steps of NG * U positions; the next step's rows are requested before the current one is
+    // computed, and the last step is computed with nothing issued behind it.
+    const int steps = (n + NG * U - 1) / (NG * U);  // block-uniform
+    if (steps > 0) {
+        load(ka, va, 0);
+        int s = 0;
+        for (;;) {
+            if (s + 1 == steps) {
+                compute(ka, va, s);
+                break;
+            }
+            load(kb, vb, s + 1);
+            compute(ka, va, s);
+            s++;
+            if (s + 1 == steps) {
+                compute(kb, vb, s);
+                break;
+            }
+            load(ka, va, s + 1);
+            compute(kb, vb, s);
+            s++;
         }
     }
-    if (lane < LPP) {
+
+    // Combine the slots of a wave: lanes lg of the PPW slots (offsets LPP, 2 LPP, ...).
 #pragma unroll
-        for (int h = 0; h < kGroupMax; h++)
-            if (h < G)
+    for (int h = 0; h < G; h++) {
+        float M = m[h];
 #pragma unroll
-                for (int d = 0; d < 8; d++) s_acc[wave][h][lg * 8 + d] = acc[h][d];
+        for (int off = LPP; off < 64; off <<= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+        const float c = M == -INFINITY ? 0.f : exp2f(m[h] - M);
+        float lw = l[h] * c;
+#pragma unroll
+        for (int off = LPP; off < 64; off <<= 1) lw += __shfl_xor(lw, off, 64);
+#pragma unroll
+        for (int d = 0; d < 8; d++) {
+            float a = acc[h][d] * c;
+#pragma unroll
+            for (int off = LPP; off < 64; off <<= 1) a += __shfl_xor(a, off, 64);
+            acc[h][d] = a;
+        }
+        if (lane < LPP) {
+#pragma unroll
+            for (int d = 0; d < 8; d++) s_acc[wave][h][lg * 8 + d] = acc[h][d];
+            if (lane == 0) {
+                s_m[wave][h] = M;
+                s_l[wave][h] = lw;
+            }
+        }
     }
     __syncthreads();
 
-    // Block partial -> workspace.
+    // Combine the waves (fixed order) and write the block's partial, or the output when the
+    // sequence is not split.
     const size_t pbase = (((size_t)b * p.nkv + g) * p.splits + split) * (size_t)G * (HD + 2);
-    float* part = p.partials + pbase;
-    for (int idx = threadIdx.x; idx < G * HD; idx += kBlock) {
+    for (int idx = tid; idx < G * HD; idx += kBlock) {
         const int h = idx / HD, d = idx - h * HD;
-        part[idx] = s_acc[0][h][d] + s_acc[1][h][d] + s_acc[2][h][d] + s_acc[3][h][d];
-    }
-    if (threadIdx.x < G) {
-        part[G * HD + threadIdx.x] = n > 0 ? s_m[threadIdx.x] : -INFINITY;
-        part[G * HD + G + threadIdx.x] = n > 0 ? s_l[threadIdx.x] : 0.f;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kWaves; w++) M = fmaxf(M, s_m[w][h]);
+        float num = 0.f, den = 0.f;
+#pragma unroll
+        for (int w = 0; w < kWaves; w++) {
+            const float c = M == -INFINITY ? 0.f : exp2f(s_m[w][h] - M);
+            num = fmaf(c, s_acc[w][h][d], num);
+            den = fmaf(c, s_l[w][h], den);
+        }
+        if (p.splits == 1) {
+            if (h < gsize)
+                store_act(p.out, p.out_dtype, (size_t)b * p.nh * HD + (size_t)(g * gsize + h) * HD + d,
+                          den > 0.f ? num / den : 0.f);
+        } else {
+            float* part = p.partials + pbase;
+            part[idx] = num;
+            if (d == 0) {
+                part[G * HD + h] = M;
+                part[G * HD + G + h] = den;
+            }
+        }
     }
 }
 
 // Log-sum-exp merge of the splits' partials: one block per (q head of the group, kv head,
-// batch). Wave w folds splits w, w+4, ... against its own running max (lane owns dims lane,
-// lane+64), then the four wave results are combined in a fixed order, so the output does not
-// depend on timing.
-template <int HD>
+// batch). The splits' maxima and sums go through LDS; thread (d, j) folds splits j, j + J, ...
+// for dim d (eight loads in flight), then the J partial sums are added in a fixed order.
+template <int HD, int G>
 __global__ __launch_bounds__(kMergeBlock) void attn_merge_kernel(const AttnParams p) {
-    constexpr int kWavesM = kMergeBlock / 64;
-    constexpr int DPL = (HD + 63) / 64;  // dims per lane
-    __shared__ float s_num[kWavesM][HD];
-    __shared__ float s_wm[kWavesM], s_wden[kWavesM];
+    constexpr int J = kMergeBlock / HD;  // split lanes per dim
+    __shared__ float s_w[kMaxSplits], s_lw[kMaxSplits], s_red[kMergeBlock / 64];
+    __shared__ float s_num[J][HD];
     const int h = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int G = p.nh / p.nkv;
+    const int tid = threadIdx.x;
+    const int gsize = p.nh / p.nkv;
+    const int S = p.splits;
     const size_t stride = (size_t)G * (HD + 2);
-    const float* all = p.partials + ((size_t)b * p.nkv + g) * p.splits * stride;
-    float M = -INFINITY;
-    for (int s = wave; s < p.splits; s += kWavesM) M = fmaxf(M, all[s * stride + G * HD + h]);
-    float num[DPL], den = 0.f;
+    const float* all = p.partials + ((size_t)b * p.nkv + g) * S * stride;
+    const int sc = min(tid, S - 1);
+    const float ms0 = all[(size_t)sc * stride + G * HD + h];
+    const float ls = all[(size_t)sc * stride + G * HD + G + h];
+    const float ms = tid < S ? ms0 : -INFINITY;
+    float M = ms;
 #pragma unroll
-    for (int j = 0; j < DPL; j++) num[j] = 0.f;
-    if (M != -INFINITY) {
-#pragma unroll 4
-        for (int s = wave; s < p.splits; s += kWavesM) {
-            const float* ps = all + s * stride;
-            const float ms = ps[G * HD + h];
-            const float w = ms == -INFINITY ? 0.f : exp2f(ms - M);
-            den = fmaf(w, ps[G * HD + G + h], den);
+    for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+    if ((tid & 63) == 0) s_red[tid >> 6] = M;
+    __syncthreads();
+    M = s_red[0];
 #pragma unroll
-            for (int j = 0; j < DPL; j++)
-                if (lane + 64 * j < HD) num[j] = fmaf(w, ps[h * HD + lane + 64 * j], num[j]);
-        }
-    }
-#pragma unroll
-    for (int j = 0; j < DPL; j++)
-        if (lane + 64 * j < HD) s_num[wave][lane + 64 * j] = num[j];
-    if (lane == 0) {
-        s_wm[wave] = M;
-        s_wden[wave] = den;
+    for (int w = 1; w < kMergeBlock / 64; w++) M = fmaxf(M, s_red[w]);
+    if (tid < S) {
+        const float w = (M == -INFINITY || ms == -INFINITY) ? 0.f : exp2f(ms - M);
+        s_w[tid] = w;
+        s_lw[tid] = w * ls;
     }
     __syncthreads();
-    float Mt = -INFINITY;
+    const int d = tid % HD, j = tid / HD;
+    float num[8];
 #pragma unroll
-    for (int w = 0; w < kWavesM; w++) Mt = fmaxf(Mt, s_wm[w]);
-    for (int d = threadIdx.x; d < HD; d += kMergeBlock) {
-        float n = 0.f, dd = 0.f;
-        if (Mt != -INFINITY) {
+    for (int u = 0; u < 8; u++) num[u] = 0.f;
+    for (int s0 = j; s0 < S; s0 += 8 * J) {
+        float v[8];
 #pragma unroll
-            for (int w = 0; w < kWavesM; w++) {
-                const float sc = s_wm[w] == -INFINITY ? 0.f : exp2f(s_wm[w] - Mt);
-                n = fmaf(sc, s_num[w][d], n);
-                dd = fmaf(sc, s_wden[w], dd);
-            }
-        }
-        store_act(p.out, p.out_dtype, (size_t)b * p.nh * HD + (size_t)(g * G + h) * HD + d, dd > 0.f ? n / dd : 0.f);
+        for (int u = 0; u < 8; u++) v[u] = all[(size_t)min(s0 + u * J, S - 1) * stride + h * HD + d];
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (s0 + u * J < S) num[u] = fmaf(s_w[s0 + u * J], v[u], num[u]);
+    }
+    float nsum = 0.f;
+#pragma unroll
+    for (int u = 0; u < 8; u++) nsum += num[u];
+    s_num[j][d] = nsum;
+    __syncthreads();
+    if (tid < HD && h < gsize) {
+        float nn = 0.f, dd = 0.f;
+#pragma unroll
+        for (int i = 0; i < J; i++) nn += s_num[i][tid];
+        for (int s = 0; s < S; s++) dd += s_lw[s];
+        store_act(p.out, p.out_dtype, (size_t)b * p.nh * HD + (size_t)(g * gsize + h) * HD + tid, dd > 0.f ? nn / dd : 0.f);
+    }
+}
+
+template <int HD, int CT, int QT, int G>
+int launch_g(hipStream_t s, const AttnParams& p, int seq_len_step, size_t cache_batch_stride) {
+    dim3 grid(p.splits, p.nkv, p.batch);
+    attn_split_kernel<HD, CT, QT, G><<<grid, kBlock, 0, s>>>(p, seq_len_step, cache_batch_stride);
+    int st = launch_status("attention");
+    if (st || p.splits == 1) return st;
+    attn_merge_kernel<HD, G><<<dim3(p.nh / p.nkv, p.nkv, p.batch), kMergeBlock, 0, s>>>(p);
+    return launch_status("attention merge");
+}
+
+int group_pow2(int gsize) { return gsize <= 1 ? 1 : gsize <= 2 ? 2 : gsize <= 4 ? 4 : 8; }
+
+template <int HD, int CT, int QT>
+int launch_q(hipStream_t s, const AttnParams& p, int seq_len_step, size_t stride) {
+    switch (group_pow2(p.nh / p.nkv)) {
+    case 1: return launch_g<HD, CT, QT, 1>(s, p, seq_len_step, stride);
+    case 2: return launch_g<HD, CT, QT, 2>(s, p, seq_len_step, stride);
+    case 4: return launch_g<HD, CT, QT, 4>(s, p, seq_len_step, stride);
+    default: return launch_g<HD, CT, QT, 8>(s, p, seq_len_step, stride);
     }
 }
 
 template <int HD>
-int launch_hd(hipStream_t s, const AttnParams& p, int seq_len_step, size_t cache_batch_stride) {
-    dim3 grid(p.splits, p.nkv, p.batch);
+int launch_hd(hipStream_t s, const AttnParams& p, int seq_len_step, size_t stride) {
     if (p.cache_dtype == L0H_F16)
-        attn_decode_kernel<HD, L0H_F16><<<grid, kBlock, 0, s>>>(p, seq_len_step, cache_batch_stride);
-    else
-        attn_decode_kernel<HD, L0H_F32><<<grid, kBlock, 0, s>>>(p, seq_len_step, cache_batch_stride);
-    int st = launch_status("attention");
-    if (st) return st;
-    attn_merge_kernel<HD><<<dim3(p.nh / p.nkv, p.nkv, p.batch), kMergeBlock, 0, s>>>(p);
-    return launch_status("attention merge");
+        return p.q_dtype == L0H_F16 ? launch_q<HD, L0H_F16, L0H_F16>(s, p, seq_len_step, stride)
+                                    : launch_q<HD, L0H_F16, L0H_F32>(s, p, seq_len_step, stride);
+    return p.q_dtype == L0H_F16 ? launch_q<HD, L0H_F32, L0H_F16>(s, p, seq_len_step, stride)
+                                : launch_q<HD, L0H_F32, L0H_F32>(s, p, seq_len_step, stride);
 }
 
 int launch_any(hipStream_t s, const AttnParams& p, int seq_len_step, size_t cache_batch_stride) {
@@ -327,9 +395,13 @@ int launch_any(hipStream_t s, const AttnParams& p, int seq_len_step, size_t cach
         return fail(L0H_ERR_UNSUPPORTED, "attention needs n_heads a multiple of n_kv_heads, at most 8 per group");
     if (p.cache_dtype != L0H_F16 && p.cache_dtype != L0H_F32)
         return fail(L0H_ERR_INVALID_ARG, "cache dtype must be F16 or F32");
-    if (p.splits < 1 || (size_t)p.max_seq_len > (size_t)p.splits * kChunkMax)
-        return fail(L0H_ERR_INVALID_ARG, "too few splits for the sequence length");
-    if (!p.partials) return fail(L0H_ERR_INVALID_ARG, "attention workspace missing");
+    if (p.q_dtype != L0H_F16 && p.q_dtype != L0H_F32)
+        return fail(L0H_ERR_INVALID_ARG, "q dtype must be F16 or F32");
+    if (p.splits < 1 || p.splits > kMaxSplits) return fail(L0H_ERR_INVALID_ARG, "attention splits out of range");
+    if (p.max_seq_len < 1 || p.batch < 1) return fail(L0H_ERR_INVALID_ARG, "attention sizes must be positive");
+    if (p.splits > 1 && !p.partials) return fail(L0H_ERR_INVALID_ARG, "attention workspace missing");
+    if ((((uintptr_t)p.q | (uintptr_t)p.kc | (uintptr_t)p.vc) & 15) != 0)
+        return fail(L0H_ERR_INVALID_ARG, "attention buffers must be 16-byte aligned");
     switch (p.head_dim) {
     case 16: return launch_hd<16>(s, p, seq_len_step, cache_batch_stride);
     case 32: return launch_hd<32>(s, p, seq_len_step, cache_batch_stride);
@@ -341,14 +413,16 @@ int launch_any(hipStream_t s, const AttnParams& p, int seq_len_step, size_t cach
 }  // namespace
 
 int attention_default_splits(int batch, int nkv, int max_len, int compute_units) {
-    const int min_splits = (int)ceil_div((size_t)std::max(max_len, 1), kChunkMax);
+    // Enough blocks to cover every CU about twice, each with at least one step of positions
+    // (64 for head_dim 128); at most kMaxSplits.
     const int target = (int)ceil_div((size_t)2 * std::max(compute_units, 1), (size_t)std::max(batch * nkv, 1));
     const int by_len = (int)ceil_div((size_t)std::max(max_len, 1), 64);
-    return std::max(min_splits, std::max(1, std::min(target, by_len)));
+    return std::max(1, std::min(kMaxSplits, std::min(target, by_len)));
 }
 
 size_t attention_partials_bytes(const AttnParams& p) {
-    const int G = p.nkv > 0 ? p.nh / p.nkv : 1;
+    const int gsize = p.nkv > 0 ? p.nh / p.nkv : 1;
+    const int G = group_pow2(gsize);
     return (size_t)p.batch * p.nkv * p.splits * G * (p.head_dim + 2) * sizeof(float);
 }
 

@@ -69,7 +69,7 @@ int ensure_workspace(l0h_device* dev, size_t bytes, size_t tickets);
 
 // ---------------------------------------------------------------- dtypes --
 
-inline int dtype_size(int dt) {
+__host__ __device__ inline int dtype_size(int dt) {
     switch (dt) {
     case L0H_F32: return 4;
     case L0H_F16:

@@ -1,12 +1,24 @@
 // Weight-streaming GEMV kernels for gfx950 (decode, M = 1 .. 8 activation rows).
 //
 // Replaces LlmKernelSuite.Gemv / GemvQ8 (call sites LlmMatrix.cs:122-171, :231-241) for the
-// BASELINE weight formats. Weights are [N, K] row-major (HuggingFace [out, in]); each wave owns
-// R consecutive rows and streams them with 16-byte non-temporal loads, 64 lanes side by side
-// along K, so a wave instruction covers 1 KiB of one row. Activations are staged once per block
-// in LDS as fp32 (with the RMSNorm prologue applied there when fused), dequantisation happens in
-// registers (int8 per-row scale folded in after the reduction), accumulation is fp32, and the
-// cross-lane sum uses DPP (quad_perm, row mirrors, row_bcast15/31).
+// weight formats of this path. Weights are [N, K] row-major (HuggingFace [out, in]).
+//
+// Work: the N rows are cut into row groups of R rows and each row group's K extent into batches
+// of 64 * U chunks of 16 bytes. Wave w of the grid walks the items (row group, batch) of row
+// groups w, w + W, w + 2W, ... (W waves in the grid) in order; in an item, lane l reads chunk
+// batch * 64U + u * 64 + l of each of the R rows, so one wave instruction reads 1 KiB of one
+// row. The loads of item i+1 (its R * U weight chunks and the per-row values its epilogue needs)
+// are issued before item i is computed. Every load is unconditional: rows past N and chunks past
+// K are clamped to the last valid ones, and the activations staged in LDS are zero past K, so a
+// clamped chunk adds nothing. The load stream is therefore straight-line and the in-order memory
+// counter waits for exactly the item being computed (a conditional load, or a use of a load
+// issued after the prefetch, would make that wait cover the prefetched item too).
+//
+// Activations are staged once per block in LDS as fp32, with the RMSNorm prologue applied there
+// when fused; the prologue's own loads (x, norm weights, RoPE frequencies) are issued before the
+// first weight item. Dequantisation happens in registers (int8: bytes biased by +128 and
+// converted with v_cvt_f32_ubyteN, the bias removed after the reduction with sum(x), the per-row
+// scale applied once), accumulation is fp32, and the cross-lane sum uses DPP.
 #include <cstdlib>
 
 #include "kernels.h"
@@ -16,6 +28,8 @@ namespace {
 
 constexpr int kWaves = 4;
 constexpr int kBlock = 64 * kWaves;
+constexpr size_t kLdsBudget = 64 * 1024;  // activation tile per block
+constexpr int kMaxRotaryHalf = 128;       // cos/sin table entries per block (rotary_dim <= 256)
 
 template <int CTRL, int ROW_MASK>
 __device__ __forceinline__ float dpp_src(float v) {
@@ -103,7 +117,31 @@ __device__ __forceinline__ void chunk_fma(const uint4& w, const float* x, float&
     }
 }
 
+// The 16 bytes of an activation chunk as fp32 (4 fp32 values or 8 fp16 / bf16 values).
+__device__ __forceinline__ int chunk_to_float(const uint4& c, int dt, float* f) {
+    const uint32_t d[4] = {c.x, c.y, c.z, c.w};
+    if (dt == L0H_F32) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) f[j] = __uint_as_float(d[j]);
+        return 4;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        if (dt == L0H_F16) {
+            float2 t = __half22float2(__builtin_bit_cast(__half2, d[j]));
+            f[2 * j] = t.x;
+            f[2 * j + 1] = t.y;
+        } else {
+            f[2 * j] = __uint_as_float(d[j] << 16);
+            f[2 * j + 1] = __uint_as_float(d[j] & 0xffff0000u);
+        }
+    }
+    return 8;
+}
+
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
+
+__device__ __forceinline__ float half_bits(uint32_t b) { return __half2float(__ushort_as_half((uint16_t)b)); }
 
 __device__ __forceinline__ void store_cache(void* cache, int dt, size_t idx, float v) {
     if (dt == L0H_F16)
@@ -112,9 +150,7 @@ __device__ __forceinline__ void store_cache(void* cache, int dt, size_t idx, flo
         static_cast<float*>(cache)[idx] = v;
 }
 
-constexpr int kMaxRotaryHalf = 128;  // cos/sin table entries per block (rotary_dim <= 256)
-
-// Epilogue for the RoPE-paired rows (r0, r0+1) of the fused q|k|v matrix; cs/sn hold
+// Epilogue for the RoPE-paired rows (row, row+1) of the fused q|k|v matrix; cs/sn hold
 // cos/sin(pos * inv_freq[i]) * scale for this launch's position.
 __device__ __forceinline__ void qkv_pair(const GemvParams& p, int row, float v0, float v1, int pos,
                                          const float* cs_tab, const float* sn_tab) {
@@ -154,182 +190,209 @@ __device__ __forceinline__ void qkv_pair(const GemvParams& p, int row, float v0,
     }
 }
 
-// R rows per wave, U chunks in flight per row per lane, MR activation rows, XLDS: x staged in
-// LDS, EPI: EPI_STORE (store or residual, chosen at run time), EPI_SWIGLU or EPI_QKV.
-template <int WT, int R, int U, int MR, bool XLDS, int EPI>
-__global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p) {
+// Per-row values an item's epilogue needs, loaded with the item's weights. A lane holds the
+// values of the rows it finalises: row r0 + r for lane mr * R + r (store / residual), or rows
+// r0 + 2j and r0 + 2j + 1 for lane j (SwiGLU and q|k|v pairs). Absent operands are read from a
+// valid address and multiplied by 0, so the load count never depends on the arguments.
+struct Side {
+    uint32_t s0 = 0, s1 = 0;  // fp16 scale bits (int8 weights)
+    float b0 = 0.f, b1 = 0.f;  // bias
+    float res = 0.f;           // residual
+};
+
+template <int WT, int R, int MR, int EPI>
+__device__ __forceinline__ Side load_side(const GemvParams& p, int group, int lane, const float* any) {
+    Side sd;
+    const float has_bias = p.bias ? 1.f : 0.f;
+    if constexpr (EPI == EPI_STORE) {
+        const int r = lane % R, mr = min(lane / R, MR - 1);
+        const int row = min(group * R + r, p.n - 1);
+        if constexpr (WT == L0H_I8PC) sd.s0 = p.scales[row];
+        sd.b0 = *(p.bias ? p.bias + row : any) * has_bias;
+        sd.res = *(p.resid ? p.resid + (size_t)mr * p.n + row : any) * (p.resid ? 1.f : 0.f);
+    } else {
+        const int j = min(lane, R / 2 - 1);
+        const int row = min(group * R + 2 * j, p.n - 2);
+        if constexpr (WT == L0H_I8PC) {
+            sd.s0 = p.scales[row];
+            sd.s1 = p.scales[row + 1];
+        }
+        sd.b0 = *(p.bias ? p.bias + row : any) * has_bias;
+        sd.b1 = *(p.bias ? p.bias + row + 1 : any) * has_bias;
+    }
+    return sd;
+}
+
+// WT weight type, R rows per wave item, U chunks per row per lane in an item, MR activation
+// rows, KX 16-byte activation chunks staged per thread (MR == 1), NORM: RMSNorm prologue,
+// EPI: EPI_STORE (store or residual, chosen at run time), EPI_SWIGLU or EPI_QKV.
+template <int WT, int R, int U, int MR, int KX, bool NORM, int EPI>
+__global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p, int k_pad) {
     extern __shared__ float4 smem4[];
-    float* xs = reinterpret_cast<float*>(smem4);  // [MR, K] when XLDS
+    float* xs = reinterpret_cast<float*>(smem4);  // [MR, k_pad], zero past K
     __shared__ float red[kWaves];
     __shared__ float xsum_s[MR];
     __shared__ float rope_cs[EPI == EPI_QKV ? kMaxRotaryHalf : 1];
     __shared__ float rope_sn[EPI == EPI_QKV ? kMaxRotaryHalf : 1];
-    int pos = 0;
     constexpr int EPC = WTraits<WT>::kElems;
+    constexpr int KB = 64 * U;  // chunks per batch
     const int K = p.k, N = p.n;
     const int C = K / EPC;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    // Persistent waves: wave w of block b owns row groups (b * kWaves + w) + i * (all waves).
-    const int wave_stride = gridDim.x * kWaves * R;
-    int row0 = (blockIdx.x * kWaves + wave) * R;
+    const int nb = (C + KB - 1) / KB;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar control flow
+    const int W = gridDim.x * kWaves;
+    const int ngroups = (N + R - 1) / R;
+    const char* wbase = static_cast<const char*>(p.w);
+    const size_t row_bytes = (size_t)K * WTraits<WT>::kBytes;
+    const float* any = static_cast<const float*>(p.x);
 
-    auto row_ptr = [&](int row) {
-        return reinterpret_cast<const uint4*>(static_cast<const char*>(p.w) +
-                                              (size_t)min(row, N - 1) * K * WTraits<WT>::kBytes);
-    };
-    uint4 wa[U][R], wb[U][R];  // double buffer: item i computes from one while item i+1 loads
-    auto load_into = [&](uint4 (&w)[U][R], int r0, int c0) {
+    auto load_w = [&](uint4 (&w)[U][R], int group, int batch) {
+        const int grp = min(group, ngroups - 1);
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-            const int c = c0 + 64 * u;
+        for (int r = 0; r < R; r++) {
+            const uint4* rp = reinterpret_cast<const uint4*>(wbase + (size_t)min(grp * R + r, N - 1) * row_bytes);
 #pragma unroll
-            for (int r = 0; r < R; r++) w[u][r] = c < C ? ld_nt16(row_ptr(r0 + r) + c) : make_uint4(0u, 0u, 0u, 0u);
+            for (int u = 0; u < U; u++) w[u][r] = ld_nt16(rp + min(batch * KB + u * 64 + lane, C - 1));
         }
     };
-    const int nb = (C + 64 * U - 1) / (64 * U);  // batches per row group, the same for every lane
-    // The first batch of weight loads goes out before the activations are staged, so the
-    // prologue overlaps their HBM latency.
-    // Per-row values the epilogue needs (int8 scale, bias, residual), fetched with the row group's
-    // first weight batch so the epilogue issues no dependent global load. A lane holds the values
-    // of the rows it finalizes: row r0 + r for lane mr * R + r (store / residual), or rows
-    // r0 + 2j and r0 + 2j + 1 for lane j (SwiGLU and q|k|v pairs).
-    struct Side {
-        float s0 = 1.f, s1 = 1.f, b0 = 0.f, b1 = 0.f, res = 0.f;
-    };
-    auto load_side = [&](int r0) {
-        Side sd;
-        if constexpr (EPI == EPI_STORE) {
-            const int r = lane % R, mr = lane / R;
-            if (mr < MR) {
-                const int row = min(r0 + r, N - 1);
-                if constexpr (WT == L0H_I8PC) sd.s0 = __half2float(__ushort_as_half(p.scales[row]));
-                if (p.bias) sd.b0 = p.bias[row];
-                if (p.epilogue == EPI_RESIDUAL) sd.res = p.resid[(size_t)mr * N + row];
-            }
-        } else if (lane < R / 2) {
-            const int row = min(r0 + 2 * lane, N - 2);
-            if constexpr (WT == L0H_I8PC) {
-                sd.s0 = __half2float(__ushort_as_half(p.scales[row]));
-                sd.s1 = __half2float(__ushort_as_half(p.scales[row + 1]));
-            }
-            if (p.bias) {
-                sd.b0 = p.bias[row];
-                sd.b1 = p.bias[row + 1];
-            }
-        }
-        return sd;
-    };
-    Side side_cur, side_next;
-    if (row0 < N) {
-        load_into(wa, row0, lane);
-        side_cur = load_side(row0);
-    }
 
-    if constexpr (EPI == EPI_QKV) {
-        pos = *p.position;
-        // cos/sin of this position for every rotated pair, once per block (accurate sincos of
-        // the fp32 product pos * inv_freq[i]); published by the staging barrier below.
-        for (int i = threadIdx.x; i < p.rotary_dim / 2; i += kBlock) {
-            float sn, cs;
-            sincosf((float)pos * p.inv_freq[i], &sn, &cs);
-            rope_cs[i] = cs * p.rope_scale;
-            rope_sn[i] = sn * p.rope_scale;
-        }
-    }
-
-    // Stage activations (and RMSNorm) in LDS.
-    if constexpr (XLDS) {
+    // ---- several activation rows: staged before any weight load (not the decode path) ----
+    if constexpr (MR > 1) {
 #pragma unroll
         for (int mr = 0; mr < MR; mr++) {
-            float* dst = xs + (size_t)mr * K;
-            float ss = 0.f;
-            if (p.x_dtype == L0H_F32) {
-                const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(p.x) + (size_t)mr * K);
-                for (int i = threadIdx.x; i < K / 4; i += kBlock) {
-                    float4 v = src[i];
-                    reinterpret_cast<float4*>(dst)[i] = v;
-                    ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-                }
-            } else {
-                for (int i = threadIdx.x; i < K; i += kBlock) {
-                    float v = load_act(p.x, p.x_dtype, (size_t)mr * K + i);
-                    dst[i] = v;
-                    ss += v * v;
-                }
-            }
-            __syncthreads();  // other threads read these LDS elements below
-            float scale = 1.f;
-            if (p.norm_w) {
-                ss = block_sum(ss, red);
-                scale = rsqrtf(ss / (float)K + p.eps);
-            }
+            float* dst = xs + (size_t)mr * k_pad;
             float xsum = 0.f;
-            if (p.norm_w || WT == L0H_I8PC) {
-                for (int i = threadIdx.x; i < K; i += kBlock) {
-                    float v = dst[i];
-                    if (p.norm_w) {
-                        v = v * scale * p.norm_w[i];
-                        dst[i] = v;
-                    }
-                    xsum += v;
-                }
+            for (int i = tid; i < k_pad; i += kBlock) {
+                const float v = i < K ? load_act(p.x, p.x_dtype, (size_t)mr * K + i) : 0.f;
+                dst[i] = v;
+                xsum += v;
             }
             if constexpr (WT == L0H_I8PC) {
                 xsum = block_sum(xsum, red);
-                if (threadIdx.x == 0) xsum_s[mr] = xsum;
+                if (tid == 0) xsum_s[mr] = xsum;
             }
-        }
-        __syncthreads();
-    } else {
-        if constexpr (WT == L0H_I8PC) {
-#pragma unroll
-            for (int mr = 0; mr < MR; mr++) {
-                const float* src = static_cast<const float*>(p.x) + (size_t)mr * K;
-                float xsum = 0.f;
-                for (int i = threadIdx.x; i < K; i += kBlock) xsum += src[i];
-                xsum = block_sum(xsum, red);
-                if (threadIdx.x == 0) xsum_s[mr] = xsum;
-            }
-            __syncthreads();
         }
     }
-    const float* xg = static_cast<const float*>(p.x);
-    // Pipelined stream over this wave's (row group, batch) items: the loads of item i+1 are issued
-    // before item i is computed, across row-group boundaries, so every HBM round trip overlaps
-    // compute. No barrier below this point: waves run independently.
+
+    // ---- one activation row: prologue loads first (x, norm weights, RoPE frequencies) ----
+    uint4 xr[KX], nr[NORM ? KX : 1];
+    const int xdt = p.x_dtype;
+    const int nxc = (int)((size_t)K * dtype_size(xdt) / 16);  // 16-byte chunks of x
+    if constexpr (MR == 1) {
+        const uint4* xp = static_cast<const uint4*>(p.x);
+#pragma unroll
+        for (int i = 0; i < KX; i++) xr[i] = xp[min(i * kBlock + tid, nxc - 1)];
+        if constexpr (NORM) {
+            const uint4* np = reinterpret_cast<const uint4*>(p.norm_w);
+#pragma unroll
+            for (int i = 0; i < KX; i++) nr[i] = np[min(i * kBlock + tid, K / 4 - 1)];
+        }
+    }
+    float inv_f = 0.f;
+    int pos = 0;
+    if constexpr (EPI == EPI_QKV) {
+        inv_f = p.inv_freq[min(tid, p.rotary_dim / 2 - 1)];
+        pos = *p.position;
+    }
+
+    // ---- first weight item ----
+    int g = blockIdx.x * kWaves + wave;
+    uint4 wa[U][R], wb[U][R];
+    Side sa, sb;
+    sa = load_side<WT, R, MR, EPI>(p, min(g, ngroups - 1), lane, any);
+    load_w(wa, g, 0);
+
+    // ---- stage the one activation row (and RMSNorm) in LDS while the weights are in flight ----
+    if constexpr (MR == 1) {
+        float scale = 1.f;
+        if constexpr (NORM) {
+            float ss = 0.f;
+#pragma unroll
+            for (int i = 0; i < KX; i++) {
+                float f[8];
+                const int n = chunk_to_float(xr[i], xdt, f);
+                if (i * kBlock + tid < nxc) {
+#pragma unroll
+                    for (int e = 0; e < 8; e++)
+                        if (e < n) ss += f[e] * f[e];
+                }
+            }
+            ss = block_sum(ss, red);
+            scale = rsqrtf(ss / (float)K + p.eps);
+        }
+        float xsum = 0.f;
+#pragma unroll
+        for (int i = 0; i < KX; i++) {
+            const int idx = i * kBlock + tid;
+            if (idx < nxc) {
+                float f[8];
+                const int n = chunk_to_float(xr[i], xdt, f);
+                if constexpr (NORM) {  // x is fp32 here: 4 values, matching the 4 norm weights
+                    f[0] *= scale * __uint_as_float(nr[i].x);
+                    f[1] *= scale * __uint_as_float(nr[i].y);
+                    f[2] *= scale * __uint_as_float(nr[i].z);
+                    f[3] *= scale * __uint_as_float(nr[i].w);
+                }
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    if (e < n) {
+                        xs[idx * n + e] = f[e];
+                        xsum += f[e];
+                    }
+                }
+            }
+        }
+        for (int i = K + tid; i < k_pad; i += kBlock) xs[i] = 0.f;
+        if constexpr (WT == L0H_I8PC) {
+            xsum = block_sum(xsum, red);
+            if (tid == 0) xsum_s[0] = xsum;
+        }
+    }
+    if constexpr (EPI == EPI_QKV) {
+        // cos/sin of this position for every rotated pair, once per block (accurate sincos of
+        // the fp32 product pos * inv_freq[i]).
+        if (tid < p.rotary_dim / 2) {
+            float sn, cs;
+            sincosf((float)pos * inv_f, &sn, &cs);
+            rope_cs[tid] = cs * p.rope_scale;
+            rope_sn[tid] = sn * p.rope_scale;
+        }
+    }
+    __syncthreads();
+
+    // ---- stream: no barrier below this point, waves run independently ----
     float acc[MR][R];
 #pragma unroll
     for (int mr = 0; mr < MR; mr++)
 #pragma unroll
         for (int r = 0; r < R; r++) acc[mr][r] = 0.f;
 
-    auto compute = [&](const uint4 (&w)[U][R], int c0) {
+    auto compute = [&](const uint4 (&w)[U][R], int batch) {
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const int c = c0 + 64 * u;
-            if (c < C) {
+            const int c = batch * KB + u * 64 + lane;  // < nb * KB: x is zero past K
 #pragma unroll
-                for (int mr = 0; mr < MR; mr++) {
-                    float xv[EPC];
-                    const float4* xp = reinterpret_cast<const float4*>(
-                        (XLDS ? xs : xg) + (size_t)mr * K + (size_t)c * EPC);
+            for (int mr = 0; mr < MR; mr++) {
+                float xv[EPC];
+                const float4* xp = reinterpret_cast<const float4*>(xs + (size_t)mr * k_pad + (size_t)c * EPC);
 #pragma unroll
-                    for (int q = 0; q < EPC / 4; q++) {
-                        float4 t = xp[q];
-                        xv[4 * q + 0] = t.x;
-                        xv[4 * q + 1] = t.y;
-                        xv[4 * q + 2] = t.z;
-                        xv[4 * q + 3] = t.w;
-                    }
-#pragma unroll
-                    for (int r = 0; r < R; r++) chunk_fma<WT>(w[u][r], xv, acc[mr][r]);
+                for (int q = 0; q < EPC / 4; q++) {
+                    float4 t = xp[q];
+                    xv[4 * q + 0] = t.x;
+                    xv[4 * q + 1] = t.y;
+                    xv[4 * q + 2] = t.z;
+                    xv[4 * q + 3] = t.w;
                 }
+#pragma unroll
+                for (int r = 0; r < R; r++) chunk_fma<WT>(w[u][r], xv, acc[mr][r]);
             }
         }
     };
 
-    // Wave reduction and epilogue of the row group starting at r0; resets the accumulators.
-    auto finish = [&](int r0, const Side& sd) {
+    // Wave reduction and epilogue of row group `group`; resets the accumulators. No loads.
+    auto finish = [&](int group, const Side& sd) {
+        const int r0 = group * R;
         float sums[MR][R];
 #pragma unroll
         for (int mr = 0; mr < MR; mr++)
@@ -346,7 +409,7 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p) {
                     const int row = r0 + r;
                     if (lane == mr * R + r && row < N) {
                         float v = sums[mr][r];
-                        if constexpr (WT == L0H_I8PC) v = (v - 128.0f * xsum_s[mr]) * sd.s0;
+                        if constexpr (WT == L0H_I8PC) v = (v - 128.0f * xsum_s[mr]) * half_bits(sd.s0);
                         v += sd.b0;
                         if (p.epilogue == EPI_STORE)
                             store_act(p.y, p.y_dtype, (size_t)mr * N + row, v);
@@ -361,8 +424,8 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p) {
                 if (lane == j && row + 1 < N) {
                     float v0 = sums[0][2 * j], v1 = sums[0][2 * j + 1];
                     if constexpr (WT == L0H_I8PC) {
-                        v0 = (v0 - 128.0f * xsum_s[0]) * sd.s0;
-                        v1 = (v1 - 128.0f * xsum_s[0]) * sd.s1;
+                        v0 = (v0 - 128.0f * xsum_s[0]) * half_bits(sd.s0);
+                        v1 = (v1 - 128.0f * xsum_s[0]) * half_bits(sd.s1);
                     }
                     v0 += sd.b0;
                     v1 += sd.b1;
@@ -375,29 +438,54 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p) {
         }
     };
 
-    int b = 0;  // batch of the current row group
-    auto step = [&](uint4 (&cur)[U][R], uint4 (&nxt)[U][R]) -> bool {
-        int n_row0 = row0, n_b = b + 1;
-        if (n_b == nb) {
-            n_b = 0;
-            n_row0 += wave_stride;
+    // Items of this wave: every batch of row groups g, g + W, ... < ngroups. Each pipeline step
+    // issues item i+1 into the other buffer, then computes item i and finishes its row group after
+    // its last batch; the last item is computed with nothing issued behind it (no re-read past the
+    // end). The branch to the last item comes before any load of its step, so the two paths never
+    // merge between a load and its use.
+    const int items = g < ngroups ? ((ngroups - 1 - g) / W + 1) * nb : 0;
+    int b = 0;  // batch of the current item
+    auto advance = [&](int& gg, int& bb) {
+        if (++bb == nb) {
+            bb = 0;
+            gg += W;
         }
-        const bool more = n_row0 < N;
-        if (more) {
-            load_into(nxt, n_row0, lane + 64 * U * n_b);
-            if (n_b == 0) side_next = load_side(n_row0);
-        }
-        compute(cur, lane + 64 * U * b);
-        if (b == nb - 1) {
-            finish(row0, side_cur);
-            side_cur = side_next;
-        }
-        row0 = n_row0;
-        b = n_b;
-        return more;
     };
-    if (row0 < N) {
-        while (step(wa, wb) && step(wb, wa)) {
+    if (items > 0) {
+        int i = 0;
+        for (;;) {
+            if (i + 1 == items) {
+                compute(wa, b);
+                finish(g, sa);
+                break;
+            }
+            {
+                int gn = g, bn = b;
+                advance(gn, bn);
+                sb = load_side<WT, R, MR, EPI>(p, gn, lane, any);
+                load_w(wb, gn, bn);
+                compute(wa, b);
+                if (b == nb - 1) finish(g, sa);
+                g = gn;
+                b = bn;
+                i++;
+            }
+            if (i + 1 == items) {
+                compute(wb, b);
+                finish(g, sb);
+                break;
+            }
+            {
+                int gn = g, bn = b;
+                advance(gn, bn);
+                sa = load_side<WT, R, MR, EPI>(p, gn, lane, any);
+                load_w(wa, gn, bn);
+                compute(wb, b);
+                if (b == nb - 1) finish(g, sb);
+                g = gn;
+                b = bn;
+                i++;
+            }
         }
     }
 }
@@ -432,46 +520,72 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_generic_kernel(const GemvParam
     }
 }
 
-template <int WT, int R, int U, int MR, bool XLDS, int EPI = EPI_STORE>
+// Zero-padded activation tile of the fast kernel: K rounded up to whole batches.
+template <int WT, int U>
+int padded_k(int k) {
+    constexpr int EPC = WTraits<WT>::kElems, KB = 64 * U;
+    const int nb = (k / EPC + KB - 1) / KB;
+    return nb * KB * EPC;
+}
+
+template <int WT, int R, int U, int MR, int KX, bool NORM, int EPI>
 int launch_fast(hipStream_t s, const GemvParams& p) {
-    const unsigned rows_per_block = kWaves * R;
-    unsigned grid = ceil_div(p.n, rows_per_block);
+    const int k_pad = padded_k<WT, U>(p.k);
+    const size_t shmem = (size_t)MR * k_pad * sizeof(float);
+    if (shmem > kLdsBudget) return fail(L0H_ERR_UNSUPPORTED, "GEMV activation tile exceeds LDS");
+    auto kern = gemv_nk_kernel<WT, R, U, MR, KX, NORM, EPI>;
+    // The dynamic tile may reach 64 KiB on top of the static LDS: raise the limit once.
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsBudget);
+    if (attr != hipSuccess) return fail(L0H_ERR_DEVICE, std::string("hipFuncSetAttribute: ") + hipGetErrorString(attr));
+    const unsigned groups = ceil_div(p.n, R);
+    unsigned grid = ceil_div(groups, kWaves);
     if (p.max_blocks > 0) grid = std::min<unsigned>(grid, (unsigned)p.max_blocks);
-    const size_t shmem = XLDS ? (size_t)MR * p.k * sizeof(float) : 0;
-    auto kern = gemv_nk_kernel<WT, R, U, MR, XLDS, EPI>;
-    if (shmem > 64 * 1024) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem);
-        if (e != hipSuccess) return fail(L0H_ERR_UNSUPPORTED, "GEMV activation tile exceeds LDS");
-    }
-    kern<<<grid, kBlock, shmem, s>>>(p);
+    kern<<<grid, kBlock, shmem, s>>>(p, k_pad);
     return launch_status("gemv_nk");
 }
 
-constexpr size_t kLdsBudget = 64 * 1024;
-
-// One activation row with x in LDS: the fused epilogues live here.
-template <int WT, int R, int U>
+// One activation row: the fused epilogues and the RMSNorm prologue live here.
+template <int WT, int R, int U, int KX>
 int dispatch_one(hipStream_t s, const GemvParams& p) {
     switch (p.epilogue) {
-    case EPI_SWIGLU: return launch_fast<WT, R, U, 1, true, EPI_SWIGLU>(s, p);
-    case EPI_QKV: return launch_fast<WT, R, U, 1, true, EPI_QKV>(s, p);
-    default: return launch_fast<WT, R, U, 1, true, EPI_STORE>(s, p);
+    case EPI_SWIGLU: return launch_fast<WT, R, U, 1, KX, true, EPI_SWIGLU>(s, p);
+    case EPI_QKV: return launch_fast<WT, R, U, 1, KX, true, EPI_QKV>(s, p);
+    default:
+        return p.norm_w ? launch_fast<WT, R, U, 1, KX, true, EPI_STORE>(s, p)
+                        : launch_fast<WT, R, U, 1, KX, false, EPI_STORE>(s, p);
     }
+}
+
+// Activation chunks per thread of a 256-thread block, rounded up to a power of two (<= 16).
+int staged_chunks(const GemvParams& p) {
+    const size_t chunks = (size_t)p.k * dtype_size(p.x_dtype) / 16;
+    const size_t per = (chunks + kBlock - 1) / kBlock;
+    int kx = 1;
+    while ((size_t)kx < per) kx <<= 1;
+    return kx;
 }
 
 template <int WT, int R, int U>
 int dispatch_mr(hipStream_t s, const GemvParams& p, int mr) {
-    const bool fits = (size_t)mr * p.k * sizeof(float) <= kLdsBudget;
-    if (mr == 1) return fits ? dispatch_one<WT, R, U>(s, p) : launch_fast<WT, R, U, 1, false>(s, p);
-    if (mr == 2) return fits ? launch_fast<WT, R, U, 2, true>(s, p) : launch_fast<WT, R, U, 2, false>(s, p);
-    if (mr == 4) return fits ? launch_fast<WT, R, U, 4, true>(s, p) : launch_fast<WT, R, U, 4, false>(s, p);
-    return fits ? launch_fast<WT, R, U, 8, true>(s, p) : launch_fast<WT, R, U, 8, false>(s, p);
+    if (mr == 1) {
+        switch (staged_chunks(p)) {
+        case 1: return dispatch_one<WT, R, U, 1>(s, p);
+        case 2: return dispatch_one<WT, R, U, 2>(s, p);
+        case 4: return dispatch_one<WT, R, U, 4>(s, p);
+        case 8: return dispatch_one<WT, R, U, 8>(s, p);
+        case 16: return dispatch_one<WT, R, U, 16>(s, p);
+        default: return fail(L0H_ERR_UNSUPPORTED, "GEMV activation row exceeds 64 KiB");
+        }
+    }
+    if (mr == 2) return launch_fast<WT, R, U, 2, 1, false, EPI_STORE>(s, p);
+    if (mr == 4) return launch_fast<WT, R, U, 4, 1, false, EPI_STORE>(s, p);
+    return launch_fast<WT, R, U, 8, 1, false, EPI_STORE>(s, p);
 }
 
-// Rows per wave (R) and 16-byte chunks in flight per row per lane (U) for the one-row int8
-// kernel: R * U loads of 1 KiB per wave are outstanding. L0H_GEMV_RU="RU" selects another
-// instantiation (for tuning sweeps); the default is the measured best.
+// Rows per wave item (R) and 16-byte chunks per row per lane (U) of the one-row int8 kernel:
+// R * U KiB per wave item. L0H_GEMV_RU="RU" selects another instantiation for tuning sweeps;
+// the default is the measured best.
 int int8_ru_choice() {
     static const int v = [] {
         const char* e = std::getenv("L0H_GEMV_RU");
@@ -483,26 +597,22 @@ int int8_ru_choice() {
 template <int WT>
 int dispatch_wt(hipStream_t s, const GemvParams& p, int mr) {
     if constexpr (WT == L0H_I8PC) {
-        if (mr == 1 && (size_t)p.k * sizeof(float) <= kLdsBudget) {
+        if (mr == 1) {
             switch (int8_ru_choice()) {
-            case 22: return dispatch_one<WT, 2, 2>(s, p);
-            case 42: return dispatch_one<WT, 4, 2>(s, p);
-            case 44: return dispatch_one<WT, 4, 4>(s, p);
-            case 82: return dispatch_one<WT, 8, 2>(s, p);
+            case 42: return dispatch_mr<WT, 4, 2>(s, p, mr);
+            case 28: return dispatch_mr<WT, 2, 8>(s, p, mr);
+            case 44: return dispatch_mr<WT, 4, 4>(s, p, mr);
             default: break;
             }
         }
     }
-    // Rows per wave and chunks in flight, chosen per weight width.
-    // (R, U) = (2, 4): 2 rows per wave, 4 x 1 KiB loads per row in flight, double-buffered
-    // (the fastest of the measured shapes at the Llama-3.1-8B decode sizes).
     return dispatch_mr<WT, 2, 4>(s, p, mr);
 }
 
 }  // namespace
 
 int gemv_max_blocks(int compute_units) {
-    // L0H_GEMV_BLOCKS_PER_CU overrides the default (0: one block per row group, no cap).
+    // L0H_GEMV_BLOCKS_PER_CU overrides the default (0: one block per 4 row groups, no cap).
     static const int per_cu = [] {
         const char* e = std::getenv("L0H_GEMV_BLOCKS_PER_CU");
         const int v = e ? std::atoi(e) : 4;
@@ -512,48 +622,53 @@ int gemv_max_blocks(int compute_units) {
 }
 
 int launch_gemv_nk(hipStream_t s, const GemvParams& p0) {
-    const int epc = p0.w_dtype == L0H_I8PC ? 16 : (p0.w_dtype == L0H_F32 ? 4 : 8);
-    const bool fused = p0.epilogue == EPI_SWIGLU || p0.epilogue == EPI_QKV || p0.norm_w;
-    const bool aligned = p0.k % epc == 0 && ((uintptr_t)p0.w & 15) == 0 &&
-                         (p0.x_dtype != L0H_F32 || ((uintptr_t)p0.x & 15) == 0);
     if (p0.n <= 0 || p0.k <= 0 || p0.m <= 0) return fail(L0H_ERR_INVALID_ARG, "GEMV sizes must be positive");
-    if (fused && (!aligned || p0.m != 1 || (size_t)p0.k * 4 > kLdsBudget))
-        return fail(L0H_ERR_UNSUPPORTED, "fused GEMV needs one row, K a multiple of the load width and K*4 <= 64 KiB");
-    if (!aligned || (p0.x_dtype != L0H_F32 && (size_t)p0.k * 4 > kLdsBudget)) {
+    const int epc = p0.w_dtype == L0H_I8PC ? 16 : (p0.w_dtype == L0H_F32 ? 4 : 8);
+    const int xsize = dtype_size(p0.x_dtype);
+    const bool fused = p0.epilogue == EPI_SWIGLU || p0.epilogue == EPI_QKV || p0.norm_w;
+    // Fast path: whole 16-byte weight chunks, aligned rows, and activation rows that fit the
+    // zero-padded LDS tile (padding up to 64 * 4 chunks of the weight row).
+    const size_t k_pad_max = (size_t)((p0.k / epc + 255) / 256) * 256 * epc;
+    const bool aligned = p0.k % epc == 0 && ((uintptr_t)p0.w & 15) == 0 && ((uintptr_t)p0.x & 15) == 0 &&
+                         ((uintptr_t)p0.norm_w & 15) == 0 && ((size_t)p0.k * xsize) % 16 == 0;
+    const bool pairs = p0.epilogue == EPI_SWIGLU || p0.epilogue == EPI_QKV;
+    if (pairs && p0.n % 2) return fail(L0H_ERR_INVALID_ARG, "paired-row epilogues need an even row count");
+    const bool fits = k_pad_max * sizeof(float) <= kLdsBudget;
+    if (fused) {
+        if (!aligned || !fits || p0.m != 1 || p0.x_dtype != L0H_F32 || (p0.epilogue != EPI_STORE && !p0.norm_w) ||
+            (p0.epilogue == EPI_QKV && (p0.rotary_dim > 2 * kMaxRotaryHalf || p0.rotary_dim < 2)))
+            return fail(L0H_ERR_UNSUPPORTED,
+                        "fused GEMV needs one fp32 activation row with the RMSNorm prologue, K a multiple of the "
+                        "load width and a zero-padded row of at most 64 KiB");
+    }
+    if (!aligned || !fits) {
         if (fused) return fail(L0H_ERR_UNSUPPORTED, "fused GEMV shape not supported");
         GemvParams p = p0;
         const size_t tasks = (size_t)p.m * p.n;
         gemv_nk_generic_kernel<<<ceil_div(tasks, kWaves), kBlock, 0, s>>>(p);
         return launch_status("gemv_nk_generic");
     }
-    // Activation rows in groups of 8/4/2/1 (each group reads W once).
+    // Activation rows in groups of 8/4/2/1 (each group reads W once), as many as fit the tile.
     int done = 0;
     while (done < p0.m) {
         const int left = p0.m - done;
-        const int mr = left >= 8 ? 8 : left >= 4 ? 4 : left >= 2 ? 2 : 1;
+        int mr = left >= 8 ? 8 : left >= 4 ? 4 : left >= 2 ? 2 : 1;
+        while (mr > 1 && (size_t)mr * k_pad_max * sizeof(float) > kLdsBudget) mr >>= 1;
         GemvParams p = p0;
         p.m = mr;
-        const bool need_lds = p.x_dtype != L0H_F32;
-        if (need_lds && (size_t)mr * p.k * 4 > kLdsBudget && mr > 1) {
-            // activations that must be converted have to fit LDS: take a smaller group
-            int smaller = mr;
-            while (smaller > 1 && (size_t)smaller * p.k * 4 > kLdsBudget) smaller >>= 1;
-            p.m = smaller;
-        }
-        const size_t xsz = (size_t)dtype_size(p.x_dtype);
-        p.x = static_cast<const char*>(p0.x) + (size_t)done * p.k * xsz;
+        p.x = static_cast<const char*>(p0.x) + (size_t)done * p.k * xsize;
         if (p.y) p.y = static_cast<char*>(p0.y) + (size_t)done * p.n * dtype_size(p.y_dtype);
         if (p.resid) p.resid = p0.resid + (size_t)done * p.n;
         int st;
         switch (p.w_dtype) {
-        case L0H_I8PC: st = dispatch_wt<L0H_I8PC>(s, p, p.m); break;
-        case L0H_F16: st = dispatch_wt<L0H_F16>(s, p, p.m); break;
-        case L0H_BF16: st = dispatch_wt<L0H_BF16>(s, p, p.m); break;
-        case L0H_F32: st = dispatch_wt<L0H_F32>(s, p, p.m); break;
+        case L0H_I8PC: st = dispatch_wt<L0H_I8PC>(s, p, mr); break;
+        case L0H_F16: st = dispatch_wt<L0H_F16>(s, p, mr); break;
+        case L0H_BF16: st = dispatch_wt<L0H_BF16>(s, p, mr); break;
+        case L0H_F32: st = dispatch_wt<L0H_F32>(s, p, mr); break;
         default: return fail(L0H_ERR_INVALID_ARG, "unknown weight dtype");
         }
         if (st) return st;
-        done += p.m;
+        done += mr;
     }
     return L0H_OK;
 }
