@@ -83,6 +83,140 @@ def hbm_copy_probe(dev, mib: int = 1024, reps: int = 10) -> dict:
                 gbs=round(8 * n / dt / 1e9, 1))
 
 
+COLD_BYTES = 640 << 20  # replicas per timed pass: well past the 256 MB Infinity Cache
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def _replicated(dev, block: np.ndarray, nbytes_each: int, count: int):
+    """One device buffer holding `count` replicas of a `nbytes_each`-byte operand, filled by
+    tiling `block` (the data only has to be finite; distinct addresses keep the cache cold)."""
+    import l0llm_amd as l0
+
+    raw = np.ascontiguousarray(block).view(np.uint8).reshape(-1)
+    one = np.resize(raw, nbytes_each)
+    buf = dev.alloc(nbytes_each * count)
+    buf.write(one)
+    suite = l0.LlmKernelSuite(dev)
+    done = 1
+    while done < count:  # doubling device copies
+        n = min(done, count - done)
+        suite.copy_execute(buf.ptr, buf.ptr + done * nbytes_each, 0, n * nbytes_each // 4)
+        done += n
+    dev.synchronize()
+    return buf
+
+
+def _replay_us(dev, enqueue, launches: int, reps: int = 5) -> float:
+    """Records `enqueue` (which issues `launches` kernels) as one command list, runs it once, then
+    replays it back to back: mean device microseconds per launch."""
+    dev.begin_recording()
+    try:
+        enqueue()
+    except Exception:
+        dev.abort_recording()
+        raise
+    dev.end_recording()
+    return dev.replay_recording(reps) * 1e3 / launches
+
+
+def measure_configs(dev) -> dict:
+    """The other workloads of the path, timed on the device (cold weights / KV, graph replay of
+    back-to-back launches): int8 GEMV 896->4864 with fp16 I/O; the Qwen2.5-0.5B decode linears
+    in int8 and fp16; the Llama-3.2-1B prefill GEMMs in bf16 on MFMA; GQA decode attention."""
+    import l0llm_amd as l0
+
+    suite = l0.LlmKernelSuite(dev)
+    rng = np.random.default_rng(7)
+    out = {}
+
+    def gemv_case(name, wdt, n, k, x_dt=l0.F16, y_dt=l0.F16):
+        wsize = 1 if wdt == l0.I8PC else 2
+        wbytes = n * k * wsize
+        reps = max(2, min(512, -(-COLD_BYTES // wbytes)))
+        if wdt == l0.I8PC:
+            wblock = rng.integers(-127, 128, size=min(n * k, 1 << 22), dtype=np.int8)
+        else:
+            wblock = (rng.standard_normal(min(n * k, 1 << 22), dtype=np.float32) * 0.02).astype(np.float16)
+        w = _replicated(dev, wblock, wbytes, reps)
+        sblock = rng.uniform(1e-3, 1e-2, n).astype(np.float16)
+        sc = _replicated(dev, sblock, 2 * n, reps) if wdt == l0.I8PC else None
+        x = dev.alloc_shared(rng.standard_normal(k).astype(np.float16 if x_dt == l0.F16 else np.float32))
+        y = dev.alloc(n * 4)
+
+        def run(count, cold=True):
+            for i in range(count):
+                j = i % reps if cold else 0
+                suite.gemv_nk(wdt, 1, n, k, x, x_dt, w.ptr + j * wbytes, None if sc is None else sc.ptr + j * 2 * n,
+                              y, y_dt)
+
+        cold_us = _replay_us(dev, lambda: run(reps), reps)
+        hot_us = _replay_us(dev, lambda: run(64, cold=False), 64)
+        xb = 2 if x_dt == l0.F16 else 4
+        nbytes = wbytes + (2 * n if wdt == l0.I8PC else 0) + k * xb + n * (2 if y_dt == l0.F16 else 4)
+        for b in (w, sc, x, y):
+            if b is not None:
+                b.free()
+        out[name] = dict(n=n, k=k, w="int8-per-row" if wdt == l0.I8PC else "fp16", bytes=nbytes,
+                         us=round(cold_us, 3), gbs=round(nbytes / cold_us / 1e3, 1),
+                         frac=round(nbytes / cold_us / 1e3 / HBM_PEAK_GBS, 4), hot_us=round(hot_us, 3))
+
+    # int8 GEMV 896 -> 4864, fp16 activations in and out (Qwen2.5-0.5B up-proj shape)
+    gemv_case("int8_gemv_896x4864_fp16io", l0.I8PC, 4864, 896)
+    # Qwen2.5-0.5B decode linears, M = 1 (gate|up measured as one 896 -> 9728 GEMV)
+    for wdt, tag in ((l0.I8PC, "int8"), (l0.F16, "fp16")):
+        for name, n, k in (("qkv", 1152, 896), ("o", 896, 896), ("gate_up", 9728, 896), ("down", 896, 4864),
+                           ("lm_head", 151936, 896)):
+            gemv_case(f"qwen05b_{tag}_{name}", wdt, n, k)
+
+    # Llama-3.2-1B prefill GEMMs, bf16 operands, fp32 accumulation on MFMA, bf16 out
+    for m in (128, 512):
+        for name, n, k in (("qkv", 3072, 2048), ("o", 2048, 2048), ("gate_up", 16384, 2048), ("down", 2048, 8192)):
+            wbytes = 2 * n * k
+            reps = max(2, min(64, -(-COLD_BYTES // wbytes)))
+            wblock = (rng.standard_normal(1 << 22, dtype=np.float32) * 0.02).astype(np.float16)
+            w = _replicated(dev, wblock, wbytes, reps)  # bf16 bits from fp16 bits: finite values suffice
+            x = dev.alloc_shared(rng.standard_normal(m * k).astype(np.float16))
+            y = dev.alloc(2 * m * n)
+            suite.gemm_nk(l0.BF16, m, n, k, x, w, y, l0.BF16)  # sizes the split-K workspace before recording
+            us = _replay_us(dev, lambda: [suite.gemm_nk(l0.BF16, m, n, k, x, w.ptr + i * wbytes, y, l0.BF16)
+                                          for i in range(reps)], reps)
+            flops = 2.0 * m * n * k
+            nbytes = 2 * (k * n + m * k + m * n)
+            tf = flops / us / 1e6
+            out[f"llama1b_prefill_bf16_m{m}_{name}"] = dict(
+                m=m, n=n, k=k, us=round(us, 3), tflops=round(tf, 2), mfma_frac=round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+                gbs=round(nbytes / us / 1e3, 1), hbm_frac=round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4))
+            for b in (w, x, y):
+                b.free()
+
+    # GQA decode attention 32 q / 8 kv heads, head_dim 128, fp16 q/K/V/out, fp32 softmax
+    hd, nh, nkv = 128, 32, 8
+    kvblock = rng.standard_normal(1 << 22).astype(np.float16)
+    for ctx in (512, 4096, 32768):
+        for batch in (1, 8):
+            cbytes = batch * ctx * nkv * hd * 2
+            reps = max(1, min(128, -(-COLD_BYTES // (2 * cbytes))))
+            kc = _replicated(dev, kvblock, cbytes, reps)
+            vc = _replicated(dev, kvblock, cbytes, reps)
+            q = dev.alloc_shared(rng.standard_normal(batch * nh * hd).astype(np.float16))
+            o = dev.alloc(batch * nh * hd * 2)
+
+            def attn(i):
+                suite.attention_decode(q, l0.F16, kc.ptr + i * cbytes, vc.ptr + i * cbytes, l0.F16, o, l0.F16, batch,
+                                       hd, nh, nkv, ctx, ctx)
+
+            attn(0)  # sizes the split workspace before recording
+            launches = max(reps, 4)
+            us = _replay_us(dev, lambda: [attn(i % reps) for i in range(launches)], launches)
+            nbytes = 2 * cbytes + 2 * 2 * batch * nh * hd
+            out[f"gqa_attention_ctx{ctx}_b{batch}"] = dict(
+                ctx=ctx, batch=batch, bytes=nbytes, us=round(us, 3), gbs=round(nbytes / us / 1e3, 1),
+                frac=round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4))
+            for b in (kc, vc, q, o):
+                b.free()
+    return out
+
+
 def cpu_baseline(model, cfg, tokens: int, position: int) -> dict:
     from oracle import pyoracle as orc
 
@@ -122,6 +256,8 @@ def main() -> int:
     ap.add_argument("--profile-rounds", type=int, default=4,
                     help="passes over all layers when timing each kernel kind for the roofline")
     ap.add_argument("--cpu-tokens", type=int, default=2, help="tokens in the CPU baseline sample (0: skip)")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the per-configuration kernel measurements (GEMV, prefill GEMM, attention)")
     ap.add_argument("--eager-step", action="store_true",
                     help="enqueue the decode step's kernels one by one instead of replaying its HIP graph "
                          "(same kernels; for profilers that cannot trace graph launches)")
@@ -175,6 +311,11 @@ def main() -> int:
         traffic = json.loads(tf.read_text()).get("hbm_bytes_per_launch")
     log(f"int8 GEMV: {achieved:.0f} GB/s over {launches} launches/step ({gemv_us:.0f} us/step)")
 
+    configs = None
+    if not args.no_configs:
+        log("timing the per-configuration kernels")
+        configs = measure_configs(dev)
+
     cpu = None
     if args.cpu_tokens > 0:
         log("CPU baseline: exporting the model and running the oracle")
@@ -207,6 +348,7 @@ def main() -> int:
                           "frac": round(tps * step_bytes / (HBM_PEAK_GBS * 1e9), 4)},
         "kernels": table,
         "hbm_copy_probe": copy,
+        "configs": configs,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -91,6 +91,11 @@ int l0h_begin_recording(l0h_device* dev);
 int l0h_end_recording(l0h_device* dev);
 /* ComputeDevice.AbortRecording (LlmModel.cs:372-377, :431-437). */
 int l0h_abort_recording(l0h_device* dev);
+/* Launches the command list of the last l0h_end_recording again, `count` times back to back on
+ * the device's stream, and reports the mean HIP-event time of one replay in milliseconds (the
+ * reference re-records a list per token, LlmModel.cs:417-443; replaying one is the same work
+ * without the recording). L0H_ERR_INVALID_OP when nothing has been recorded. */
+int l0h_replay_recording(l0h_device* dev, int count, float* ms_per_replay);
 /* ComputeDevice.IsRecording (LlmModel.cs:353, :417). */
 int l0h_is_recording(l0h_device* dev, int* out);
 /* Wait for every queued operation. */

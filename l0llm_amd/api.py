@@ -124,6 +124,13 @@ class Device:
     def abort_recording(self) -> None:
         check(lib.l0h_abort_recording(self.handle))
 
+    def replay_recording(self, count: int = 1) -> float:
+        """Launches the last recorded command list `count` more times back to back; returns the
+        mean device time of one replay in milliseconds."""
+        ms = ctypes.c_float()
+        check(lib.l0h_replay_recording(self.handle, count, ctypes.byref(ms)))
+        return ms.value
+
     @property
     def is_recording(self) -> bool:
         v = ctypes.c_int()

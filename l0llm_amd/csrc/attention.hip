@@ -10,7 +10,8 @@
 // log2 domain) over its positions; the slots of a block are combined at the end (lane shuffles,
 // then LDS across waves) into one (max, sum, acc) partial per q head. A second small kernel
 // merges the splits' partials with a log-sum-exp combine in a fixed order, so the result does
-// not depend on timing.
+// not depend on timing. (The kernel boundary publishes the partials: a completion ticket with
+// device-scope fences inside one kernel measured several microseconds slower on gfx950.)
 //
 // Every load is unconditional (positions past the slice are clamped to valid rows and masked in
 // the softmax), the next step's K and V rows are requested before the current step is computed,
@@ -19,6 +20,7 @@
 #include "kernels.h"
 
 #include <cmath>
+#include <cstdlib>
 
 namespace l0h {
 namespace {
@@ -27,7 +29,6 @@ constexpr int kBlock = 256;
 constexpr int kWaves = kBlock / 64;
 constexpr int kGroupMax = 8;  // q heads per kv head
 constexpr int kUnroll = 4;    // positions per slot per step
-constexpr int kMergeBlock = 256;
 constexpr int kMaxSplits = 256;
 
 template <int CTRL, int ROW_MASK>
@@ -48,6 +49,22 @@ __device__ __forceinline__ float group_sum(float v) {
         v += dpp_src<0x128, 0xf>(v);  // row_ror:8
     }
     return v;
+}
+
+// Reduction over the position slots of a wave: lanes lane % LPP == const. Within a 16-lane row
+// the slots are LPP lanes apart (DPP row rotations), then rows are combined with the gfx950 row
+// swaps: permlane16_swap(v, v) yields rows (r0, r0, r2, r2) and (r1, r1, r3, r3), permlane32_swap
+// the two 32-lane halves, so op(first, second) reduces across them.
+template <int LPP, bool MAX>
+__device__ __forceinline__ float slot_reduce(float v) {
+    auto op = [](float a, float b) { return MAX ? fmaxf(a, b) : a + b; };
+    if constexpr (LPP <= 8) v = op(v, dpp_src<0x120 + (LPP <= 8 ? LPP : 1), 0xf>(v));   // row_ror:LPP
+    if constexpr (LPP <= 4) v = op(v, dpp_src<0x120 + (LPP <= 4 ? 2 * LPP : 1), 0xf>(v));  // row_ror:2 LPP
+    if constexpr (LPP <= 2) v = op(v, dpp_src<0x120 + (LPP <= 2 ? 4 * LPP : 1), 0xf>(v));  // row_ror:4 LPP
+    const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = op(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+    const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return op(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
 }
 
 template <int CT>
@@ -100,6 +117,9 @@ __device__ __forceinline__ void load8(const void* base, size_t idx, float* f) {
         }
     }
 }
+
+// Floats per split partial: G * HD accumulators, then G maxima and G sums, padded to 16 bytes.
+__host__ __device__ constexpr int partial_stride(int G, int HD) { return G * HD + ((2 * G + 3) / 4) * 4; }
 
 // Sequence length of batch entry b, and this split's slice [lo, lo + n) of it. Slices are whole
 // steps (NG * kUnroll positions) so a block's slots stay in step.
@@ -241,23 +261,14 @@ __global__ __launch_bounds__(kBlock) void attn_split_kernel(const AttnParams p, 
         }
     }
 
-    // Combine the slots of a wave: lanes lg of the PPW slots (offsets LPP, 2 LPP, ...).
+    // Combine the PPW slots of a wave (lanes lane % LPP == lg).
 #pragma unroll
     for (int h = 0; h < G; h++) {
-        float M = m[h];
-#pragma unroll
-        for (int off = LPP; off < 64; off <<= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+        const float M = slot_reduce<LPP, true>(m[h]);
         const float c = M == -INFINITY ? 0.f : exp2f(m[h] - M);
-        float lw = l[h] * c;
+        const float lw = slot_reduce<LPP, false>(l[h] * c);
 #pragma unroll
-        for (int off = LPP; off < 64; off <<= 1) lw += __shfl_xor(lw, off, 64);
-#pragma unroll
-        for (int d = 0; d < 8; d++) {
-            float a = acc[h][d] * c;
-#pragma unroll
-            for (int off = LPP; off < 64; off <<= 1) a += __shfl_xor(a, off, 64);
-            acc[h][d] = a;
-        }
+        for (int d = 0; d < 8; d++) acc[h][d] = slot_reduce<LPP, false>(acc[h][d] * c);
         if (lane < LPP) {
 #pragma unroll
             for (int d = 0; d < 8; d++) s_acc[wave][h][lg * 8 + d] = acc[h][d];
@@ -269,9 +280,10 @@ __global__ __launch_bounds__(kBlock) void attn_split_kernel(const AttnParams p, 
     }
     __syncthreads();
 
-    // Combine the waves (fixed order) and write the block's partial, or the output when the
-    // sequence is not split.
-    const size_t pbase = (((size_t)b * p.nkv + g) * p.splits + split) * (size_t)G * (HD + 2);
+    // Combine the waves (fixed order): the output directly when the sequence is not split, else
+    // this split's partial.
+    constexpr int PS = partial_stride(G, HD);
+    float* part = p.splits > 1 ? p.partials + (((size_t)b * p.nkv + g) * p.splits + split) * PS : nullptr;
     for (int idx = tid; idx < G * HD; idx += kBlock) {
         const int h = idx / HD, d = idx - h * HD;
         float M = -INFINITY;
@@ -289,7 +301,6 @@ __global__ __launch_bounds__(kBlock) void attn_split_kernel(const AttnParams p, 
                 store_act(p.out, p.out_dtype, (size_t)b * p.nh * HD + (size_t)(g * gsize + h) * HD + d,
                           den > 0.f ? num / den : 0.f);
         } else {
-            float* part = p.partials + pbase;
             part[idx] = num;
             if (d == 0) {
                 part[G * HD + h] = M;
@@ -299,61 +310,91 @@ __global__ __launch_bounds__(kBlock) void attn_split_kernel(const AttnParams p, 
     }
 }
 
-// Log-sum-exp merge of the splits' partials: one block per (q head of the group, kv head,
-// batch). The splits' maxima and sums go through LDS; thread (d, j) folds splits j, j + J, ...
-// for dim d (eight loads in flight), then the J partial sums are added in a fixed order.
+// Log-sum-exp merge of the splits' partials. Block (column group, kv head, batch): thread
+// (column c of 4 dims, lane j of J) loads the max, sum and 4 accumulators of splits j, j + J, ...
+// in one round (eight splits in flight), folds them with an online max, and the J lanes of a
+// column are combined in a fixed order.
 template <int HD, int G>
-__global__ __launch_bounds__(kMergeBlock) void attn_merge_kernel(const AttnParams p) {
-    constexpr int J = kMergeBlock / HD;  // split lanes per dim
-    __shared__ float s_w[kMaxSplits], s_lw[kMaxSplits], s_red[kMergeBlock / 64];
-    __shared__ float s_num[J][HD];
-    const int h = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
-    const int tid = threadIdx.x;
+__global__ __launch_bounds__(kBlock) void attn_merge_kernel(const AttnParams p) {
+    constexpr int NC = G * HD / 4;  // float4 columns of a (batch, kv head)
+    constexpr int CB = NC < 32 ? NC : 32;  // columns per block
+    constexpr int J = kBlock / CB;  // split lanes per column
+    constexpr int PS = partial_stride(G, HD);
+    __shared__ float s_mx[J][CB], s_den[J][CB];
+    __shared__ float4 s_num[J][CB];
+    const int g = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x, cl = tid % CB, j = tid / CB;
+    const int c = blockIdx.x * CB + cl;
+    const int cc = min(c, NC - 1);
+    const int h = cc * 4 / HD;
     const int gsize = p.nh / p.nkv;
     const int S = p.splits;
-    const size_t stride = (size_t)G * (HD + 2);
-    const float* all = p.partials + ((size_t)b * p.nkv + g) * S * stride;
-    const int sc = min(tid, S - 1);
-    const float ms0 = all[(size_t)sc * stride + G * HD + h];
-    const float ls = all[(size_t)sc * stride + G * HD + G + h];
-    const float ms = tid < S ? ms0 : -INFINITY;
-    float M = ms;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
-    if ((tid & 63) == 0) s_red[tid >> 6] = M;
-    __syncthreads();
-    M = s_red[0];
-#pragma unroll
-    for (int w = 1; w < kMergeBlock / 64; w++) M = fmaxf(M, s_red[w]);
-    if (tid < S) {
-        const float w = (M == -INFINITY || ms == -INFINITY) ? 0.f : exp2f(ms - M);
-        s_w[tid] = w;
-        s_lw[tid] = w * ls;
-    }
-    __syncthreads();
-    const int d = tid % HD, j = tid / HD;
-    float num[8];
-#pragma unroll
-    for (int u = 0; u < 8; u++) num[u] = 0.f;
+    const float* all = p.partials + ((size_t)b * p.nkv + g) * S * PS;
+    float M = -INFINITY, den = 0.f;
+    float4 num = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int s0 = j; s0 < S; s0 += 8 * J) {
-        float v[8];
+        float ms[8], ls[8];
+        float4 v[8];
 #pragma unroll
-        for (int u = 0; u < 8; u++) v[u] = all[(size_t)min(s0 + u * J, S - 1) * stride + h * HD + d];
+        for (int u = 0; u < 8; u++) {
+            const float* ps = all + (size_t)min(s0 + u * J, S - 1) * PS;
+            v[u] = *reinterpret_cast<const float4*>(ps + cc * 4);
+            ms[u] = ps[G * HD + h];
+            ls[u] = ps[G * HD + G + h];
+        }
+        float mx = M;
 #pragma unroll
         for (int u = 0; u < 8; u++)
-            if (s0 + u * J < S) num[u] = fmaf(s_w[s0 + u * J], v[u], num[u]);
+            if (s0 + u * J < S) mx = fmaxf(mx, ms[u]);
+        if (mx != -INFINITY) {
+            const float cs = exp2f(M - mx);  // 0 while M is still -inf
+            num.x *= cs;
+            num.y *= cs;
+            num.z *= cs;
+            num.w *= cs;
+            den *= cs;
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                if (s0 + u * J < S && ms[u] != -INFINITY) {
+                    const float w = exp2f(ms[u] - mx);
+                    num.x = fmaf(w, v[u].x, num.x);
+                    num.y = fmaf(w, v[u].y, num.y);
+                    num.z = fmaf(w, v[u].z, num.z);
+                    num.w = fmaf(w, v[u].w, num.w);
+                    den = fmaf(w, ls[u], den);
+                }
+            }
+            M = mx;
+        }
     }
-    float nsum = 0.f;
-#pragma unroll
-    for (int u = 0; u < 8; u++) nsum += num[u];
-    s_num[j][d] = nsum;
+    s_mx[j][cl] = M;
+    s_den[j][cl] = den;
+    s_num[j][cl] = num;
     __syncthreads();
-    if (tid < HD && h < gsize) {
-        float nn = 0.f, dd = 0.f;
+    if (j == 0 && c < NC && h < gsize) {
+        float Mt = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < J; i++) nn += s_num[i][tid];
-        for (int s = 0; s < S; s++) dd += s_lw[s];
-        store_act(p.out, p.out_dtype, (size_t)b * p.nh * HD + (size_t)(g * gsize + h) * HD + tid, dd > 0.f ? nn / dd : 0.f);
+        for (int i = 0; i < J; i++) Mt = fmaxf(Mt, s_mx[i][cl]);
+        float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
+        float dt = 0.f;
+        if (Mt != -INFINITY) {
+#pragma unroll
+            for (int i = 0; i < J; i++) {
+                const float w = s_mx[i][cl] == -INFINITY ? 0.f : exp2f(s_mx[i][cl] - Mt);
+                const float4 u = s_num[i][cl];
+                t.x = fmaf(w, u.x, t.x);
+                t.y = fmaf(w, u.y, t.y);
+                t.z = fmaf(w, u.z, t.z);
+                t.w = fmaf(w, u.w, t.w);
+                dt = fmaf(w, s_den[i][cl], dt);
+            }
+        }
+        const float inv = dt > 0.f ? 1.f / dt : 0.f;
+        const size_t o = (size_t)b * p.nh * HD + (size_t)(g * gsize + h) * HD + (cc * 4 - h * HD);
+        store_act(p.out, p.out_dtype, o + 0, t.x * inv);
+        store_act(p.out, p.out_dtype, o + 1, t.y * inv);
+        store_act(p.out, p.out_dtype, o + 2, t.z * inv);
+        store_act(p.out, p.out_dtype, o + 3, t.w * inv);
     }
 }
 
@@ -363,7 +404,8 @@ int launch_g(hipStream_t s, const AttnParams& p, int seq_len_step, size_t cache_
     attn_split_kernel<HD, CT, QT, G><<<grid, kBlock, 0, s>>>(p, seq_len_step, cache_batch_stride);
     int st = launch_status("attention");
     if (st || p.splits == 1) return st;
-    attn_merge_kernel<HD, G><<<dim3(p.nh / p.nkv, p.nkv, p.batch), kMergeBlock, 0, s>>>(p);
+    constexpr int NC = G * HD / 4, CB = NC < 32 ? NC : 32;
+    attn_merge_kernel<HD, G><<<dim3(NC / CB, p.nkv, p.batch), kBlock, 0, s>>>(p);
     return launch_status("attention merge");
 }
 
@@ -413,17 +455,23 @@ int launch_any(hipStream_t s, const AttnParams& p, int seq_len_step, size_t cach
 }  // namespace
 
 int attention_default_splits(int batch, int nkv, int max_len, int compute_units) {
-    // Enough blocks to cover every CU about twice, each with at least one step of positions
-    // (64 for head_dim 128); at most kMaxSplits.
+    // Positions per split: at least two steps (128 positions at head_dim 128), so a block
+    // overlaps its second step's loads with the first step's compute, and about two blocks per
+    // CU in total; at most kMaxSplits. L0H_ATTN_SPLIT_POSITIONS overrides the minimum (tuning).
+    static const int min_pos = [] {
+        const char* e = std::getenv("L0H_ATTN_SPLIT_POSITIONS");
+        const int v = e ? std::atoi(e) : 128;
+        return v > 0 ? v : 128;
+    }();
     const int target = (int)ceil_div((size_t)2 * std::max(compute_units, 1), (size_t)std::max(batch * nkv, 1));
-    const int by_len = (int)ceil_div((size_t)std::max(max_len, 1), 64);
+    const int by_len = (int)ceil_div((size_t)std::max(max_len, 1), (size_t)min_pos);
     return std::max(1, std::min(kMaxSplits, std::min(target, by_len)));
 }
 
 size_t attention_partials_bytes(const AttnParams& p) {
     const int gsize = p.nkv > 0 ? p.nh / p.nkv : 1;
     const int G = group_pow2(gsize);
-    return (size_t)p.batch * p.nkv * p.splits * G * (p.head_dim + 2) * sizeof(float);
+    return (size_t)p.batch * p.nkv * p.splits * partial_stride(G, p.head_dim) * sizeof(float);
 }
 
 int launch_attention_decode(hipStream_t s, const AttnParams& p) {

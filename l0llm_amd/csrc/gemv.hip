@@ -15,8 +15,8 @@
 // issued after the prefetch, would make that wait cover the prefetched item too).
 //
 // Activations are staged once per block in LDS as fp32, with the RMSNorm prologue applied there
-// when fused; the prologue's own loads (x, norm weights, RoPE frequencies) are issued before the
-// first weight item. Dequantisation happens in registers (int8: bytes biased by +128 and
+// when fused, before the first weight item is requested: a CU's memory pipeline returns data in
+// order, so activation loads issued behind a weight stream would wait on HBM. Dequantisation happens in registers (int8: bytes biased by +128 and
 // converted with v_cvt_f32_ubyteN, the bias removed after the reduction with sum(x), the per-row
 // scale applied once), accumulation is fp32, and the cross-lane sum uses DPP.
 #include <cstdlib>
@@ -57,6 +57,26 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
     float t = 0.f;
 #pragma unroll
     for (int i = 0; i < kWaves; i++) t += red[i];
+    return t;
+}
+
+// Block-wide sums of two values in one exchange (all threads of a kBlock block must call it).
+__device__ __forceinline__ float2 block_sum2(float a, float b, float* red) {
+    a = wave_sum(a);
+    b = wave_sum(b);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) {
+        red[wave] = a;
+        red[kWaves + wave] = b;
+    }
+    __syncthreads();
+    float2 t = make_float2(0.f, 0.f);
+#pragma unroll
+    for (int i = 0; i < kWaves; i++) {
+        t.x += red[i];
+        t.y += red[kWaves + i];
+    }
     return t;
 }
 
@@ -230,7 +250,7 @@ template <int WT, int R, int U, int MR, int KX, bool NORM, int EPI>
 __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p, int k_pad) {
     extern __shared__ float4 smem4[];
     float* xs = reinterpret_cast<float*>(smem4);  // [MR, k_pad], zero past K
-    __shared__ float red[kWaves];
+    __shared__ float red[2 * kWaves];
     __shared__ float xsum_s[MR];
     __shared__ float rope_cs[EPI == EPI_QKV ? kMaxRotaryHalf : 1];
     __shared__ float rope_sn[EPI == EPI_QKV ? kMaxRotaryHalf : 1];
@@ -296,58 +316,57 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p, int
         pos = *p.position;
     }
 
-    // ---- first weight item ----
-    int g = blockIdx.x * kWaves + wave;
-    uint4 wa[U][R], wb[U][R];
-    Side sa, sb;
-    sa = load_side<WT, R, MR, EPI>(p, min(g, ngroups - 1), lane, any);
-    load_w(wa, g, 0);
-
-    // ---- stage the one activation row (and RMSNorm) in LDS while the weights are in flight ----
+    // ---- stage the one activation row (and RMSNorm) in LDS before any weight load: the memory
+    // pipeline of a CU returns data in order, so activation loads queued behind a block's weight
+    // stream would wait for HBM ----
     if constexpr (MR == 1) {
-        float scale = 1.f;
-        if constexpr (NORM) {
-            float ss = 0.f;
+        // One pass: sum of squares (RMSNorm) and the sum of the values the dot products will use
+        // (the int8 bias correction), reduced together; then x * scale * w goes to LDS.
+        float ss = 0.f, xw = 0.f;
 #pragma unroll
-            for (int i = 0; i < KX; i++) {
-                float f[8];
-                const int n = chunk_to_float(xr[i], xdt, f);
-                if (i * kBlock + tid < nxc) {
+        for (int i = 0; i < KX; i++) {
+            float f[8];
+            const int n = chunk_to_float(xr[i], xdt, f);
+            if (i * kBlock + tid < nxc) {
+                if constexpr (NORM) {  // x is fp32 here: 4 values, matching the 4 norm weights
+                    const float nw[4] = {__uint_as_float(nr[i].x), __uint_as_float(nr[i].y), __uint_as_float(nr[i].z),
+                                         __uint_as_float(nr[i].w)};
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        ss += f[e] * f[e];
+                        xw += f[e] * nw[e];
+                    }
+                } else {
 #pragma unroll
                     for (int e = 0; e < 8; e++)
-                        if (e < n) ss += f[e] * f[e];
+                        if (e < n) xw += f[e];
                 }
             }
-            ss = block_sum(ss, red);
-            scale = rsqrtf(ss / (float)K + p.eps);
         }
-        float xsum = 0.f;
+        float scale = 1.f;
+        if constexpr (NORM || WT == L0H_I8PC) {
+            const float2 t = block_sum2(ss, xw, red);
+            if constexpr (NORM) scale = rsqrtf(t.x / (float)K + p.eps);
+            if (tid == 0) xsum_s[0] = scale * t.y;
+        }
 #pragma unroll
         for (int i = 0; i < KX; i++) {
             const int idx = i * kBlock + tid;
             if (idx < nxc) {
                 float f[8];
                 const int n = chunk_to_float(xr[i], xdt, f);
-                if constexpr (NORM) {  // x is fp32 here: 4 values, matching the 4 norm weights
+                if constexpr (NORM) {
                     f[0] *= scale * __uint_as_float(nr[i].x);
                     f[1] *= scale * __uint_as_float(nr[i].y);
                     f[2] *= scale * __uint_as_float(nr[i].z);
                     f[3] *= scale * __uint_as_float(nr[i].w);
                 }
 #pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    if (e < n) {
-                        xs[idx * n + e] = f[e];
-                        xsum += f[e];
-                    }
-                }
+                for (int e = 0; e < 8; e++)
+                    if (e < n) xs[idx * n + e] = f[e];
             }
         }
         for (int i = K + tid; i < k_pad; i += kBlock) xs[i] = 0.f;
-        if constexpr (WT == L0H_I8PC) {
-            xsum = block_sum(xsum, red);
-            if (tid == 0) xsum_s[0] = xsum;
-        }
     }
     if constexpr (EPI == EPI_QKV) {
         // cos/sin of this position for every rotated pair, once per block (accurate sincos of
@@ -360,6 +379,13 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p, int
         }
     }
     __syncthreads();
+
+    // ---- first weight item ----
+    int g = blockIdx.x * kWaves + wave;
+    uint4 wa[U][R], wb[U][R];
+    Side sa, sb;
+    sa = load_side<WT, R, MR, EPI>(p, min(g, ngroups - 1), lane, any);
+    load_w(wa, g, 0);
 
     // ---- stream: no barrier below this point, waves run independently ----
     float acc[MR][R];
@@ -540,7 +566,21 @@ int launch_fast(hipStream_t s, const GemvParams& p) {
     if (attr != hipSuccess) return fail(L0H_ERR_DEVICE, std::string("hipFuncSetAttribute: ") + hipGetErrorString(attr));
     const unsigned groups = ceil_div(p.n, R);
     unsigned grid = ceil_div(groups, kWaves);
-    if (p.max_blocks > 0) grid = std::min<unsigned>(grid, (unsigned)p.max_blocks);
+    if (p.max_blocks > 0) {
+        // A persistent grid must be resident in one round: at most as many blocks per CU as the
+        // kernel's registers and this launch's LDS allow (queried once per instantiation and
+        // tile size).
+        static thread_local int occ_shmem = -1, occ_blocks = 0;
+        if (occ_shmem != (int)shmem) {
+            int nb = 0;
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void*>(kern), kBlock, shmem) != hipSuccess)
+                nb = 1;
+            occ_shmem = (int)shmem;
+            occ_blocks = std::max(1, nb);
+        }
+        const unsigned cap = std::min<unsigned>((unsigned)p.max_blocks, (unsigned)(occ_blocks * std::max(1, p.compute_units)));
+        grid = std::min(grid, cap);
+    }
     kern<<<grid, kBlock, shmem, s>>>(p, k_pad);
     return launch_status("gemv_nk");
 }

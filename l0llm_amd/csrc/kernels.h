@@ -46,6 +46,7 @@ struct GemvParams {
     // Grid cap: 0 launches one block per group of rows; otherwise at most this many blocks
     // loop over the row groups (activations staged once per block).
     int max_blocks = 0;
+    int compute_units = 0;  // with max_blocks: caps the grid at the blocks resident in one round
 };
 
 // Persistent-grid size for weight-streaming kernels on a device with `compute_units` CUs.
@@ -102,7 +103,7 @@ struct AttnParams {
     int seq_len_add = 0;
     int max_seq_len = 0;
     int splits = 1;  // sequence partitions per (batch, kv head)
-    float* partials = nullptr;  // [batch, nkv, splits, group, head_dim + 2]
+    float* partials = nullptr;  // per (batch, kv head, split): G*head_dim acc, G max, G sum (padded)
 };
 int attention_default_splits(int batch, int nkv, int max_len, int compute_units);
 size_t attention_partials_bytes(const AttnParams& p);

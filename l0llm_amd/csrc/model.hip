@@ -293,6 +293,7 @@ int launch_op(l0h_model* m, hipStream_t s, int kind, int li) {
     GemvParams g;
     g.w_dtype = m->storage;
     g.max_blocks = gemv_max_blocks(m->dev->compute_units);
+    g.compute_units = m->dev->compute_units;
     switch (kind) {
     case L0H_KERNEL_EMBEDDING:  // LlmModel.cs:424
         return launch_embedding(s, m->token, m->embedding, m->hidden, H, (size_t)H);

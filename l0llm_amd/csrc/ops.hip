@@ -226,6 +226,7 @@ int l0h_gemv_nk(l0h_device* dev, int w_dtype, int rows, int out_dim, int in_dim,
     p.y_dtype = y_dtype;
     p.epilogue = EPI_STORE;
     p.max_blocks = gemv_max_blocks(dev->compute_units);
+    p.compute_units = dev->compute_units;
     return launch_gemv_nk(dev->stream, p);
 }
 

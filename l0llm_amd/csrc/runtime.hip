@@ -290,6 +290,28 @@ int l0h_end_recording(l0h_device* dev) {
     return L0H_OK;
 }
 
+int l0h_replay_recording(l0h_device* dev, int count, float* ms_per_replay) {
+    int st = use_device(dev);
+    if (st) return st;
+    L0H_CHECK_ARG(count > 0 && ms_per_replay, "count must be positive and ms_per_replay non-null");
+    if (dev->recording) return fail(L0H_ERR_INVALID_OP, "the device is recording");
+    if (!dev->cached_exec) return fail(L0H_ERR_INVALID_OP, "nothing has been recorded");
+    hipEvent_t a = nullptr, b = nullptr;
+    L0H_HIP_TRY(hipEventCreate(&a));
+    hipError_t e = hipEventCreate(&b);
+    if (e == hipSuccess) e = hipEventRecord(a, dev->stream);
+    for (int i = 0; i < count && e == hipSuccess; i++) e = hipGraphLaunch(dev->cached_exec, dev->stream);
+    if (e == hipSuccess) e = hipEventRecord(b, dev->stream);
+    if (e == hipSuccess) e = hipEventSynchronize(b);
+    float ms = 0.f;
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, a, b);
+    (void)hipEventDestroy(a);
+    if (b) (void)hipEventDestroy(b);
+    if (e != hipSuccess) return fail(L0H_ERR_DEVICE, std::string("replay: ") + hipGetErrorString(e));
+    *ms_per_replay = ms / (float)count;
+    return L0H_OK;
+}
+
 int l0h_abort_recording(l0h_device* dev) {
     int st = use_device(dev);
     if (st) return st;
