@@ -1,0 +1,6 @@
+// Instantiations of the weight-streaming GEMV for L0H_I8PC weights (see gemv_kernel.h).
+#include "gemv_kernel.h"
+
+namespace l0h {
+int gemv_dispatch_i8(hipStream_t s, const GemvParams& p, int mr) { return dispatch_wt<L0H_I8PC>(s, p, mr); }
+}  // namespace l0h

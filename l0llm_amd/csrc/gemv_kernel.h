@@ -1,0 +1,633 @@
+// Weight-streaming GEMV kernel template for gfx950 (decode, M = 1 .. 8 activation rows), shared
+// by the per-weight-type translation units gemv_i8.hip, gemv_f16.hip, gemv_bf16.hip and
+// gemv_f32.hip (compiled in parallel).
+//
+// Replaces LlmKernelSuite.Gemv / GemvQ8 (call sites LlmMatrix.cs:122-171, :231-241) for the
+// weight formats of this path. Weights are [N, K] row-major (HuggingFace [out, in]).
+//
+// Work: the N rows are cut into row groups of R rows and each row group's K extent into batches
+// of 64 * U chunks of 16 bytes. Wave w of the grid walks the items (row group, batch) of row
+// groups w, w + W, w + 2W, ... (W waves in the grid) in order; in an item, lane l reads chunk
+// batch * 64U + u * 64 + l of each of the R rows, so one wave instruction reads 1 KiB of one
+// row. The loads of item i+1 (its R * U weight chunks and the per-row values its epilogue needs)
+// are issued before item i is computed. Every load is unconditional: rows past N and chunks past
+// K are clamped to the last valid ones, and the activations staged in LDS are zero past K, so a
+// clamped chunk adds nothing. The load stream is therefore straight-line and the in-order memory
+// counter waits for exactly the item being computed (a conditional load, or a use of a load
+// issued after the prefetch, would make that wait cover the prefetched item too).
+//
+// Activations are staged once per block in LDS as fp32, with the RMSNorm prologue applied there
+// when fused. Every wave issues its activation loads, then the block meets at a barrier before
+// the first weight item is requested: a CU's memory pipeline returns data in order, so the
+// activations come back ahead of the weight stream and are staged while it is in flight; the
+// staging barriers wait on LDS only, never on the weight loads. Dequantisation
+// happens in registers (int8: bytes biased by +128 and converted with v_cvt_f32_ubyteN, the bias
+// removed after the reduction with sum(x), the per-row scale applied once), accumulation is
+// fp32, and the cross-lane sum uses DPP.
+#pragma once
+
+#include <cstdlib>
+
+#include "kernels.h"
+
+namespace l0h {
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kBlock = 64 * kWaves;
+constexpr size_t kLdsBudget = 64 * 1024;  // activation tile per block
+constexpr int kMaxRotaryHalf = 128;       // cos/sin table entries per block (rotary_dim <= 256)
+
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_src(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, false));
+}
+
+// Sum over the 64 lanes of a wave, returned to every lane (wave-uniform).
+__device__ __forceinline__ float wave_sum(float v) {
+    v += dpp_src<0xB1, 0xf>(v);   // quad_perm [1,0,3,2]
+    v += dpp_src<0x4E, 0xf>(v);   // quad_perm [2,3,0,1]
+    v += dpp_src<0x141, 0xf>(v);  // row_half_mirror
+    v += dpp_src<0x140, 0xf>(v);  // row_mirror
+    v += dpp_src<0x142, 0xa>(v);  // row_bcast15 into rows 1, 3
+    v += dpp_src<0x143, 0xc>(v);  // row_bcast31 into rows 2, 3
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Block-wide sum (all threads of a kBlock block must call it). Returns the sum to all.
+__device__ __forceinline__ float block_sum(float v, float* red) {
+    v = wave_sum(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < kWaves; i++) t += red[i];
+    return t;
+}
+
+// Workgroup barrier that orders LDS only: the wave's LDS operations complete, then s_barrier. Unlike
+// __syncthreads it does not wait for outstanding global loads, so a weight stream issued before it
+// stays in flight.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// Block-wide sums of two values in one exchange (all threads of a kBlock block must call it);
+// LDS-only barriers (see lds_barrier).
+__device__ __forceinline__ float2 block_sum2(float a, float b, float* red) {
+    a = wave_sum(a);
+    b = wave_sum(b);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    lds_barrier();
+    if (lane == 0) {
+        red[wave] = a;
+        red[kWaves + wave] = b;
+    }
+    lds_barrier();
+    float2 t = make_float2(0.f, 0.f);
+#pragma unroll
+    for (int i = 0; i < kWaves; i++) {
+        t.x += red[i];
+        t.y += red[kWaves + i];
+    }
+    return t;
+}
+
+template <int WT>
+struct WTraits;
+template <>
+struct WTraits<L0H_I8PC> {
+    static constexpr int kElems = 16;
+    static constexpr int kBytes = 1;
+};
+template <>
+struct WTraits<L0H_F16> {
+    static constexpr int kElems = 8;
+    static constexpr int kBytes = 2;
+};
+template <>
+struct WTraits<L0H_BF16> {
+    static constexpr int kElems = 8;
+    static constexpr int kBytes = 2;
+};
+template <>
+struct WTraits<L0H_F32> {
+    static constexpr int kElems = 4;
+    static constexpr int kBytes = 4;
+};
+
+// acc += dot(chunk, x). For int8 the bytes are biased by +128 and converted with
+// v_cvt_f32_ubyteN; the bias is removed after the reduction using sum(x).
+template <int WT>
+__device__ __forceinline__ void chunk_fma(const uint4& w, const float* x, float& acc) {
+    const uint32_t d[4] = {w.x, w.y, w.z, w.w};
+    if constexpr (WT == L0H_I8PC) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            uint32_t u = d[j] ^ 0x80808080u;
+            acc = fmaf((float)(u & 0xffu), x[4 * j + 0], acc);
+            acc = fmaf((float)((u >> 8) & 0xffu), x[4 * j + 1], acc);
+            acc = fmaf((float)((u >> 16) & 0xffu), x[4 * j + 2], acc);
+            acc = fmaf((float)(u >> 24), x[4 * j + 3], acc);
+        }
+    } else if constexpr (WT == L0H_F16) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            __half2 h = __builtin_bit_cast(__half2, d[j]);
+            float2 f = __half22float2(h);
+            acc = fmaf(f.x, x[2 * j + 0], acc);
+            acc = fmaf(f.y, x[2 * j + 1], acc);
+        }
+    } else if constexpr (WT == L0H_BF16) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            acc = fmaf(__uint_as_float(d[j] << 16), x[2 * j + 0], acc);
+            acc = fmaf(__uint_as_float(d[j] & 0xffff0000u), x[2 * j + 1], acc);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc = fmaf(__uint_as_float(d[j]), x[j], acc);
+    }
+}
+
+// The 16 bytes of an activation chunk as fp32 (4 fp32 values or 8 fp16 / bf16 values).
+__device__ __forceinline__ int chunk_to_float(const uint4& c, int dt, float* f) {
+    const uint32_t d[4] = {c.x, c.y, c.z, c.w};
+    if (dt == L0H_F32) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) f[j] = __uint_as_float(d[j]);
+        return 4;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        if (dt == L0H_F16) {
+            float2 t = __half22float2(__builtin_bit_cast(__half2, d[j]));
+            f[2 * j] = t.x;
+            f[2 * j + 1] = t.y;
+        } else {
+            f[2 * j] = __uint_as_float(d[j] << 16);
+            f[2 * j + 1] = __uint_as_float(d[j] & 0xffff0000u);
+        }
+    }
+    return 8;
+}
+
+__device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
+
+__device__ __forceinline__ float half_bits(uint32_t b) { return __half2float(__ushort_as_half((uint16_t)b)); }
+
+__device__ __forceinline__ void store_cache(void* cache, int dt, size_t idx, float v) {
+    if (dt == L0H_F16)
+        static_cast<uint16_t*>(cache)[idx] = __half_as_ushort(__float2half_rn(v));
+    else
+        static_cast<float*>(cache)[idx] = v;
+}
+
+// Epilogue for the RoPE-paired rows (row, row+1) of the fused q|k|v matrix; cs/sn hold
+// cos/sin(pos * inv_freq[i]) * scale for this launch's position.
+__device__ __forceinline__ void qkv_pair(const GemvParams& p, int row, float v0, float v1, int pos,
+                                         const float* cs_tab, const float* sn_tab) {
+    const int hd = p.head_dim, rot = p.rotary_dim;
+    if (row >= p.q_dim + p.kv_dim) {  // v rows: natural order
+        const int off = row - p.q_dim - p.kv_dim;
+        size_t base = (size_t)pos * p.kv_dim + off;
+        store_cache(p.v_cache, p.cache_dtype, base, v0);
+        store_cache(p.v_cache, p.cache_dtype, base + 1, v1);
+        return;
+    }
+    const bool is_q = row < p.q_dim;
+    const int off = is_q ? row : row - p.q_dim;
+    const int head = off / hd, j = off - head * hd;
+    int d0, d1;
+    float o0, o1;
+    if (j < rot) {
+        const int i = j >> 1;
+        d0 = i;
+        d1 = i + (rot >> 1);
+        const float cs = cs_tab[i], sn = sn_tab[i];
+        o0 = v0 * cs - v1 * sn;
+        o1 = v1 * cs + v0 * sn;
+    } else {
+        d0 = j;
+        d1 = j + 1;
+        o0 = v0;
+        o1 = v1;
+    }
+    if (is_q) {
+        p.q_out[head * hd + d0] = o0;
+        p.q_out[head * hd + d1] = o1;
+    } else {
+        size_t base = (size_t)pos * p.kv_dim + (size_t)head * hd;
+        store_cache(p.k_cache, p.cache_dtype, base + d0, o0);
+        store_cache(p.k_cache, p.cache_dtype, base + d1, o1);
+    }
+}
+
+// Per-row values an item's epilogue needs, loaded with the item's weights. A lane holds the
+// values of the rows it finalises: row r0 + r for lane mr * R + r (store / residual), or rows
+// r0 + 2j and r0 + 2j + 1 for lane j (SwiGLU and q|k|v pairs). Absent operands are read from a
+// valid address and multiplied by 0, so the load count never depends on the arguments.
+struct Side {
+    uint32_t s0 = 0, s1 = 0;  // fp16 scale bits (int8 weights)
+    float b0 = 0.f, b1 = 0.f;  // bias
+    float res = 0.f;           // residual
+};
+
+template <int WT, int R, int MR, int EPI>
+__device__ __forceinline__ Side load_side(const GemvParams& p, int group, int lane, const float* any) {
+    Side sd;
+    const float has_bias = p.bias ? 1.f : 0.f;
+    if constexpr (EPI == EPI_STORE) {
+        const int r = lane % R, mr = min(lane / R, MR - 1);
+        const int row = min(group * R + r, p.n - 1);
+        if constexpr (WT == L0H_I8PC) sd.s0 = p.scales[row];
+        sd.b0 = *(p.bias ? p.bias + row : any) * has_bias;
+        sd.res = *(p.resid ? p.resid + (size_t)mr * p.n + row : any) * (p.resid ? 1.f : 0.f);
+    } else {
+        const int j = min(lane, R / 2 - 1);
+        const int row = min(group * R + 2 * j, p.n - 2);
+        if constexpr (WT == L0H_I8PC) {
+            sd.s0 = p.scales[row];
+            sd.s1 = p.scales[row + 1];
+        }
+        sd.b0 = *(p.bias ? p.bias + row : any) * has_bias;
+        sd.b1 = *(p.bias ? p.bias + row + 1 : any) * has_bias;
+    }
+    return sd;
+}
+
+// WT weight type, R rows per wave item, U chunks per row per lane in an item, MR activation
+// rows, KX 16-byte activation chunks staged per thread (MR == 1), NORM: RMSNorm prologue,
+// EPI: EPI_STORE (store or residual, chosen at run time), EPI_SWIGLU or EPI_QKV.
+template <int WT, int R, int U, int MR, int KX, bool NORM, int EPI>
+__global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p, int k_pad) {
+    extern __shared__ float4 smem4[];
+    float* xs = reinterpret_cast<float*>(smem4);  // [MR, k_pad], zero past K
+    __shared__ float red[2 * kWaves];
+    __shared__ float xsum_s[MR];
+    __shared__ float rope_cs[EPI == EPI_QKV ? kMaxRotaryHalf : 1];
+    __shared__ float rope_sn[EPI == EPI_QKV ? kMaxRotaryHalf : 1];
+    constexpr int EPC = WTraits<WT>::kElems;
+    constexpr int KB = 64 * U;  // chunks per batch
+    const int K = p.k, N = p.n;
+    const int C = K / EPC;
+    const int nb = (C + KB - 1) / KB;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar control flow
+    const int W = gridDim.x * kWaves;
+    const int ngroups = (N + R - 1) / R;
+    const char* wbase = static_cast<const char*>(p.w);
+    const size_t row_bytes = (size_t)K * WTraits<WT>::kBytes;
+    const float* any = static_cast<const float*>(p.x);
+
+    auto load_w = [&](uint4 (&w)[U][R], int group, int batch) {
+        const int grp = min(group, ngroups - 1);
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint4* rp = reinterpret_cast<const uint4*>(wbase + (size_t)min(grp * R + r, N - 1) * row_bytes);
+#pragma unroll
+            for (int u = 0; u < U; u++) w[u][r] = ld_nt16(rp + min(batch * KB + u * 64 + lane, C - 1));
+        }
+    };
+
+    // ---- several activation rows: staged before any weight load (not the decode path) ----
+    if constexpr (MR > 1) {
+#pragma unroll
+        for (int mr = 0; mr < MR; mr++) {
+            float* dst = xs + (size_t)mr * k_pad;
+            float xsum = 0.f;
+            for (int i = tid; i < k_pad; i += kBlock) {
+                const float v = i < K ? load_act(p.x, p.x_dtype, (size_t)mr * K + i) : 0.f;
+                dst[i] = v;
+                xsum += v;
+            }
+            if constexpr (WT == L0H_I8PC) {
+                xsum = block_sum(xsum, red);
+                if (tid == 0) xsum_s[mr] = xsum;
+            }
+        }
+    }
+
+    // ---- one activation row: prologue loads first (x, norm weights, RoPE frequencies) ----
+    uint4 xr[KX], nr[NORM ? KX : 1];
+    const int xdt = p.x_dtype;
+    const int nxc = (int)((size_t)K * dtype_size(xdt) / 16);  // 16-byte chunks of x
+    if constexpr (MR == 1) {
+        const uint4* xp = static_cast<const uint4*>(p.x);
+#pragma unroll
+        for (int i = 0; i < KX; i++) xr[i] = xp[min(i * kBlock + tid, nxc - 1)];
+        if constexpr (NORM) {
+            const uint4* np = reinterpret_cast<const uint4*>(p.norm_w);
+#pragma unroll
+            for (int i = 0; i < KX; i++) nr[i] = np[min(i * kBlock + tid, K / 4 - 1)];
+        }
+    }
+    float inv_f = 0.f;
+    int pos = 0;
+    if constexpr (EPI == EPI_QKV) {
+        inv_f = p.inv_freq[min(tid, p.rotary_dim / 2 - 1)];
+        pos = *p.position;
+    }
+
+    // ---- first weight item, issued once every wave of the block has issued its activation loads:
+    // a CU's memory pipeline returns data in order, so the activations come back ahead of the
+    // block's weight stream and are staged while the weights are in flight ----
+    __builtin_amdgcn_s_barrier();
+    int g = blockIdx.x * kWaves + wave;
+    uint4 wa[U][R], wb[U][R];
+    Side sa, sb;
+    sa = load_side<WT, R, MR, EPI>(p, min(g, ngroups - 1), lane, any);
+    load_w(wa, g, 0);
+
+    // ---- stage the one activation row (and RMSNorm) in LDS ----
+    if constexpr (MR == 1) {
+        // One pass: sum of squares (RMSNorm) and the sum of the values the dot products will use
+        // (the int8 bias correction), reduced together; then x * scale * w goes to LDS.
+        float ss = 0.f, xw = 0.f;
+#pragma unroll
+        for (int i = 0; i < KX; i++) {
+            float f[8];
+            const int n = chunk_to_float(xr[i], xdt, f);
+            if (i * kBlock + tid < nxc) {
+                if constexpr (NORM) {  // x is fp32 here: 4 values, matching the 4 norm weights
+                    const float nw[4] = {__uint_as_float(nr[i].x), __uint_as_float(nr[i].y), __uint_as_float(nr[i].z),
+                                         __uint_as_float(nr[i].w)};
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        ss += f[e] * f[e];
+                        xw += f[e] * nw[e];
+                    }
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; e++)
+                        if (e < n) xw += f[e];
+                }
+            }
+        }
+        float scale = 1.f;
+        if constexpr (NORM || WT == L0H_I8PC) {
+            const float2 t = block_sum2(ss, xw, red);
+            if constexpr (NORM) scale = rsqrtf(t.x / (float)K + p.eps);
+            if (tid == 0) xsum_s[0] = scale * t.y;
+        }
+#pragma unroll
+        for (int i = 0; i < KX; i++) {
+            const int idx = i * kBlock + tid;
+            if (idx < nxc) {
+                float f[8];
+                const int n = chunk_to_float(xr[i], xdt, f);
+                if constexpr (NORM) {
+                    f[0] *= scale * __uint_as_float(nr[i].x);
+                    f[1] *= scale * __uint_as_float(nr[i].y);
+                    f[2] *= scale * __uint_as_float(nr[i].z);
+                    f[3] *= scale * __uint_as_float(nr[i].w);
+                }
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                    if (e < n) xs[idx * n + e] = f[e];
+            }
+        }
+        for (int i = K + tid; i < k_pad; i += kBlock) xs[i] = 0.f;
+    }
+    if constexpr (EPI == EPI_QKV) {
+        // cos/sin of this position for every rotated pair, once per block (accurate sincos of
+        // the fp32 product pos * inv_freq[i]).
+        if (tid < p.rotary_dim / 2) {
+            float sn, cs;
+            sincosf((float)pos * inv_f, &sn, &cs);
+            rope_cs[tid] = cs * p.rope_scale;
+            rope_sn[tid] = sn * p.rope_scale;
+        }
+    }
+    lds_barrier();
+
+    // ---- stream: no barrier below this point, waves run independently ----
+    float acc[MR][R];
+#pragma unroll
+    for (int mr = 0; mr < MR; mr++)
+#pragma unroll
+        for (int r = 0; r < R; r++) acc[mr][r] = 0.f;
+
+    auto compute = [&](const uint4 (&w)[U][R], int batch) {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int c = batch * KB + u * 64 + lane;  // < nb * KB: x is zero past K
+#pragma unroll
+            for (int mr = 0; mr < MR; mr++) {
+                float xv[EPC];
+                const float4* xp = reinterpret_cast<const float4*>(xs + (size_t)mr * k_pad + (size_t)c * EPC);
+#pragma unroll
+                for (int q = 0; q < EPC / 4; q++) {
+                    float4 t = xp[q];
+                    xv[4 * q + 0] = t.x;
+                    xv[4 * q + 1] = t.y;
+                    xv[4 * q + 2] = t.z;
+                    xv[4 * q + 3] = t.w;
+                }
+#pragma unroll
+                for (int r = 0; r < R; r++) chunk_fma<WT>(w[u][r], xv, acc[mr][r]);
+            }
+        }
+    };
+
+    // Wave reduction and epilogue of row group `group`; resets the accumulators. No loads.
+    auto finish = [&](int group, const Side& sd) {
+        const int r0 = group * R;
+        float sums[MR][R];
+#pragma unroll
+        for (int mr = 0; mr < MR; mr++)
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                sums[mr][r] = wave_sum(acc[mr][r]);
+                acc[mr][r] = 0.f;
+            }
+        if constexpr (EPI == EPI_STORE) {
+#pragma unroll
+            for (int mr = 0; mr < MR; mr++)
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    const int row = r0 + r;
+                    if (lane == mr * R + r && row < N) {
+                        float v = sums[mr][r];
+                        if constexpr (WT == L0H_I8PC) v = (v - 128.0f * xsum_s[mr]) * half_bits(sd.s0);
+                        v += sd.b0;
+                        if (p.epilogue == EPI_STORE)
+                            store_act(p.y, p.y_dtype, (size_t)mr * N + row, v);
+                        else
+                            p.resid[(size_t)mr * N + row] = sd.res + v;
+                    }
+                }
+        } else {
+#pragma unroll
+            for (int j = 0; j < R / 2; j++) {
+                const int row = r0 + 2 * j;
+                if (lane == j && row + 1 < N) {
+                    float v0 = sums[0][2 * j], v1 = sums[0][2 * j + 1];
+                    if constexpr (WT == L0H_I8PC) {
+                        v0 = (v0 - 128.0f * xsum_s[0]) * half_bits(sd.s0);
+                        v1 = (v1 - 128.0f * xsum_s[0]) * half_bits(sd.s1);
+                    }
+                    v0 += sd.b0;
+                    v1 += sd.b1;
+                    if constexpr (EPI == EPI_SWIGLU)
+                        store_act(p.y, p.y_dtype, (size_t)(row >> 1), silu(v0) * v1);
+                    else
+                        qkv_pair(p, row, v0, v1, pos, rope_cs, rope_sn);
+                }
+            }
+        }
+    };
+
+    // Items of this wave: every batch of row groups g, g + W, ... < ngroups. Each pipeline step
+    // issues item i+1 into the other buffer, then computes item i and finishes its row group after
+    // its last batch; the last item is computed with nothing issued behind it (no re-read past the
+    // end). The branch to the last item comes before any load of its step, so the two paths never
+    // merge between a load and its use.
+    const int items = g < ngroups ? ((ngroups - 1 - g) / W + 1) * nb : 0;
+    int b = 0;  // batch of the current item
+    auto advance = [&](int& gg, int& bb) {
+        if (++bb == nb) {
+            bb = 0;
+            gg += W;
+        }
+    };
+    if (items > 0) {
+        int i = 0;
+        for (;;) {
+            if (i + 1 == items) {
+                compute(wa, b);
+                finish(g, sa);
+                break;
+            }
+            {
+                int gn = g, bn = b;
+                advance(gn, bn);
+                sb = load_side<WT, R, MR, EPI>(p, gn, lane, any);
+                load_w(wb, gn, bn);
+                compute(wa, b);
+                if (b == nb - 1) finish(g, sa);
+                g = gn;
+                b = bn;
+                i++;
+            }
+            if (i + 1 == items) {
+                compute(wb, b);
+                finish(g, sb);
+                break;
+            }
+            {
+                int gn = g, bn = b;
+                advance(gn, bn);
+                sa = load_side<WT, R, MR, EPI>(p, gn, lane, any);
+                load_w(wa, gn, bn);
+                compute(wb, b);
+                if (b == nb - 1) finish(g, sb);
+                g = gn;
+                b = bn;
+                i++;
+            }
+        }
+    }
+}
+
+// Zero-padded activation tile of the fast kernel: K rounded up to whole batches.
+template <int WT, int U>
+int padded_k(int k) {
+    constexpr int EPC = WTraits<WT>::kElems, KB = 64 * U;
+    const int nb = (k / EPC + KB - 1) / KB;
+    return nb * KB * EPC;
+}
+
+template <int WT, int R, int U, int MR, int KX, bool NORM, int EPI>
+int launch_fast(hipStream_t s, const GemvParams& p) {
+    const int k_pad = padded_k<WT, U>(p.k);
+    const size_t shmem = (size_t)MR * k_pad * sizeof(float);
+    if (shmem > kLdsBudget) return fail(L0H_ERR_UNSUPPORTED, "GEMV activation tile exceeds LDS");
+    auto kern = gemv_nk_kernel<WT, R, U, MR, KX, NORM, EPI>;
+    // The dynamic tile may reach 64 KiB on top of the static LDS: raise the limit once.
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsBudget);
+    if (attr != hipSuccess) return fail(L0H_ERR_DEVICE, std::string("hipFuncSetAttribute: ") + hipGetErrorString(attr));
+    const unsigned groups = ceil_div(p.n, R);
+    unsigned grid = ceil_div(groups, kWaves);
+    if (p.max_blocks > 0) {
+        // A persistent grid must be resident in one round: at most as many blocks per CU as the
+        // kernel's registers and this launch's LDS allow (queried once per instantiation and
+        // tile size).
+        static thread_local int occ_shmem = -1, occ_blocks = 0;
+        if (occ_shmem != (int)shmem) {
+            int nb = 0;
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void*>(kern), kBlock, shmem) != hipSuccess)
+                nb = 1;
+            occ_shmem = (int)shmem;
+            occ_blocks = std::max(1, nb);
+        }
+        const unsigned cap = std::min<unsigned>((unsigned)p.max_blocks, (unsigned)(occ_blocks * std::max(1, p.compute_units)));
+        grid = std::min(grid, cap);
+    }
+    kern<<<grid, kBlock, shmem, s>>>(p, k_pad);
+    return launch_status("gemv_nk");
+}
+
+// One activation row: the fused epilogues and the RMSNorm prologue live here.
+template <int WT, int R, int U, int KX>
+int dispatch_one(hipStream_t s, const GemvParams& p) {
+    switch (p.epilogue) {
+    case EPI_SWIGLU: return launch_fast<WT, R, U, 1, KX, true, EPI_SWIGLU>(s, p);
+    case EPI_QKV: return launch_fast<WT, R, U, 1, KX, true, EPI_QKV>(s, p);
+    default:
+        return p.norm_w ? launch_fast<WT, R, U, 1, KX, true, EPI_STORE>(s, p)
+                        : launch_fast<WT, R, U, 1, KX, false, EPI_STORE>(s, p);
+    }
+}
+
+// Activation chunks per thread of a 256-thread block, rounded up to a power of two (<= 16).
+int staged_chunks(const GemvParams& p) {
+    const size_t chunks = (size_t)p.k * dtype_size(p.x_dtype) / 16;
+    const size_t per = (chunks + kBlock - 1) / kBlock;
+    int kx = 1;
+    while ((size_t)kx < per) kx <<= 1;
+    return kx;
+}
+
+template <int WT, int R, int U>
+int dispatch_mr(hipStream_t s, const GemvParams& p, int mr) {
+    if (mr == 1) {
+        switch (staged_chunks(p)) {
+        case 1: return dispatch_one<WT, R, U, 1>(s, p);
+        case 2: return dispatch_one<WT, R, U, 2>(s, p);
+        case 4: return dispatch_one<WT, R, U, 4>(s, p);
+        case 8: return dispatch_one<WT, R, U, 8>(s, p);
+        case 16: return dispatch_one<WT, R, U, 16>(s, p);
+        default: return fail(L0H_ERR_UNSUPPORTED, "GEMV activation row exceeds 64 KiB");
+        }
+    }
+    if (mr == 2) return launch_fast<WT, R, U, 2, 1, false, EPI_STORE>(s, p);
+    if (mr == 4) return launch_fast<WT, R, U, 4, 1, false, EPI_STORE>(s, p);
+    return launch_fast<WT, R, U, 8, 1, false, EPI_STORE>(s, p);
+}
+
+// Rows per wave item (R) and 16-byte chunks per row per lane (U), chosen by the row length so an
+// item carries about 8 KiB of real weights for int8 (R * U KiB): C <= 64 chunks per row -> 8 rows
+// x 1 chunk per lane, C <= 128 -> 4 x 2, else 2 x 4. Several activation rows use 2 x 4.
+template <int WT>
+int dispatch_wt(hipStream_t s, const GemvParams& p, int mr) {
+    const int C = p.k / WTraits<WT>::kElems;
+    if (mr == 1 && C <= 64) return dispatch_mr<WT, 8, 1>(s, p, mr);
+    if (mr == 1 && C <= 128) return dispatch_mr<WT, 4, 2>(s, p, mr);
+    return dispatch_mr<WT, 2, 4>(s, p, mr);
+}
+
+}  // namespace
+
+// One-row / multi-row dispatch for one weight type (defined in gemv_<type>.hip).
+int gemv_dispatch_i8(hipStream_t s, const GemvParams& p, int mr);
+int gemv_dispatch_f16(hipStream_t s, const GemvParams& p, int mr);
+int gemv_dispatch_bf16(hipStream_t s, const GemvParams& p, int mr);
+int gemv_dispatch_f32(hipStream_t s, const GemvParams& p, int mr);
+
+}  // namespace l0h
