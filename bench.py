@@ -305,10 +305,14 @@ def main() -> int:
     launches = sum(table[k]["launches_per_step"] for k in GEMV_KINDS)
     achieved = gemv_bytes / (gemv_us * 1e-6) / 1e9
     step_bytes = sum(t["bytes_per_launch"] * t["launches_per_step"] for t in table.values())
+    # HBM bytes per int8 GEMV launch from the rocprofv3 FETCH_SIZE / WRITE_SIZE runs (calibrated
+    # against the copy kernel of known size), summarised in profiles/.
     traffic = None
-    tf = ROOT / "profiles" / "gemv_i8_traffic.json"
+    tf = ROOT / "profiles" / "gemv_int8_hbm_traffic.txt"
     if tf.exists():
-        traffic = json.loads(tf.read_text()).get("hbm_bytes_per_launch")
+        for line in tf.read_text().splitlines():
+            if line.startswith("hbm_bytes_per_launch:"):
+                traffic = int(line.split(":", 1)[1])
     log(f"int8 GEMV: {achieved:.0f} GB/s over {launches} launches/step ({gemv_us:.0f} us/step)")
 
     configs = None
