@@ -3,10 +3,29 @@
 //
 // Both operands are K-contiguous, which is the layout v_mfma_f32_16x16x32_{bf16,f16} wants:
 // lane l holds A[l % 16][8 (l / 16) .. +7] and B[8 (l / 16) .. +7][l % 16] and receives
-// D[4 (l / 16) + r][l % 16], r < 4. A block of 4 waves (2 x 2) computes a BM x BN tile; tiles
-// of BM x 64 and BN x 64 are staged in LDS (rows padded by 16 bytes against bank conflicts),
-// double-buffered so the next tile's global loads overlap the current tile's MFMAs. Small-M
-// shapes split K across blocks into fp32 partials that a second pass sums.
+// D[4 (l / 16) + r][l % 16], r < 4. So a lane's B operand for 16 columns and one K step of 32 is
+// 16 contiguous bytes of one weight row.
+//
+// A block of 4 waves computes BM rows x 4 NW columns; wave w owns NW columns and all BM rows.
+// The weights, which no two waves share, go from HBM straight into MFMA operand registers; only
+// the activation tile (BM x 32 per K step, read by all 4 waves) passes through LDS. That halves
+// the LDS traffic per MFMA against staging both operands (the LDS port, 128 bytes per clock per
+// CU, is what bounds a 64 x 64 wave tile with both operands in LDS). K steps pass through a ring
+// of P register stages: the loads of step t + P - 1 are issued while step t is computed, so P - 1
+// steps of weights are in flight per wave. Step t + 1's activation chunks go from their stage to
+// the LDS buffer the MFMAs are not reading (rows padded by 16 bytes, so the fragment reads of 16
+// rows hit distinct banks). Every global load is unconditional (rows past M / N and steps past
+// the end are clamped to valid addresses and never used), and the one barrier per step waits on
+// LDS only, so the in-order memory counter's waits are exact: the wait before step t + 1's
+// LDS store lets the P - 2 younger stages stay in flight.
+//
+// Shapes with fewer blocks than the GPU has CUs split K across blocks into fp32 partials that a
+// second pass sums in a fixed order (deterministic). Blocks are renumbered so the blocks that
+// read the same weight columns run on the same XCD (blocks are dealt to the 8 XCDs round robin),
+// where they share that XCD's L2.
+#include <type_traits>
+#include <utility>
+
 #include "kernels.h"
 
 namespace l0h {
@@ -15,119 +34,186 @@ namespace {
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
 typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(16))) float f32x16;
 
-constexpr int BK = 64;
-constexpr int kPad = 8;  // elements of padding per LDS row
+constexpr int BK = 32;     // K per step = one MFMA
+constexpr int kPad = 8;    // elements of padding per LDS row
 constexpr int kLds = BK + kPad;
+constexpr int kMaxSplits = 16;
+constexpr int kXcds = 8;
 
-template <int DT>
-__device__ __forceinline__ f32x4 mfma(const uint4& a, const uint4& b, f32x4 c) {
-    if constexpr (DT == L0H_BF16)
-        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-    else
-        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+// One MFMA of the MF x MF x (512 / MF) shape: MF = 16 (v_mfma_f32_16x16x32) or 32
+// (v_mfma_f32_32x32x16). The 32 x 32 form reaches the MFMA peak with a few independent
+// accumulators per wave; the 16 x 16 form needs about twice as many waves or accumulators.
+template <int MF>
+using acc_t = typename std::conditional<MF == 16, f32x4, f32x16>::type;
+
+template <int DT, int MF>
+__device__ __forceinline__ acc_t<MF> mfma(const uint4& a, const uint4& b, acc_t<MF> c) {
+    if constexpr (MF == 16) {
+        if constexpr (DT == L0H_BF16)
+            return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+        else
+            return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+    } else {
+        if constexpr (DT == L0H_BF16)
+            return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+        else
+            return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+    }
 }
 
-// BM x BN block tile, 2 x 2 waves, each (BM/2) x (BN/2) = TM x TN MFMA tiles.
-template <int DT, int BM, int BN>
-__global__ __launch_bounds__(256) void gemm_nk_kernel(int M, int N, int K, int k_per_split,
-                                                      const uint16_t* __restrict__ X,
-                                                      const uint16_t* __restrict__ W, void* Y,
-                                                      int y_dtype, float* partial) {
-    constexpr int TM = BM / 32, TN = BN / 32;
-    constexpr int A_CHUNKS = BM * BK / 8 / 256;  // 16-byte chunks per thread per tile
-    constexpr int B_CHUNKS = BN * BK / 8 / 256;
+// Barrier for LDS hand-offs only: waits for this wave's LDS operations, not its global loads.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// f(integral_constant<int, 0>), ..., f(integral_constant<int, N - 1>): ring stage indices are
+// constants in each call, so the stages stay in registers.
+template <class F, int... I>
+__device__ __forceinline__ void for_each_index_impl(F&& f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void for_each_index(F&& f) {
+    for_each_index_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// Row blocks per group in the block order: all of them up to 8, else the largest power of two
+// up to 8 that divides the count.
+__device__ __forceinline__ int row_group(int gx) {
+    if (gx <= 8) return gx;
+    return gx % 8 == 0 ? 8 : gx % 4 == 0 ? 4 : gx % 2 == 0 ? 2 : 1;
+}
+
+// Ring depth: deeper for tiles with fewer registers per stage, within a budget of 256 registers
+// per lane (two waves per SIMD) for all but the 128 x 64 wave tile.
+constexpr int ring_depth(int bm, int nw) { return nw == 64 ? 4 : (bm == 64 && nw == 16) ? 8 : 6; }
+
+template <int DT, int BM, int NW, bool NT, int P = ring_depth(BM, NW), int MF = (NW % 32 == 0 ? 32 : 16)>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void gemm_nk_kernel(
+    int M, int N, int K, int k_per_split, const uint16_t* __restrict__ X, const uint16_t* __restrict__ W,
+    void* Y, int y_dtype, float* partial) {
+    constexpr int S = BK * MF / 512;       // MFMAs per K step (k of one MFMA = 512 / MF)
+    constexpr int MI = BM / MF;            // MF-row A fragments
+    constexpr int NJ = NW / MF;            // MF-column B fragments per wave
+    constexpr int NB = NJ * S;             // B registers (16 bytes) per stage
+    constexpr int AC = BM * BK / 8 / 256;  // 16-byte A chunks per thread per step
+    static_assert(AC >= 1 && MI >= 1 && NJ >= 1, "tile too small");
     __shared__ __attribute__((aligned(16))) uint16_t sa[2][BM * kLds];
-    __shared__ __attribute__((aligned(16))) uint16_t sb[2][BN * kLds];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-    const int kbeg = blockIdx.z * k_per_split;
-    const int kend = min(K, kbeg + k_per_split);
-    const int ntiles = (kend - kbeg) / BK;
+    // Renumber blocks so that consecutive ids land on one XCD, then walk them as groups of G row
+    // blocks: rows of the group first, then K splits, then column blocks, then the next group.
+    // The blocks an XCD runs together thus share G activation slabs and about 32 / G weight slabs.
+    const int gx = gridDim.x, gy = gridDim.y, gz = gridDim.z;
+    const int total = gx * gy * gz;
+    int lin = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
+    if (total % kXcds == 0) lin = (lin % kXcds) * (total / kXcds) + lin / kXcds;
+    const int G = row_group(gx);
+    const int gr = lin % G, rest = lin / G;
+    const int bz = rest % gy, bn = (rest / gy) % gz, bm = (rest / (gy * gz)) * G + gr;
+    const int m0 = bm * BM, nw0 = bn * 4 * NW + wave * NW;
+    const int kbeg = bz * k_per_split;
+    const int nsteps = max(0, min(K, kbeg + k_per_split) - kbeg) / BK;
+    const int last = max(nsteps - 1, 0);
 
-    uint4 ra[A_CHUNKS], rb[B_CHUNKS];
-    auto gload = [&](int kt) {
-        const int k0 = kbeg + kt * BK;
+    // Operand lane layout: lane l holds row / column l % MF and, of MFMA s of the step, the 8
+    // K values from s (512 / MF) + 8 (l / MF).
+    const int li = lane % MF, lk = (lane / MF) * 8;
+    const uint16_t* bptr[NB];
 #pragma unroll
-        for (int c = 0; c < A_CHUNKS; c++) {
-            const int idx = tid + c * 256;
-            const int r = idx >> 3, kc = (idx & 7) * 8;
-            const int row = m0 + r;
-            ra[c] = row < M ? *reinterpret_cast<const uint4*>(X + (size_t)row * K + k0 + kc) : make_uint4(0u, 0u, 0u, 0u);
-        }
+    for (int j = 0; j < NJ; j++)
 #pragma unroll
-        for (int c = 0; c < B_CHUNKS; c++) {
-            const int idx = tid + c * 256;
-            const int r = idx >> 3, kc = (idx & 7) * 8;
-            const int row = n0 + r;
-            rb[c] = row < N ? ld_nt16(W + (size_t)row * K + k0 + kc)
-                            : make_uint4(0u, 0u, 0u, 0u);
+        for (int q = 0; q < S; q++)
+            bptr[j * S + q] = W + (size_t)min(nw0 + j * MF + li, N - 1) * K + kbeg + q * (512 / MF) + lk;
+    const uint16_t* aptr[AC];
+#pragma unroll
+    for (int c = 0; c < AC; c++) {
+        const int idx = tid + c * 256;
+        aptr[c] = X + (size_t)min(m0 + (idx >> 2), M - 1) * K + kbeg + (idx & 3) * 8;
+    }
+
+    uint4 ra[P][AC], rb[P][NB];
+    // Step t of this block's K range into a ring stage; steps past the end re-read the last one.
+    auto gload = [&](uint4 (&a)[AC], uint4 (&b)[NB], int t) {
+        const int k0 = min(t, last) * BK;
+#pragma unroll
+        for (int c = 0; c < AC; c++) a[c] = *reinterpret_cast<const uint4*>(aptr[c] + k0);
+#pragma unroll
+        for (int j = 0; j < NB; j++) {
+            if constexpr (NT)
+                b[j] = ld_nt16(bptr[j] + k0);
+            else
+                b[j] = *reinterpret_cast<const uint4*>(bptr[j] + k0);
         }
     };
-    auto sstore = [&](int buf) {
+    auto sstore = [&](const uint4 (&a)[AC], int buf) {
 #pragma unroll
-        for (int c = 0; c < A_CHUNKS; c++) {
+        for (int c = 0; c < AC; c++) {
             const int idx = tid + c * 256;
-            const int r = idx >> 3, kc = (idx & 7) * 8;
-            *reinterpret_cast<uint4*>(&sa[buf][r * kLds + kc]) = ra[c];
-        }
-#pragma unroll
-        for (int c = 0; c < B_CHUNKS; c++) {
-            const int idx = tid + c * 256;
-            const int r = idx >> 3, kc = (idx & 7) * 8;
-            *reinterpret_cast<uint4*>(&sb[buf][r * kLds + kc]) = rb[c];
+            // As a vector value: a struct copy would keep the ring in memory instead of registers.
+            *reinterpret_cast<u32x4_t*>(&sa[buf][(idx >> 2) * kLds + (idx & 3) * 8]) =
+                u32x4_t{a[c].x, a[c].y, a[c].z, a[c].w};
         }
     };
 
-    f32x4 acc[TM][TN];
+    acc_t<MF> acc[MI][NJ];
 #pragma unroll
-    for (int i = 0; i < TM; i++)
+    for (int i = 0; i < MI; i++)
 #pragma unroll
-        for (int j = 0; j < TN; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < NJ; j++) acc[i][j] = acc_t<MF>{};
 
-    const int li = lane & 15, lk = (lane >> 4) * 8;
-    if (ntiles > 0) {
-        gload(0);
-        sstore(0);
-        __syncthreads();
-        for (int kt = 0; kt < ntiles; kt++) {
-            const int buf = kt & 1;
-            if (kt + 1 < ntiles) gload(kt + 1);
+    auto mma = [&](int buf, const uint4 (&b)[NB]) {
 #pragma unroll
-            for (int ks = 0; ks < BK; ks += 32) {
-                uint4 af[TM], bf[TN];
+        for (int q = 0; q < S; q++) {
 #pragma unroll
-                for (int i = 0; i < TM; i++)
-                    af[i] = *reinterpret_cast<const uint4*>(&sa[buf][(wm * (BM / 2) + i * 16 + li) * kLds + ks + lk]);
+            for (int i = 0; i < MI; i++) {
+                const uint4 af = *reinterpret_cast<const uint4*>(&sa[buf][(i * MF + li) * kLds + q * (512 / MF) + lk]);
 #pragma unroll
-                for (int j = 0; j < TN; j++)
-                    bf[j] = *reinterpret_cast<const uint4*>(&sb[buf][(wn * (BN / 2) + j * 16 + li) * kLds + ks + lk]);
-#pragma unroll
-                for (int i = 0; i < TM; i++)
-#pragma unroll
-                    for (int j = 0; j < TN; j++) acc[i][j] = mfma<DT>(af[i], bf[j], acc[i][j]);
+                for (int j = 0; j < NJ; j++) acc[i][j] = mfma<DT, MF>(af, b[j * S + q], acc[i][j]);
             }
-            if (kt + 1 < ntiles) sstore(buf ^ 1);
-            __syncthreads();
+        }
+    };
+
+    if (nsteps > 0) {
+        // Prologue: steps 0 .. P-2 in flight, step 0's activations into LDS buffer 0.
+        for_each_index<P - 1>([&](auto sc) { gload(ra[sc.value], rb[sc.value], sc.value); });
+        sstore(ra[0], 0);
+        lds_barrier();
+        // Step t: issue step t + P - 1 into stage (t + P - 1) % P, move step t + 1's activations
+        // into LDS buffer (t + 1) % 2, compute step t from buffer t % 2 and stage t % P's weights.
+        // Unrolled by P so the stages are registers.
+        for (int t0 = 0; t0 < nsteps; t0 += P) {
+            for_each_index<P>([&](auto jc) {
+                constexpr int j = decltype(jc)::value;
+                const int t = t0 + j;
+                gload(ra[(j + P - 1) % P], rb[(j + P - 1) % P], t + P - 1);
+                sstore(ra[(j + 1) % P], (t + 1) & 1);  // past the end: unread, harmless
+                if (t < nsteps) mma(t & 1, rb[j]);
+                lds_barrier();
+            });
         }
     }
 
-    // D[4 (l/16) + r][l % 16] of each 16 x 16 tile.
-    const int rq = (lane >> 4) * 4;
+    // Accumulator register r of lane l holds D[row][l % MF] with row = 4 (l / 16) + r for
+    // MF = 16 and row = 8 (r / 4) + 4 (l / 32) + r % 4 for MF = 32.
+    constexpr int R = MF == 16 ? 4 : 16;
 #pragma unroll
-    for (int i = 0; i < TM; i++) {
+    for (int i = 0; i < MI; i++) {
 #pragma unroll
-        for (int j = 0; j < TN; j++) {
-            const int col = n0 + wn * (BN / 2) + j * 16 + li;
+        for (int j = 0; j < NJ; j++) {
+            const int col = nw0 + j * MF + li;
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int row = m0 + wm * (BM / 2) + i * 16 + rq + r;
+            for (int r = 0; r < R; r++) {
+                const int rr = MF == 16 ? (lane / 16) * 4 + r : (r / 4) * 8 + (lane / 32) * 4 + (r % 4);
+                const int row = m0 + i * MF + rr;
                 if (row < M && col < N) {
                     const float v = acc[i][j][r];
                     if (partial)
-                        partial[((size_t)blockIdx.z * M + row) * N + col] = v;
+                        partial[((size_t)bz * M + row) * N + col] = v;
                     else
                         store_act(Y, y_dtype, (size_t)row * N + col, v);
                 }
@@ -144,7 +230,7 @@ __global__ void splitk_reduce_kernel(const float* partial, int splits, size_t mn
     store_act(Y, y_dtype, i, s);
 }
 
-// Any shape (K not a multiple of 64): one thread per output, fp32 accumulation.
+// Any shape (K not a multiple of 32): one thread per output, fp32 accumulation.
 __global__ void gemm_nk_generic_kernel(int dt, int M, int N, int K, const uint16_t* X, const uint16_t* W,
                                        void* Y, int y_dtype) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -160,14 +246,48 @@ __global__ void gemm_nk_generic_kernel(int dt, int M, int N, int K, const uint16
     store_act(Y, y_dtype, i, acc);
 }
 
-template <int DT, int BM, int BN>
+struct Plan {
+    int bm = 128, nw = 64, splits = 1;
+};
+
+// Tile and split-K choice (from a sweep over the Llama-3.2-1B prefill shapes and square ones on
+// MI355X). Tiles are tried from the largest (fewest L1 bytes per flop) down; a tile is taken with
+// the smallest power-of-two K split that gives about one block per CU (3/4 of the CUs or more)
+// while each split keeps at least 64 K steps (no split needs none). When no tile gets there, the smallest tile is split
+// further, down to two rings of K steps per split.
+Plan plan_for(int m, int n, int k, int cus) {
+    static const int tiles[][2] = {{128, 64}, {128, 32}, {128, 16}, {64, 64}, {64, 32}, {64, 16}};
+    const int steps = k / BK;
+    const size_t want = (size_t)cus * 3 / 4;
+    auto blocks = [&](int bm, int nw) { return (size_t)ceil_div(n, 4 * nw) * ceil_div(m, bm); };
+    for (const auto& t : tiles) {
+        if (m <= 64 && t[0] == 128) continue;
+        if (m > 64 && t[0] == 64 && t[1] == 64) continue;
+        const size_t b = blocks(t[0], t[1]);
+        for (int s = 1; s <= kMaxSplits && (s == 1 || steps / s >= 64); s *= 2)
+            if (b * s >= want) return Plan{t[0], t[1], s};
+    }
+    Plan p{64, 16, 1};
+    const size_t b = blocks(p.bm, p.nw);
+    while (p.splits < kMaxSplits && b * p.splits < want && steps / (p.splits * 2) >= 2 * ring_depth(p.bm, p.nw))
+        p.splits *= 2;
+    return p;
+}
+
+template <int DT, int BM, int NW>
 int launch_tiles(hipStream_t s, int m, int n, int k, const void* x, const void* w, void* y, int y_dtype,
                  int splits, float* ws) {
     const int k_per_split = (k / BK + splits - 1) / splits * BK;
-    dim3 grid(ceil_div(n, BN), ceil_div(m, BM), splits);
-    gemm_nk_kernel<DT, BM, BN><<<grid, 256, 0, s>>>(m, n, k, k_per_split, static_cast<const uint16_t*>(x),
-                                                    static_cast<const uint16_t*>(w), y, y_dtype,
-                                                    splits > 1 ? ws : nullptr);
+    // The kernel decodes (row block, split, column block) from the linear block id; the grid only
+    // has to hold that many blocks, in the order x = row blocks, y = splits, z = column blocks.
+    dim3 grid(ceil_div(m, BM), splits, ceil_div(n, 4 * NW));
+    const auto* xp = static_cast<const uint16_t*>(x);
+    const auto* wp = static_cast<const uint16_t*>(w);
+    float* part = splits > 1 ? ws : nullptr;
+    if (grid.x == 1)  // each weight byte is read by one block: stream it past the caches
+        gemm_nk_kernel<DT, BM, NW, true><<<grid, 256, 0, s>>>(m, n, k, k_per_split, xp, wp, y, y_dtype, part);
+    else
+        gemm_nk_kernel<DT, BM, NW, false><<<grid, 256, 0, s>>>(m, n, k, k_per_split, xp, wp, y, y_dtype, part);
     int st = launch_status("gemm_nk");
     if (st || splits == 1) return st;
     const size_t mn = (size_t)m * n;
@@ -176,24 +296,26 @@ int launch_tiles(hipStream_t s, int m, int n, int k, const void* x, const void* 
 }
 
 template <int DT>
-int dispatch(hipStream_t s, int m, int n, int k, const void* x, const void* w, void* y, int y_dtype,
-             float* ws, size_t ws_bytes, int cus) {
-    // Tile choice: large M uses 128 x 128; small M 64 x 64 tiles with split-K to fill the CUs.
-    if (m >= 256) {
-        return launch_tiles<DT, 128, 128>(s, m, n, k, x, w, y, y_dtype, 1, ws);
-    }
-    const size_t blocks = (size_t)ceil_div(n, 64) * ceil_div(m, 64);
-    int splits = 1;
-    while (blocks * splits < (size_t)cus * 2 && (k / BK) / (splits * 2) >= 4) splits *= 2;
-    while (splits > 1 && (size_t)splits * m * n * sizeof(float) > ws_bytes) splits /= 2;
-    return launch_tiles<DT, 64, 64>(s, m, n, k, x, w, y, y_dtype, splits, ws);
+int launch_plan(hipStream_t s, const Plan& p, int m, int n, int k, const void* x, const void* w, void* y,
+                int y_dtype, float* ws) {
+#define L0H_GEMM_CASE(BM_, NW_) \
+    if (p.bm == BM_ && p.nw == NW_) return launch_tiles<DT, BM_, NW_>(s, m, n, k, x, w, y, y_dtype, p.splits, ws);
+    L0H_GEMM_CASE(64, 16)
+    L0H_GEMM_CASE(64, 32)
+    L0H_GEMM_CASE(64, 64)
+    L0H_GEMM_CASE(128, 16)
+    L0H_GEMM_CASE(128, 32)
+    L0H_GEMM_CASE(128, 64)
+#undef L0H_GEMM_CASE
+    return fail(L0H_ERR_UNSUPPORTED, "no GEMM tile for this plan");
 }
 
 }  // namespace
 
-size_t gemm_workspace_bytes(int m, int n, int k) {
-    if (m >= 256 || k % BK) return 0;
-    return (size_t)16 * m * n * sizeof(float);
+size_t gemm_workspace_bytes(int m, int n, int k, int compute_units) {
+    if (k % BK) return 0;
+    const Plan p = plan_for(m, n, k, compute_units);
+    return p.splits > 1 ? (size_t)p.splits * m * n * sizeof(float) : 0;
 }
 
 int launch_gemm_nk(hipStream_t s, int dtype, int m, int n, int k, const void* x, const void* w,
@@ -207,8 +329,10 @@ int launch_gemm_nk(hipStream_t s, int dtype, int m, int n, int k, const void* x,
                                                                  static_cast<const uint16_t*>(w), y, y_dtype);
         return launch_status("gemm_nk_generic");
     }
-    return dtype == L0H_BF16 ? dispatch<L0H_BF16>(s, m, n, k, x, w, y, y_dtype, ws, ws_bytes, cus)
-                             : dispatch<L0H_F16>(s, m, n, k, x, w, y, y_dtype, ws, ws_bytes, cus);
+    Plan p = plan_for(m, n, k, cus);
+    while (p.splits > 1 && (size_t)p.splits * m * n * sizeof(float) > ws_bytes) p.splits /= 2;
+    return dtype == L0H_BF16 ? launch_plan<L0H_BF16>(s, p, m, n, k, x, w, y, y_dtype, ws)
+                             : launch_plan<L0H_F16>(s, p, m, n, k, x, w, y, y_dtype, ws);
 }
 
 }  // namespace l0h

@@ -114,7 +114,7 @@ int launch_attention_prefill(hipStream_t s, AttnParams p, int pos0, int tokens);
 
 // MFMA GEMM Y[M,N] = X[M,K] * W[N,K]^T (f16 or bf16 operands).
 // Small M splits K into fp32 partials in `ws` (gemm_workspace_bytes) when it fits.
-size_t gemm_workspace_bytes(int m, int n, int k);
+size_t gemm_workspace_bytes(int m, int n, int k, int compute_units);
 int launch_gemm_nk(hipStream_t s, int dtype, int m, int n, int k, const void* x, const void* w,
                    void* y, int y_dtype, float* ws, size_t ws_bytes, int compute_units);
 

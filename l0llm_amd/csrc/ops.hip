@@ -236,7 +236,7 @@ int l0h_gemm_nk(l0h_device* dev, int dtype, int m, int n, int k, const void* x, 
     L0H_CHECK_ARG(x && w && y, "null buffer");
     L0H_CHECK_ARG(y_dtype >= L0H_F32 && y_dtype <= L0H_BF16, "output is F32, F16 or BF16");
     L0H_CHECK_ARG(m > 0 && n > 0 && k > 0, "sizes must be positive");
-    const size_t ws = gemm_workspace_bytes(m, n, k);
+    const size_t ws = gemm_workspace_bytes(m, n, k, dev->compute_units);
     if (ws) {
         int st = ensure_workspace(dev, ws, 0);
         if (st) return st;
