@@ -194,6 +194,12 @@ int l0h_gemv_nk(l0h_device* dev, int w_dtype, int rows, int out_dim, int in_dim,
  * ProjectRows of LlmMatrix.cs:149-171 for M >= 64. */
 int l0h_gemm_nk(l0h_device* dev, int dtype, int m, int n, int k, const void* x, const void* w,
                 void* y, int y_dtype);
+/* Prefill GEMM on MFMA with int8 weight-only per-row weights (the chunked-prefill role of
+ * LlmMatrix.ProjectRows, LlmMatrix.cs:149-171, for Int8 storage): Y[M, N] = (X[M, K] *
+ * W[N, K]^T) * scales[n], X L0H_F16, W int8, scales fp16, fp32 accumulation, y_dtype L0H_F32,
+ * L0H_F16 or L0H_BF16. K must be a multiple of 32. */
+int l0h_gemm_nk_i8pc(l0h_device* dev, int m, int n, int k, const void* x, const int8_t* w,
+                     const uint16_t* scales, void* y, int y_dtype);
 /* Batched GQA decode attention (Attention.Execute generalised to a batch; LlmDecoderLayer.cs:325-327).
  * q: [batch, n_heads*head_dim] (q_dtype L0H_F32 or L0H_F16); caches: [batch, max_seq_len,
  * n_kv_heads*head_dim] of cache_dtype; out: [batch, n_heads*head_dim] of out_dtype. Each

@@ -232,6 +232,10 @@ class LlmKernelSuite:
     def gemm_nk(self, dtype, m, n, k, x, w, y, y_dtype):
         check(lib.l0h_gemm_nk(self.device.handle, dtype, m, n, k, _ptr(x), _ptr(w), _ptr(y), y_dtype))
 
+    def gemm_nk_i8pc(self, m, n, k, x, w, scales, y, y_dtype):
+        """x fp16 [m, k], w int8 [n, k], scales fp16 [n]."""
+        check(lib.l0h_gemm_nk_i8pc(self.device.handle, m, n, k, _ptr(x), _ptr(w), _ptr(scales), _ptr(y), y_dtype))
+
     def attention_decode(self, q, q_dtype, k_cache, v_cache, cache_dtype, out, out_dtype, batch, head_dim, n_heads,
                          n_kv, seq_len, max_seq_len):
         check(lib.l0h_attention_decode(self.device.handle, _ptr(q), q_dtype, _ptr(k_cache), _ptr(v_cache),

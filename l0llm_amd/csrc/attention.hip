@@ -452,6 +452,254 @@ int launch_any(hipStream_t s, const AttnParams& p, int seq_len_step, size_t cach
     }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Causal prefill (Attention.ExecutePrefill, LlmDecoderLayer.cs:369-371), query-tiled: block
+// (query tile, kv head) holds 64 query vectors (64 / G tokens x the G q heads of the group) in LDS
+// and streams that kv head's K and V rows in tiles of 64 positions through LDS once for all of
+// them, so the cache is read once per tile of tokens instead of once per token. Scores, the online
+// softmax (fp32, log2 domain, as in the decode kernel) and P.V run on fp32 FMAs: thread
+// (ti, tj) = (tid / 16, tid % 16) owns query rows ti + 16 a and key columns tj + 16 b (a, b < 4),
+// and output dims 4 tj + 64 e; a row's 16 threads are 16 consecutive lanes, reduced by lane
+// shuffles. The next K/V tile is loaded into registers while the current one is computed; rows
+// past a query's position (and the tile padding) are clamped to valid cache rows and masked.
+// ---------------------------------------------------------------------------------------------
+constexpr int kPQ = 64;  // query vectors per block
+constexpr int kPK = 64;  // key positions per tile
+
+template <int HD>
+constexpr size_t prefill_smem_bytes() { return (size_t)(3 * 64 * (HD + 4) + 64 * (kPK + 4)) * sizeof(float); }
+
+__device__ __forceinline__ float row16_max(float v) {
+#pragma unroll
+    for (int o = 8; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 16));
+    return v;
+}
+__device__ __forceinline__ float row16_sum(float v) {
+#pragma unroll
+    for (int o = 8; o >= 1; o >>= 1) v += __shfl_xor(v, o, 16);
+    return v;
+}
+
+template <int HD, int CT, int QT>
+__global__ __launch_bounds__(kBlock) void attn_prefill_tiled_kernel(const AttnParams p, int pos0, int tokens,
+                                                                    int gsize, int tq_tokens) {
+    extern __shared__ __attribute__((aligned(16))) float smem[];
+    constexpr int LD = HD + 4;     // row stride of the Q, K and V tiles (16-byte aligned rows)
+    constexpr int SLD = kPK + 4;   // row stride of the probability tile
+    constexpr int E = HD / 64;     // float4 output chunks per thread
+    constexpr int ES = CT == L0H_F16 ? 2 : 4;
+    constexpr int CPR = HD * ES / 16;            // 16-byte chunks per cache row
+    constexpr int NC = kPK * CPR / kBlock;       // chunks per thread per tile (K, and again V)
+    static_assert(NC >= 1 && (kPK * CPR) % kBlock == 0, "tile / block mismatch");
+    float* Qs = smem;
+    float* Ks = Qs + kPQ * LD;
+    float* Vs = Ks + kPK * LD;
+    float* Ps = Vs + kPK * LD;
+
+    const int tid = threadIdx.x, ti = tid >> 4, tj = tid & 15;
+    const int g = blockIdx.y;
+    const int t0 = blockIdx.x * tq_tokens;
+    const int t_last = min(t0 + tq_tokens, tokens) - 1;
+    const int kmax = pos0 + t_last;  // last key position any query of the tile sees
+    const int row_elems = p.nkv * HD;
+    const typename CacheRow<CT>::T* kc = static_cast<const typename CacheRow<CT>::T*>(p.kc);
+    const typename CacheRow<CT>::T* vc = static_cast<const typename CacheRow<CT>::T*>(p.vc);
+
+    // Query vector i = token (t0 + i / gsize), head g * gsize + i % gsize; scaled by
+    // log2(e) / sqrt(HD). Vectors past the tile are zero and never written.
+    const float qscale = 1.4426950408889634f / sqrtf((float)HD);
+    for (int c = tid; c < kPQ * (HD / 8); c += kBlock) {
+        const int i = c / (HD / 8), d = (c % (HD / 8)) * 8;
+        const int tq = i / gsize, t = t0 + tq;
+        float f[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        if (tq < tq_tokens && t < tokens) {
+            load8<QT>(p.q, (size_t)t * p.nh * HD + (size_t)(g * gsize + i % gsize) * HD + d, f);
+#pragma unroll
+            for (int e = 0; e < 8; e++) f[e] *= qscale;
+        }
+        *reinterpret_cast<float4*>(&Qs[i * LD + d]) = make_float4(f[0], f[1], f[2], f[3]);
+        *reinterpret_cast<float4*>(&Qs[i * LD + d + 4]) = make_float4(f[4], f[5], f[6], f[7]);
+    }
+    // Last key position of each owned row (-1: padding row, fully masked).
+    int lim[4];
+#pragma unroll
+    for (int a = 0; a < 4; a++) {
+        const int i = ti + 16 * a, tq = i / gsize, t = t0 + tq;
+        lim[a] = (tq < tq_tokens && t < tokens) ? pos0 + t : -1;
+    }
+
+    // K / V tile kt into registers: chunk c of this thread is row (tid + c * kBlock) / CPR.
+    uint4 kr[NC], vr[NC];
+    auto load_tile = [&](int kt) {
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            const int q = tid + c * kBlock, r = q / CPR, col = q % CPR;
+            const int pos = min(kt * kPK + r, kmax);
+            const size_t off = (size_t)pos * row_elems + (size_t)g * HD + col * (16 / ES);
+            kr[c] = ld_nt16(kc + off);
+            vr[c] = ld_nt16(vc + off);
+        }
+    };
+    auto store_tile = [&]() {
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            const int q = tid + c * kBlock, r = q / CPR, col = q % CPR;
+            float* kd = &Ks[r * LD + col * (16 / ES)];
+            float* vd = &Vs[r * LD + col * (16 / ES)];
+            if constexpr (CT == L0H_F16) {
+                const uint32_t kw[4] = {kr[c].x, kr[c].y, kr[c].z, kr[c].w};
+                const uint32_t vw[4] = {vr[c].x, vr[c].y, vr[c].z, vr[c].w};
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const float2 k0 = __half22float2(__builtin_bit_cast(__half2, kw[2 * j]));
+                    const float2 k1 = __half22float2(__builtin_bit_cast(__half2, kw[2 * j + 1]));
+                    const float2 v0 = __half22float2(__builtin_bit_cast(__half2, vw[2 * j]));
+                    const float2 v1 = __half22float2(__builtin_bit_cast(__half2, vw[2 * j + 1]));
+                    *reinterpret_cast<float4*>(kd + 4 * j) = make_float4(k0.x, k0.y, k1.x, k1.y);
+                    *reinterpret_cast<float4*>(vd + 4 * j) = make_float4(v0.x, v0.y, v1.x, v1.y);
+                }
+            } else {
+                *reinterpret_cast<uint4*>(kd) = kr[c];
+                *reinterpret_cast<uint4*>(vd) = vr[c];
+            }
+        }
+    };
+
+    float m[4], l[4];
+    float4 o[4][E];
+#pragma unroll
+    for (int a = 0; a < 4; a++) {
+        m[a] = -INFINITY;
+        l[a] = 0.f;
+#pragma unroll
+        for (int e = 0; e < E; e++) o[a][e] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+
+    const int ntiles = kmax / kPK + 1;
+    load_tile(0);
+    for (int kt = 0; kt < ntiles; kt++) {
+        __syncthreads();  // the previous tile's K, V and P are no longer read
+        store_tile();
+        if (kt + 1 < ntiles) load_tile(kt + 1);
+        __syncthreads();
+
+        // Scores of rows ti + 16 a against keys tj + 16 b.
+        float sc[4][4];
+#pragma unroll
+        for (int a = 0; a < 4; a++)
+#pragma unroll
+            for (int b = 0; b < 4; b++) sc[a][b] = 0.f;
+#pragma unroll 4
+        for (int d = 0; d < HD; d += 4) {
+            float4 qa[4], kb[4];
+#pragma unroll
+            for (int a = 0; a < 4; a++) qa[a] = *reinterpret_cast<const float4*>(&Qs[(ti + 16 * a) * LD + d]);
+#pragma unroll
+            for (int b = 0; b < 4; b++) kb[b] = *reinterpret_cast<const float4*>(&Ks[(tj + 16 * b) * LD + d]);
+#pragma unroll
+            for (int a = 0; a < 4; a++)
+#pragma unroll
+                for (int b = 0; b < 4; b++) {
+                    sc[a][b] = fmaf(qa[a].x, kb[b].x, sc[a][b]);
+                    sc[a][b] = fmaf(qa[a].y, kb[b].y, sc[a][b]);
+                    sc[a][b] = fmaf(qa[a].z, kb[b].z, sc[a][b]);
+                    sc[a][b] = fmaf(qa[a].w, kb[b].w, sc[a][b]);
+                }
+        }
+        // Online softmax per row; probabilities to LDS, accumulators rescaled.
+#pragma unroll
+        for (int a = 0; a < 4; a++) {
+            float mt = -INFINITY;
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                const int pos = kt * kPK + tj + 16 * b;
+                if (pos > lim[a]) sc[a][b] = -INFINITY;
+                mt = fmaxf(mt, sc[a][b]);
+            }
+            const float mn = fmaxf(m[a], row16_max(mt));
+            const float corr = mn == -INFINITY ? 1.f : exp2f(m[a] - mn);  // 0 while m is -inf
+            float ps = 0.f;
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                const float pr = mn == -INFINITY ? 0.f : exp2f(sc[a][b] - mn);
+                Ps[(ti + 16 * a) * SLD + tj + 16 * b] = pr;
+                ps += pr;
+            }
+            l[a] = l[a] * corr + row16_sum(ps);
+            m[a] = mn;
+#pragma unroll
+            for (int e = 0; e < E; e++) {
+                o[a][e].x *= corr;
+                o[a][e].y *= corr;
+                o[a][e].z *= corr;
+                o[a][e].w *= corr;
+            }
+        }
+        __syncthreads();
+        // o[rows][dims 4 tj + 64 e ..] += P . V
+#pragma unroll 2
+        for (int j = 0; j < kPK; j += 4) {
+            float4 pa[4];
+#pragma unroll
+            for (int a = 0; a < 4; a++) pa[a] = *reinterpret_cast<const float4*>(&Ps[(ti + 16 * a) * SLD + j]);
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) {
+#pragma unroll
+                for (int e = 0; e < E; e++) {
+                    const float4 v = *reinterpret_cast<const float4*>(&Vs[(j + jj) * LD + 4 * tj + 64 * e]);
+#pragma unroll
+                    for (int a = 0; a < 4; a++) {
+                        const float pv = jj == 0 ? pa[a].x : jj == 1 ? pa[a].y : jj == 2 ? pa[a].z : pa[a].w;
+                        o[a][e].x = fmaf(pv, v.x, o[a][e].x);
+                        o[a][e].y = fmaf(pv, v.y, o[a][e].y);
+                        o[a][e].z = fmaf(pv, v.z, o[a][e].z);
+                        o[a][e].w = fmaf(pv, v.w, o[a][e].w);
+                    }
+                }
+            }
+        }
+    }
+
+    // out[token][head][d] = o / l
+#pragma unroll
+    for (int a = 0; a < 4; a++) {
+        if (lim[a] < 0) continue;
+        const int i = ti + 16 * a, t = t0 + i / gsize, h = g * gsize + i % gsize;
+        const float inv = l[a] > 0.f ? 1.f / l[a] : 0.f;
+#pragma unroll
+        for (int e = 0; e < E; e++) {
+            const size_t base = (size_t)t * p.nh * HD + (size_t)h * HD + 4 * tj + 64 * e;
+            store_act(p.out, p.out_dtype, base + 0, o[a][e].x * inv);
+            store_act(p.out, p.out_dtype, base + 1, o[a][e].y * inv);
+            store_act(p.out, p.out_dtype, base + 2, o[a][e].z * inv);
+            store_act(p.out, p.out_dtype, base + 3, o[a][e].w * inv);
+        }
+    }
+}
+
+template <int HD, int CT, int QT>
+int launch_prefill_tiled(hipStream_t s, const AttnParams& p, int pos0, int tokens) {
+    const int gsize = p.nh / p.nkv;
+    const int tq = kPQ / gsize;
+    const size_t smem = prefill_smem_bytes<HD>();
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&attn_prefill_tiled_kernel<HD, CT, QT>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+    if (attr != hipSuccess) return fail(L0H_ERR_DEVICE, "prefill attention: LDS size attribute refused");
+    dim3 grid(ceil_div(tokens, tq), p.nkv);
+    attn_prefill_tiled_kernel<HD, CT, QT><<<grid, kBlock, smem, s>>>(p, pos0, tokens, gsize, tq);
+    return launch_status("attn_prefill_tiled");
+}
+
+template <int HD>
+int launch_prefill_hd(hipStream_t s, const AttnParams& p, int pos0, int tokens) {
+    if (p.cache_dtype == L0H_F16)
+        return p.q_dtype == L0H_F16 ? launch_prefill_tiled<HD, L0H_F16, L0H_F16>(s, p, pos0, tokens)
+                                    : launch_prefill_tiled<HD, L0H_F16, L0H_F32>(s, p, pos0, tokens);
+    return p.q_dtype == L0H_F16 ? launch_prefill_tiled<HD, L0H_F32, L0H_F16>(s, p, pos0, tokens)
+                                : launch_prefill_tiled<HD, L0H_F32, L0H_F32>(s, p, pos0, tokens);
+}
+
 }  // namespace
 
 int attention_default_splits(int batch, int nkv, int max_len, int compute_units) {
@@ -478,8 +726,21 @@ int launch_attention_decode(hipStream_t s, const AttnParams& p) {
     return launch_any(s, p, 0, (size_t)p.max_seq_len * p.nkv * p.head_dim);
 }
 
-// Prefill: token t of the chunk is batch entry t with length pos0 + t + 1 over the shared cache.
+bool attention_prefill_tiled(const AttnParams& p) {
+    return (p.head_dim == 64 || p.head_dim == 128) && p.nkv > 0 && p.nh % p.nkv == 0 && p.nh / p.nkv <= kPQ &&
+           (p.cache_dtype == L0H_F16 || p.cache_dtype == L0H_F32) && (p.q_dtype == L0H_F16 || p.q_dtype == L0H_F32);
+}
+
+// Prefill: the query-tiled kernel where it applies; otherwise token t of the chunk is batch entry t
+// with length pos0 + t + 1 over the shared cache (the split decode kernel).
 int launch_attention_prefill(hipStream_t s, AttnParams p, int pos0, int tokens) {
+    if (tokens < 1 || pos0 < 0 || pos0 + tokens > p.max_seq_len)
+        return fail(L0H_ERR_INVALID_ARG, "prefill chunk outside the cache");
+    if (attention_prefill_tiled(p)) {
+        if ((((uintptr_t)p.q | (uintptr_t)p.kc | (uintptr_t)p.vc) & 15) != 0)
+            return fail(L0H_ERR_INVALID_ARG, "attention buffers must be 16-byte aligned");
+        return p.head_dim == 64 ? launch_prefill_hd<64>(s, p, pos0, tokens) : launch_prefill_hd<128>(s, p, pos0, tokens);
+    }
     p.batch = tokens;
     p.seq_len = pos0 + 1;
     p.seq_len_device = nullptr;

@@ -92,15 +92,40 @@ __device__ __forceinline__ int row_group(int gx) {
 // per lane (two waves per SIMD) for all but the 128 x 64 wave tile.
 constexpr int ring_depth(int bm, int nw) { return nw == 64 ? 4 : (bm == 64 && nw == 16) ? 8 : 6; }
 
-template <int DT, int BM, int NW, bool NT, int P = ring_depth(BM, NW), int MF = (NW % 32 == 0 ? 32 : 16)>
+// int8 weights: 8 signed bytes -> 8 exact fp16 values. Byte u = q + 128 (sign bit flipped) under
+// the fp16 exponent of 1024 reads as 1024 + u; subtracting 1152 leaves q. Bytes 0 and 2 (1 and 3)
+// share a 32-bit word, so the fp16 order is b0 b2 b1 b3 b4 b6 b5 b7; the activation chunks are
+// stored in LDS in that order too (a permutation of K within 8 values, the same for both
+// operands).
+__device__ __forceinline__ uint4 i8x8_to_f16(uint32_t lo, uint32_t hi) {
+    lo ^= 0x80808080u;
+    hi ^= 0x80808080u;
+    const uint32_t m = 0x00FF00FFu, e = 0x64006400u;
+    const __half2 off = __builtin_bit_cast(__half2, 0xE480E480u);  // (-1152, -1152)
+    auto cv = [&](uint32_t w) { return __builtin_bit_cast(uint32_t, __hadd2(__builtin_bit_cast(__half2, w), off)); };
+    return make_uint4(cv((lo & m) | e), cv(((lo >> 8) & m) | e), cv((hi & m) | e), cv(((hi >> 8) & m) | e));
+}
+__device__ __forceinline__ u32x4_t perm_f16x8(const uint4& a) {  // a0 a2 a1 a3 a4 a6 a5 a7
+    return u32x4_t{(a.x & 0xFFFFu) | (a.y << 16), (a.x >> 16) | (a.y & 0xFFFF0000u), (a.z & 0xFFFFu) | (a.w << 16),
+                   (a.z >> 16) | (a.w & 0xFFFF0000u)};
+}
+
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+
+// WT: weight storage (F16, BF16, or I8PC with fp16 activations and one fp16 scale per weight row).
+template <int WT, int BM, int NW, bool NT, int P = ring_depth(BM, NW), int MF = (NW % 32 == 0 ? 32 : 16)>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void gemm_nk_kernel(
-    int M, int N, int K, int k_per_split, const uint16_t* __restrict__ X, const uint16_t* __restrict__ W,
-    void* Y, int y_dtype, float* partial) {
+    int M, int N, int K, int k_per_split, const uint16_t* __restrict__ X, const void* __restrict__ Wv,
+    const uint16_t* __restrict__ scales, void* Y, int y_dtype, float* partial) {
+    constexpr bool I8 = WT == L0H_I8PC;
+    constexpr int DT = I8 ? L0H_F16 : WT;  // MFMA operand type
     constexpr int S = BK * MF / 512;       // MFMAs per K step (k of one MFMA = 512 / MF)
     constexpr int MI = BM / MF;            // MF-row A fragments
     constexpr int NJ = NW / MF;            // MF-column B fragments per wave
-    constexpr int NB = NJ * S;             // B registers (16 bytes) per stage
+    constexpr int NB = I8 ? NJ : NJ * S;   // B registers per stage (int8: one covers the step)
     constexpr int AC = BM * BK / 8 / 256;  // 16-byte A chunks per thread per step
+    constexpr int WB = I8 ? 1 : 2;         // bytes per weight
+    using breg = typename std::conditional<I8 && MF == 16, uint2, uint4>::type;
     static_assert(AC >= 1 && MI >= 1 && NJ >= 1, "tile too small");
     __shared__ __attribute__((aligned(16))) uint16_t sa[2][BM * kLds];
 
@@ -120,15 +145,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     const int nsteps = max(0, min(K, kbeg + k_per_split) - kbeg) / BK;
     const int last = max(nsteps - 1, 0);
 
-    // Operand lane layout: lane l holds row / column l % MF and, of MFMA s of the step, the 8
-    // K values from s (512 / MF) + 8 (l / MF).
+    // Operand lane layout: lane l holds row / column l % MF and, of MFMA q of the step, the 8
+    // K values from q (512 / MF) + 8 (l / MF). int8 at MF = 32: a lane loads its row's 16 bytes
+    // from 16 (l / 32) at once, and MFMA q takes bytes 8 q .. 8 q + 7 of them, i.e. K values
+    // 16 (l / 32) + 8 q (the activation fragment is read from the same place).
     const int li = lane % MF, lk = (lane / MF) * 8;
-    const uint16_t* bptr[NB];
+    const char* W = static_cast<const char*>(Wv);
+    const char* bptr[NB];
 #pragma unroll
-    for (int j = 0; j < NJ; j++)
+    for (int j = 0; j < NJ; j++) {
+        const size_t row = (size_t)min(nw0 + j * MF + li, N - 1) * K;
+        if constexpr (I8) {
+            bptr[j] = W + row + kbeg + (MF == 32 ? 16 * (lane / 32) : lk);
+        } else {
 #pragma unroll
-        for (int q = 0; q < S; q++)
-            bptr[j * S + q] = W + (size_t)min(nw0 + j * MF + li, N - 1) * K + kbeg + q * (512 / MF) + lk;
+            for (int q = 0; q < S; q++) bptr[j * S + q] = W + (row + kbeg + q * (512 / MF) + lk) * WB;
+        }
+    }
     const uint16_t* aptr[AC];
 #pragma unroll
     for (int c = 0; c < AC; c++) {
@@ -136,18 +169,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
         aptr[c] = X + (size_t)min(m0 + (idx >> 2), M - 1) * K + kbeg + (idx & 3) * 8;
     }
 
-    uint4 ra[P][AC], rb[P][NB];
+    uint4 ra[P][AC];
+    breg rb[P][NB];
     // Step t of this block's K range into a ring stage; steps past the end re-read the last one.
-    auto gload = [&](uint4 (&a)[AC], uint4 (&b)[NB], int t) {
+    auto gload = [&](uint4 (&a)[AC], breg (&b)[NB], int t) {
         const int k0 = min(t, last) * BK;
 #pragma unroll
         for (int c = 0; c < AC; c++) a[c] = *reinterpret_cast<const uint4*>(aptr[c] + k0);
 #pragma unroll
         for (int j = 0; j < NB; j++) {
-            if constexpr (NT)
-                b[j] = ld_nt16(bptr[j] + k0);
-            else
-                b[j] = *reinterpret_cast<const uint4*>(bptr[j] + k0);
+            const char* bp = bptr[j] + (size_t)k0 * WB;
+            if constexpr (std::is_same<breg, uint2>::value) {
+                const u32x2_t v = NT ? __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(bp))
+                                     : *reinterpret_cast<const u32x2_t*>(bp);
+                b[j] = make_uint2(v.x, v.y);
+            } else if constexpr (NT) {
+                b[j] = ld_nt16(bp);
+            } else {
+                b[j] = *reinterpret_cast<const uint4*>(bp);
+            }
         }
     };
     auto sstore = [&](const uint4 (&a)[AC], int buf) {
@@ -156,7 +196,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
             const int idx = tid + c * 256;
             // As a vector value: a struct copy would keep the ring in memory instead of registers.
             *reinterpret_cast<u32x4_t*>(&sa[buf][(idx >> 2) * kLds + (idx & 3) * 8]) =
-                u32x4_t{a[c].x, a[c].y, a[c].z, a[c].w};
+                I8 ? perm_f16x8(a[c]) : u32x4_t{a[c].x, a[c].y, a[c].z, a[c].w};
         }
     };
 
@@ -166,14 +206,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
 #pragma unroll
         for (int j = 0; j < NJ; j++) acc[i][j] = acc_t<MF>{};
 
-    auto mma = [&](int buf, const uint4 (&b)[NB]) {
+    auto mma = [&](int buf, const breg (&b)[NB]) {
 #pragma unroll
         for (int q = 0; q < S; q++) {
+            uint4 bq[NJ];
+#pragma unroll
+            for (int j = 0; j < NJ; j++) {
+                if constexpr (!I8) {
+                    bq[j] = b[j * S + q];
+                } else if constexpr (MF == 16) {
+                    bq[j] = i8x8_to_f16(b[j].x, b[j].y);
+                } else {
+                    const uint4& w = reinterpret_cast<const uint4&>(b[j]);
+                    bq[j] = q == 0 ? i8x8_to_f16(w.x, w.y) : i8x8_to_f16(w.z, w.w);
+                }
+            }
+            const int ak = (I8 && MF == 32) ? 16 * (lane / 32) + 8 * q : q * (512 / MF) + lk;
 #pragma unroll
             for (int i = 0; i < MI; i++) {
-                const uint4 af = *reinterpret_cast<const uint4*>(&sa[buf][(i * MF + li) * kLds + q * (512 / MF) + lk]);
+                const uint4 af = *reinterpret_cast<const uint4*>(&sa[buf][(i * MF + li) * kLds + ak]);
 #pragma unroll
-                for (int j = 0; j < NJ; j++) acc[i][j] = mfma<DT, MF>(af, b[j * S + q], acc[i][j]);
+                for (int j = 0; j < NJ; j++) acc[i][j] = mfma<DT, MF>(af, bq[j], acc[i][j]);
             }
         }
     };
@@ -202,16 +255,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     // MF = 16 and row = 8 (r / 4) + 4 (l / 32) + r % 4 for MF = 32.
     constexpr int R = MF == 16 ? 4 : 16;
 #pragma unroll
-    for (int i = 0; i < MI; i++) {
+    for (int j = 0; j < NJ; j++) {
+        const int col = nw0 + j * MF + li;
+        const float scale = I8 ? __half2float(__ushort_as_half(scales[min(col, N - 1)])) : 1.f;
 #pragma unroll
-        for (int j = 0; j < NJ; j++) {
-            const int col = nw0 + j * MF + li;
+        for (int i = 0; i < MI; i++) {
 #pragma unroll
             for (int r = 0; r < R; r++) {
                 const int rr = MF == 16 ? (lane / 16) * 4 + r : (r / 4) * 8 + (lane / 32) * 4 + (r % 4);
                 const int row = m0 + i * MF + rr;
                 if (row < M && col < N) {
-                    const float v = acc[i][j][r];
+                    const float v = I8 ? acc[i][j][r] * scale : acc[i][j][r];
                     if (partial)
                         partial[((size_t)bz * M + row) * N + col] = v;
                     else
@@ -274,20 +328,19 @@ Plan plan_for(int m, int n, int k, int cus) {
     return p;
 }
 
-template <int DT, int BM, int NW>
-int launch_tiles(hipStream_t s, int m, int n, int k, const void* x, const void* w, void* y, int y_dtype,
-                 int splits, float* ws) {
+template <int WT, int BM, int NW>
+int launch_tiles(hipStream_t s, int m, int n, int k, const void* x, const void* w, const uint16_t* scales, void* y,
+                 int y_dtype, int splits, float* ws) {
     const int k_per_split = (k / BK + splits - 1) / splits * BK;
     // The kernel decodes (row block, split, column block) from the linear block id; the grid only
     // has to hold that many blocks, in the order x = row blocks, y = splits, z = column blocks.
     dim3 grid(ceil_div(m, BM), splits, ceil_div(n, 4 * NW));
     const auto* xp = static_cast<const uint16_t*>(x);
-    const auto* wp = static_cast<const uint16_t*>(w);
     float* part = splits > 1 ? ws : nullptr;
     if (grid.x == 1)  // each weight byte is read by one block: stream it past the caches
-        gemm_nk_kernel<DT, BM, NW, true><<<grid, 256, 0, s>>>(m, n, k, k_per_split, xp, wp, y, y_dtype, part);
+        gemm_nk_kernel<WT, BM, NW, true><<<grid, 256, 0, s>>>(m, n, k, k_per_split, xp, w, scales, y, y_dtype, part);
     else
-        gemm_nk_kernel<DT, BM, NW, false><<<grid, 256, 0, s>>>(m, n, k, k_per_split, xp, wp, y, y_dtype, part);
+        gemm_nk_kernel<WT, BM, NW, false><<<grid, 256, 0, s>>>(m, n, k, k_per_split, xp, w, scales, y, y_dtype, part);
     int st = launch_status("gemm_nk");
     if (st || splits == 1) return st;
     const size_t mn = (size_t)m * n;
@@ -295,11 +348,12 @@ int launch_tiles(hipStream_t s, int m, int n, int k, const void* x, const void* 
     return launch_status("gemm splitk reduce");
 }
 
-template <int DT>
-int launch_plan(hipStream_t s, const Plan& p, int m, int n, int k, const void* x, const void* w, void* y,
-                int y_dtype, float* ws) {
-#define L0H_GEMM_CASE(BM_, NW_) \
-    if (p.bm == BM_ && p.nw == NW_) return launch_tiles<DT, BM_, NW_>(s, m, n, k, x, w, y, y_dtype, p.splits, ws);
+template <int WT>
+int launch_plan(hipStream_t s, const Plan& p, int m, int n, int k, const void* x, const void* w,
+                const uint16_t* scales, void* y, int y_dtype, float* ws) {
+#define L0H_GEMM_CASE(BM_, NW_)                                                                                  \
+    if (p.bm == BM_ && p.nw == NW_)                                                                              \
+        return launch_tiles<WT, BM_, NW_>(s, m, n, k, x, w, scales, y, y_dtype, p.splits, ws);
     L0H_GEMM_CASE(64, 16)
     L0H_GEMM_CASE(64, 32)
     L0H_GEMM_CASE(64, 64)
@@ -319,11 +373,15 @@ size_t gemm_workspace_bytes(int m, int n, int k, int compute_units) {
 }
 
 int launch_gemm_nk(hipStream_t s, int dtype, int m, int n, int k, const void* x, const void* w,
-                   void* y, int y_dtype, float* ws, size_t ws_bytes, int cus) {
+                   void* y, int y_dtype, float* ws, size_t ws_bytes, int cus, const uint16_t* scales) {
     if (m <= 0 || n <= 0 || k <= 0) return fail(L0H_ERR_INVALID_ARG, "GEMM sizes must be positive");
-    if (dtype != L0H_BF16 && dtype != L0H_F16) return fail(L0H_ERR_INVALID_ARG, "GEMM operands are F16 or BF16");
+    if (dtype != L0H_BF16 && dtype != L0H_F16 && dtype != L0H_I8PC)
+        return fail(L0H_ERR_INVALID_ARG, "GEMM weights are F16, BF16 or I8PC");
     const bool aligned = k % BK == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)w & 15) == 0;
-    if (!aligned) {
+    if (dtype == L0H_I8PC) {
+        if (!scales) return fail(L0H_ERR_INVALID_ARG, "int8 GEMM needs the per-row scales");
+        if (!aligned) return fail(L0H_ERR_UNSUPPORTED, "int8 GEMM needs K a multiple of 32 and 16-byte aligned operands");
+    } else if (!aligned) {
         const size_t mn = (size_t)m * n;
         gemm_nk_generic_kernel<<<ceil_div(mn, 256), 256, 0, s>>>(dtype, m, n, k, static_cast<const uint16_t*>(x),
                                                                  static_cast<const uint16_t*>(w), y, y_dtype);
@@ -331,8 +389,11 @@ int launch_gemm_nk(hipStream_t s, int dtype, int m, int n, int k, const void* x,
     }
     Plan p = plan_for(m, n, k, cus);
     while (p.splits > 1 && (size_t)p.splits * m * n * sizeof(float) > ws_bytes) p.splits /= 2;
-    return dtype == L0H_BF16 ? launch_plan<L0H_BF16>(s, p, m, n, k, x, w, y, y_dtype, ws)
-                             : launch_plan<L0H_F16>(s, p, m, n, k, x, w, y, y_dtype, ws);
+    switch (dtype) {
+    case L0H_BF16: return launch_plan<L0H_BF16>(s, p, m, n, k, x, w, nullptr, y, y_dtype, ws);
+    case L0H_F16: return launch_plan<L0H_F16>(s, p, m, n, k, x, w, nullptr, y, y_dtype, ws);
+    default: return launch_plan<L0H_I8PC>(s, p, m, n, k, x, w, scales, y, y_dtype, ws);
+    }
 }
 
 }  // namespace l0h

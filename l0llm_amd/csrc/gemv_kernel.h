@@ -189,8 +189,9 @@ __device__ __forceinline__ void store_cache(void* cache, int dt, size_t idx, flo
 
 // Epilogue for the RoPE-paired rows (row, row+1) of the fused q|k|v matrix; cs/sn hold
 // cos/sin(pos * inv_freq[i]) * scale for this launch's position.
-__device__ __forceinline__ void qkv_pair(const GemvParams& p, int row, float v0, float v1, int pos,
-                                         const float* cs_tab, const float* sn_tab) {
+// rope(i, cs, sn) gives cos/sin * scale of rotated pair i.
+template <class Rope>
+__device__ __forceinline__ void qkv_pair_with(const GemvParams& p, int row, float v0, float v1, int pos, Rope&& rope) {
     const int hd = p.head_dim, rot = p.rotary_dim;
     if (row >= p.q_dim + p.kv_dim) {  // v rows: natural order
         const int off = row - p.q_dim - p.kv_dim;
@@ -208,7 +209,8 @@ __device__ __forceinline__ void qkv_pair(const GemvParams& p, int row, float v0,
         const int i = j >> 1;
         d0 = i;
         d1 = i + (rot >> 1);
-        const float cs = cs_tab[i], sn = sn_tab[i];
+        float cs, sn;
+        rope(i, cs, sn);
         o0 = v0 * cs - v1 * sn;
         o1 = v1 * cs + v0 * sn;
     } else {
@@ -225,6 +227,14 @@ __device__ __forceinline__ void qkv_pair(const GemvParams& p, int row, float v0,
         store_cache(p.k_cache, p.cache_dtype, base + d0, o0);
         store_cache(p.k_cache, p.cache_dtype, base + d1, o1);
     }
+}
+
+__device__ __forceinline__ void qkv_pair(const GemvParams& p, int row, float v0, float v1, int pos,
+                                         const float* cs_tab, const float* sn_tab) {
+    qkv_pair_with(p, row, v0, v1, pos, [&](int i, float& cs, float& sn) {
+        cs = cs_tab[i];
+        sn = sn_tab[i];
+    });
 }
 
 // Per-row values an item's epilogue needs, loaded with the item's weights. A lane holds the

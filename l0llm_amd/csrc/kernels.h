@@ -111,12 +111,16 @@ int launch_attention_decode(hipStream_t s, const AttnParams& p);
 // Prefill over a shared cache: token t of the chunk attends to slots 0 .. pos0 + t (q and out
 // are [tokens, nh*hd]; p.batch and p.seq_len are set from pos0/tokens).
 int launch_attention_prefill(hipStream_t s, AttnParams p, int pos0, int tokens);
+// True when the prefill runs the query-tiled kernel (no split workspace needed).
+bool attention_prefill_tiled(const AttnParams& p);
 
-// MFMA GEMM Y[M,N] = X[M,K] * W[N,K]^T (f16 or bf16 operands).
-// Small M splits K into fp32 partials in `ws` (gemm_workspace_bytes) when it fits.
+// MFMA GEMM Y[M,N] = X[M,K] * W[N,K]^T: f16 or bf16 operands, or int8 weights with one fp16
+// scale per row (`scales`) and fp16 activations. Small M splits K into fp32 partials in `ws`
+// (gemm_workspace_bytes) when it fits.
 size_t gemm_workspace_bytes(int m, int n, int k, int compute_units);
 int launch_gemm_nk(hipStream_t s, int dtype, int m, int n, int k, const void* x, const void* w,
-                   void* y, int y_dtype, float* ws, size_t ws_bytes, int compute_units);
+                   void* y, int y_dtype, float* ws, size_t ws_bytes, int compute_units,
+                   const uint16_t* scales = nullptr);
 
 // Random init: w[i] ~ N(0, std^2) from (seed, i); stored as dtype (F32/F16/BF16).
 int launch_init_normal(hipStream_t s, void* dst, int dtype, size_t count, uint64_t seed,

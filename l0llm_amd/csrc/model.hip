@@ -19,6 +19,7 @@
 
 #include "host.h"
 #include "kernels.h"
+#include "gemv_kernel.h"
 
 namespace l0h {
 namespace {
@@ -51,6 +52,37 @@ __global__ void scatter_rows_kernel(char* dst, const char* src, const int* map, 
     }
 }
 
+// q|k|v rows of a prefill chunk (stored row order, bias added) -> RoPE at position pos0 + t,
+// q rows in head order, k and v rows into the cache: the decode epilogue, row by row. Thread x
+// of block (x-block, t) finishes row pair x of token t.
+__global__ void qkv_rows_kernel(GemvParams p, const float* qkv, float* q_rows, int pos0) {
+    const int t = blockIdx.y;
+    const int pair = blockIdx.x * blockDim.x + threadIdx.x;
+    const int nrows = p.q_dim + 2 * p.kv_dim;
+    if (2 * pair >= nrows) return;
+    const int pos = pos0 + t;
+    const float* r = qkv + (size_t)t * nrows;
+    p.q_out = q_rows + (size_t)t * p.q_dim;
+    qkv_pair_with(p, 2 * pair, r[2 * pair], r[2 * pair + 1], pos, [&](int i, float& cs, float& sn) {
+        float sv, cv;
+        sincosf((float)pos * p.inv_freq[i], &sv, &cv);
+        cs = cv * p.rope_scale;
+        sn = sv * p.rope_scale;
+    });
+}
+
+// act[t, i] = silu(gu[t, 2i]) * gu[t, 2i + 1] (gate/up rows interleaved, as the SwiGLU epilogue).
+__global__ void swiglu_rows_kernel(const float* gu, float* act, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) act[i] = silu(gu[2 * i]) * gu[2 * i + 1];
+}
+
+// fp32 activations -> the weight dtype (F16 / BF16) for the MFMA GEMM.
+__global__ void to_16bit_kernel(const float* x, uint16_t* y, size_t n, int dt) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = dt == L0H_BF16 ? float_to_bf16_bits(x[i]) : __half_as_ushort(__float2half_rn(x[i]));
+}
+
 }  // namespace
 }  // namespace l0h
 
@@ -78,6 +110,13 @@ struct l0h_model {
     unsigned long long* argmax_partials = nullptr;
     unsigned* argmax_ticket = nullptr;
     int attn_splits = 1;
+    // chunked prefill (allocated on first use): rows of up to pf_cap tokens
+    int pf_cap = 0;
+    float *pf_hidden = nullptr, *pf_xn = nullptr, *pf_qkv = nullptr, *pf_q = nullptr, *pf_attn = nullptr,
+          *pf_gu = nullptr, *pf_act = nullptr, *pf_tmp = nullptr, *pf_ws = nullptr;
+    uint16_t* pf_x16 = nullptr;
+    int* pf_ids = nullptr;
+    size_t pf_ws_bytes = 0;
     hipGraphExec_t step_exec = nullptr;
     bool eager = false;  // L0H_EAGER_STEP=1: enqueue the step's kernels instead of replaying the graph
     int pos = 0;  // LlmModel.Position
@@ -466,6 +505,144 @@ int run_step(l0h_model* m, int token, int position) {
     return launch_step(m);
 }
 
+// ---- chunked prefill (LlmModel.Prefill, LlmModel.cs:320-385; LlmDecoderLayer.ForwardBatch,
+// LlmDecoderLayer.cs:337-378): the tokens of a chunk go through each layer together, their
+// projections as one MFMA GEMM (int8 / fp16 / bf16 weights, 64 rows or more; activations rounded
+// to fp16, or to bf16 for bf16 weights) or one multi-row GEMV (fp32 weights, short chunks: each
+// launch reads W once per 8 rows), their attention through the query-tiled causal kernel, and their k / v rows into the
+// cache. Only the cache carries a chunk's result forward, so the last layer stops after its
+// attention's cache writes. int8 weights go through the MFMA GEMM as well (exact int8 -> fp16
+// in registers, fp16 activations, row scale in the epilogue): the multi-row GEMV would re-read a
+// wide-K matrix (down: K = 14336) once per token. ----
+constexpr int kPrefillChunk = 256;
+
+bool prefill_uses_gemm(const l0h_model* m, int T, int k) {
+    return m->storage != L0H_F32 && T >= 64 && k % 32 == 0;
+}
+
+int ensure_prefill(l0h_model* m) {
+    if (m->pf_cap) return L0H_OK;
+    const auto& c = m->cfg;
+    const int T = std::min(kPrefillChunk, m->max_seq);
+    const size_t H = c.hidden_size, I = c.intermediate_size, nqkv = m->qd + 2 * m->kvd;
+    int st;
+    if ((st = alloc_t(m, T * H, &m->pf_hidden)) || (st = alloc_t(m, T * H, &m->pf_xn)) ||
+        (st = alloc_t(m, T * nqkv, &m->pf_qkv)) || (st = alloc_t(m, (size_t)T * m->qd, &m->pf_q)) ||
+        (st = alloc_t(m, (size_t)T * m->qd, &m->pf_attn)) || (st = alloc_t(m, T * 2 * I, &m->pf_gu)) ||
+        (st = alloc_t(m, T * I, &m->pf_act)) || (st = alloc_t(m, (size_t)T, &m->pf_ids)))
+        return st;
+    if (m->storage != L0H_F32) {
+        const size_t kmax = std::max<size_t>({H, I, (size_t)m->qd});
+        if ((st = alloc_t(m, T * kmax, &m->pf_x16)) || (st = alloc_t(m, T * H, &m->pf_tmp))) return st;
+        const int cus = m->dev->compute_units;
+        size_t ws = 0;
+        for (int t = 64; t <= T; t++) {  // the largest split-K workspace any chunk size asks for
+            ws = std::max({ws, gemm_workspace_bytes(t, (int)nqkv, (int)H, cus), gemm_workspace_bytes(t, (int)H, m->qd, cus),
+                           gemm_workspace_bytes(t, (int)(2 * I), (int)H, cus), gemm_workspace_bytes(t, (int)H, (int)I, cus)});
+        }
+        if (ws && (st = alloc_owned(m, ws, reinterpret_cast<void**>(&m->pf_ws)))) return st;
+        m->pf_ws_bytes = ws;
+    }
+    m->pf_cap = T;
+    return L0H_OK;
+}
+
+// y = x W^T for T rows: STORE into y (+ bias in stored row order) or RESIDUAL into resid.
+int project_rows(l0h_model* m, hipStream_t s, const Proj& P, const float* x, int T, float* y, const float* bias,
+                 int epilogue, float* resid) {
+    if (prefill_uses_gemm(m, T, P.k)) {
+        const size_t nx = (size_t)T * P.k;
+        const int xdt = m->storage == L0H_BF16 ? L0H_BF16 : L0H_F16;
+        to_16bit_kernel<<<ceil_div(nx, 256), 256, 0, s>>>(x, m->pf_x16, nx, xdt);
+        int st = launch_status("to_16bit");
+        if (st) return st;
+        float* out = epilogue == EPI_RESIDUAL ? m->pf_tmp : y;
+        if ((st = launch_gemm_nk(s, m->storage, T, P.n, P.k, m->pf_x16, P.w, out, L0H_F32, m->pf_ws, m->pf_ws_bytes,
+                                 m->dev->compute_units, P.s)))
+            return st;
+        if (bias && (st = launch_bias_add(s, y, bias, P.n, T))) return st;
+        return epilogue == EPI_RESIDUAL ? launch_add(s, resid, m->pf_tmp, T * P.n) : L0H_OK;
+    }
+    GemvParams g;
+    g.w_dtype = m->storage;
+    g.w = P.w;
+    g.scales = P.s;
+    g.n = P.n;
+    g.k = P.k;
+    g.m = T;
+    g.x = x;
+    g.x_dtype = L0H_F32;
+    g.epilogue = epilogue;
+    g.bias = bias;
+    g.y = y;
+    g.y_dtype = L0H_F32;
+    g.resid = resid;
+    g.max_blocks = gemv_max_blocks(m->dev->compute_units);
+    g.compute_units = m->dev->compute_units;
+    return launch_gemv_nk(s, g);
+}
+
+// Tokens ids[0, T) at positions pos0 .. pos0 + T - 1 into every layer's cache.
+int prefill_chunk(l0h_model* m, const int* ids, int pos0, int T) {
+    const auto& c = m->cfg;
+    hipStream_t s = m->dev->stream;
+    const int H = c.hidden_size, I = c.intermediate_size;
+    int st = l0h_write(m->dev, m->pf_ids, 0, ids, (size_t)T * sizeof(int));
+    if (st) return st;
+    if ((st = launch_embedding(s, m->pf_ids, m->embedding, m->pf_hidden, H, (size_t)T * H))) return st;
+    for (int li = 0; li < c.num_layers; li++) {
+        Layer& L = m->layers[li];
+        if ((st = launch_rmsnorm(s, m->pf_hidden, nullptr, L.input_norm, m->pf_xn, c.rms_norm_eps, H, T, 0))) return st;
+        if ((st = project_rows(m, s, L.qkv, m->pf_xn, T, m->pf_qkv, L.qkv_bias, EPI_STORE, nullptr))) return st;
+        GemvParams g;
+        g.k_cache = L.k_cache;
+        g.v_cache = L.v_cache;
+        g.cache_dtype = m->cache_dtype;
+        g.inv_freq = m->inv_freq;
+        g.rope_scale = m->rope_scale;
+        g.q_dim = m->qd;
+        g.kv_dim = m->kvd;
+        g.head_dim = c.head_dim;
+        g.rotary_dim = m->rot;
+        const int pairs = (m->qd + 2 * m->kvd) / 2;
+        qkv_rows_kernel<<<dim3(ceil_div(pairs, 256), T), 256, 0, s>>>(g, m->pf_qkv, m->pf_q, pos0);
+        if ((st = launch_status("qkv_rows"))) return st;
+        AttnParams a;
+        a.q = m->pf_q;
+        a.q_dtype = L0H_F32;
+        a.kc = L.k_cache;
+        a.vc = L.v_cache;
+        a.cache_dtype = m->cache_dtype;
+        a.out = m->pf_attn;
+        a.out_dtype = L0H_F32;
+        a.head_dim = c.head_dim;
+        a.nh = c.num_attention_heads;
+        a.nkv = c.num_key_value_heads;
+        a.max_seq_len = m->max_seq;
+        a.splits = 1;  // the query-tiled kernel; other head sizes: one split per token
+        if ((st = launch_attention_prefill(s, a, pos0, T))) return st;
+        if (li + 1 == c.num_layers) break;
+        if ((st = project_rows(m, s, L.o, m->pf_attn, T, nullptr, nullptr, EPI_RESIDUAL, m->pf_hidden))) return st;
+        if ((st = launch_rmsnorm(s, m->pf_hidden, nullptr, L.post_norm, m->pf_xn, c.rms_norm_eps, H, T, 0))) return st;
+        if ((st = project_rows(m, s, L.gu, m->pf_xn, T, m->pf_gu, nullptr, EPI_STORE, nullptr))) return st;
+        const size_t na = (size_t)T * I;
+        swiglu_rows_kernel<<<ceil_div(na, 256), 256, 0, s>>>(m->pf_gu, m->pf_act, na);
+        if ((st = launch_status("swiglu_rows"))) return st;
+        if ((st = project_rows(m, s, L.down, m->pf_act, T, nullptr, nullptr, EPI_RESIDUAL, m->pf_hidden))) return st;
+    }
+    return L0H_OK;
+}
+
+// ids[0, count) at positions 0 .. count - 1 into the cache, in chunks.
+int prefill_tokens(l0h_model* m, const int* ids, int count) {
+    for (int i = 0; i < count; i++)
+        if ((unsigned)ids[i] >= (unsigned)m->cfg.vocab_size)
+            return fail(L0H_ERR_INVALID_ARG, "token id " + std::to_string(ids[i]) + " outside the vocabulary");
+    int st = ensure_prefill(m);
+    for (int p0 = 0; p0 < count && !st; p0 += m->pf_cap) st = prefill_chunk(m, ids + p0, p0, std::min(m->pf_cap, count - p0));
+    return st;
+}
+
 }  // namespace
 }  // namespace l0h
 
@@ -780,8 +957,10 @@ int l0h_model_prefill(l0h_model* m, const int* ids, int count, float* host_logit
     L0H_CHECK_ARG(count > 0, "the prompt must contain at least one token");
     L0H_CHECK_ARG(count <= m->max_seq, "prompt longer than the cache");
     m->pos = 0;
-    for (int i = 0; i < count; i++)
-        if ((st = run_step(m, ids[i], i))) return st;
+    // All but the last token fill the cache in chunks; the last one runs the decode step, which
+    // leaves its logits (LlmModel.Prefill returns the last position's logits).
+    if (count > 1 && (st = prefill_tokens(m, ids, count - 1))) return st;
+    if ((st = run_step(m, ids[count - 1], count - 1))) return st;
     m->pos = count;
     if (host_logits) return l0h_read(m->dev, m->logits, 0, host_logits, (size_t)m->cfg.vocab_size * 4);
     return l0h_synchronize(m->dev);
@@ -823,8 +1002,8 @@ int l0h_model_generate_greedy(l0h_model* m, const int* prompt, int prompt_len, i
     *n_out = 0;
     if (max_new == 0) return L0H_OK;
     const int saved = m->pos;
-    for (int i = 0; i < prompt_len; i++)
-        if ((st = run_step(m, prompt[i], i))) return st;
+    if (prompt_len > 1 && (st = prefill_tokens(m, prompt, prompt_len - 1))) return st;
+    if ((st = run_step(m, prompt[prompt_len - 1], prompt_len - 1))) return st;
     // The last prompt step chose token 0 of the output (out_list[0]) and advanced the device
     // position; the remaining steps replay the graph with the token fed back on the device.
     for (int i = 1; i < max_new; i++)

@@ -14,6 +14,7 @@ constexpr int kMaxRows = 8;
 int attention_run(l0h_device* dev, AttnParams p, bool prefill, int pos0, int tokens) {
     if (prefill) {
         p.batch = tokens;
+        if (attention_prefill_tiled(p)) return launch_attention_prefill(dev->stream, p, pos0, tokens);
     }
     p.splits = attention_default_splits(p.batch, p.nkv, p.max_seq_len, dev->compute_units);
     const size_t bytes = attention_partials_bytes(p);
@@ -243,6 +244,21 @@ int l0h_gemm_nk(l0h_device* dev, int dtype, int m, int n, int k, const void* x, 
     }
     return launch_gemm_nk(dev->stream, dtype, m, n, k, x, w, y, y_dtype, static_cast<float*>(dev->workspace),
                           dev->workspace_bytes, dev->compute_units);
+}
+
+int l0h_gemm_nk_i8pc(l0h_device* dev, int m, int n, int k, const void* x, const int8_t* w, const uint16_t* scales,
+                     void* y, int y_dtype) {
+    L0H_ENTER(dev);
+    L0H_CHECK_ARG(x && w && scales && y, "null buffer");
+    L0H_CHECK_ARG(y_dtype >= L0H_F32 && y_dtype <= L0H_BF16, "output is F32, F16 or BF16");
+    L0H_CHECK_ARG(m > 0 && n > 0 && k > 0, "sizes must be positive");
+    const size_t ws = gemm_workspace_bytes(m, n, k, dev->compute_units);
+    if (ws) {
+        int st = ensure_workspace(dev, ws, 0);
+        if (st) return st;
+    }
+    return launch_gemm_nk(dev->stream, L0H_I8PC, m, n, k, x, w, y, y_dtype, static_cast<float*>(dev->workspace),
+                          dev->workspace_bytes, dev->compute_units, scales);
 }
 
 int l0h_attention_decode(l0h_device* dev, const void* q, int q_dtype, const void* k_cache, const void* v_cache,

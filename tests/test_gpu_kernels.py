@@ -310,16 +310,26 @@ def test_attention_decode_batched_fp16(device, suite, batch, seq):
         assert np.max(np.abs(out[b] - want)) <= 1e-2 * np.max(np.abs(want)), b
 
 
-def test_attention_prefill_matches_oracle(device, suite):
-    rng = np.random.default_rng(8)
-    hd, nh, nkv, pos0, T, max_seq = 64, 14, 2, 9, 8, 32
-    kc = rng.normal(0, 1, (max_seq, nkv * hd)).astype(np.float32)
-    vc = rng.normal(0, 1, (max_seq, nkv * hd)).astype(np.float32)
+# (head_dim, q heads, kv heads, pos0, tokens, max_seq, cache): query-tiled kernel for head_dim 64
+# and 128 (group sizes 7, 4, 8 and 1, ragged last tiles, chunks starting mid-cache), split decode
+# kernel per token for the other head sizes.
+PREFILL = [(64, 14, 2, 9, 8, 32, l0.F32), (128, 32, 8, 0, 200, 256, l0.F16), (128, 32, 8, 100, 77, 300, l0.F16),
+           (64, 16, 2, 5, 130, 200, l0.F32), (128, 8, 8, 63, 65, 200, l0.F16), (128, 16, 2, 1, 1, 4, l0.F32),
+           (32, 8, 2, 3, 10, 20, l0.F32), (16, 4, 2, 0, 40, 48, l0.F16)]
+
+
+@pytest.mark.parametrize("hd,nh,nkv,pos0,T,max_seq,cache", PREFILL)
+def test_attention_prefill_matches_oracle(device, suite, hd, nh, nkv, pos0, T, max_seq, cache):
+    rng = np.random.default_rng(8 + pos0 + T)
+    kf = rng.normal(0, 1, (max_seq, nkv * hd)).astype(np.float32)
+    vf = rng.normal(0, 1, (max_seq, nkv * hd)).astype(np.float32)
+    kc, vc = (kf, vf) if cache == l0.F32 else (kf.astype(np.float16).view(np.uint16), vf.astype(np.float16).view(np.uint16))
     q = rng.normal(0, 1, (T, nh * hd)).astype(np.float32)
     ob = device.alloc(T * nh * hd * 4)
-    suite.attention_execute_prefill(up(device, q), up(device, kc), up(device, vc), ob, hd, nh, nkv, pos0, T, max_seq)
-    want = orc.attention_prefill(q, kc, vc, orc.F32, hd, nh, nkv, pos0, T, max_seq)
-    assert rel_err(ob.read(), want) < 1e-4
+    suite.attention_execute_prefill(up(device, q), up(device, kc), up(device, vc), ob, hd, nh, nkv, pos0, T, max_seq,
+                                    cache_dtype=cache)
+    want = orc.attention_prefill(q, kc, vc, cache, hd, nh, nkv, pos0, T, max_seq)
+    assert rel_err(ob.read(), want) < 1e-4, rel_err(ob.read(), want)
 
 
 # ---- embedding, copy, greedy pick --------------------------------------------------------------
@@ -392,4 +402,22 @@ def test_gemm_nk_matches_oracle(device, suite, m, n, k, dtype):
     want = orc.gemv_nk(dtype, ws, xf)
     yb = device.alloc(m * n * 4)
     suite.gemm_nk(dtype, m, n, k, up(device, xs), up(device, ws), yb, l0.F32)
+    assert rel_err(yb.read().reshape(m, n), want) < 2e-5
+
+
+@pytest.mark.parametrize("m,n,k", [(64, 256, 512), (256, 768, 4096), (256, 512, 14336), (100, 200, 128),
+                                   (33, 48, 96), (128, 2048, 1024), (512, 320, 2048)])
+def test_gemm_nk_i8pc_matches_oracle(device, suite, m, n, k):
+    """int8 weights converted to fp16 in registers (exact), fp16 activations, fp32 accumulation,
+    row scale in the epilogue: the oracle's int8 per-channel product on the same fp16 inputs."""
+    rng = np.random.default_rng(3 * m + n + k)
+    x = rng.normal(0, 1, (m, k)).astype(np.float16)
+    q = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    q[0, :] = 127  # extremes of the byte range
+    q[-1, : k // 2] = -127
+    q[-1, k // 2:] = -128
+    sc = rng.uniform(1e-3, 1e-2, n).astype(np.float16).view(np.uint16)
+    want = orc.gemv_nk(l0.I8PC, q, x.astype(np.float32), sc)
+    yb = device.alloc(m * n * 4)
+    suite.gemm_nk_i8pc(m, n, k, up(device, x.view(np.uint16)), up(device, q), up(device, sc), yb, l0.F32)
     assert rel_err(yb.read().reshape(m, n), want) < 2e-5

@@ -118,6 +118,44 @@ def test_prefill_matches_sequential_decode(device):  # Qwen25PrefillTests.cs:41-
         assert np.max(np.abs(seq_after - after)) < 2e-3
 
 
+# Chunked prefill against token-by-token decode on a random-init model whose head size takes the
+# query-tiled prefill attention: 300 prompt tokens = a full 256-token chunk + a ragged one + the
+# last token through the decode step. fp32 weights run multi-row GEMVs on fp32 activations (the
+# decode arithmetic); int8 / fp16 / bf16 run the MFMA GEMM on activations rounded to fp16 / fp16 /
+# bf16, hence their looser bounds (relative to max |logit|).
+CHUNKED = [(l0.PRECISION_INT8, 1e-2), (l0.PRECISION_FLOAT32, 2e-3), (l0.PRECISION_FLOAT16, 1e-2),
+           (l0.PRECISION_BFLOAT16, 5e-2)]
+
+
+@pytest.mark.parametrize("precision,tol", CHUNKED)
+def test_chunked_prefill_matches_sequential_decode(device, precision, tol):
+    cfg = l0.HfConfig(hidden_size=256, intermediate_size=512, num_layers=3, num_attention_heads=4,
+                      num_key_value_heads=2, head_dim=64, vocab_size=512, max_position_embeddings=4096,
+                      rms_norm_eps=1e-5, rope_theta=500000.0, attention_bias=True)
+    prompt = np.random.default_rng(11).integers(0, cfg.vocab_size, 300).tolist()
+    with l0.LlmModel(device, cfg, precision=precision, cache_dtype=l0.F16, max_seq_len=320) as m:
+        m.init_random(1234, 0.05)
+        seq = None
+        for i, t in enumerate(prompt):
+            seq = m.compute_logits(t, i)
+        kv_elems = len(prompt) * 2 * 64
+
+        def keys(li):
+            return l0.Buffer(device, kv_elems * 2, ptr=m.kv_cache(li)[0], owned=False).read(np.float16, kv_elems)
+
+        k_seq = [keys(li) for li in range(3)]
+        batched = m.prefill(prompt)
+        assert m.position == len(prompt)
+        scale = np.max(np.abs(seq))
+        assert np.max(np.abs(seq - batched)) <= tol * scale, np.max(np.abs(seq - batched)) / scale
+        if int(np.argmax(batched)) != int(np.argmax(seq)):
+            assert orc.top2_margin(seq) < tol * scale
+        for li in range(3):  # keys of every prompt position (the last one written by the decode step)
+            a = k_seq[li].astype(np.float32)
+            b = keys(li).astype(np.float32)
+            assert np.max(np.abs(a - b)) <= 4 * tol * max(1.0, np.max(np.abs(a))), li
+
+
 def test_generate_greedy_matches_step_loop_and_stops(device):
     d = load_hf("llama")
     with load_model(device, d, l0.PRECISION_INT8, l0.F16) as m:
