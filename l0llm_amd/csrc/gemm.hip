@@ -1,23 +1,25 @@
-// Prefill GEMM on gfx950 MFMA: Y[M, N] = X[M, K] * W[N, K]^T, fp16 or bf16 operands, fp32
-// accumulation (the role of LlmMatrix.ProjectRows, LlmMatrix.cs:149-171, for M >= 64).
+// Prefill GEMM on gfx950 MFMA: Y[M, N] = X[M, K] * W[N, K]^T with fp16 or bf16 operands, or int8
+// weights (one fp16 scale per row) and fp16 activations; fp32 accumulation (the role of
+// LlmMatrix.ProjectRows, LlmMatrix.cs:149-171, for M >= 64).
 //
 // Both operands are K-contiguous, which is the layout v_mfma_f32_16x16x32_{bf16,f16} wants:
 // lane l holds A[l % 16][8 (l / 16) .. +7] and B[8 (l / 16) .. +7][l % 16] and receives
-// D[4 (l / 16) + r][l % 16], r < 4. So a lane's B operand for 16 columns and one K step of 32 is
-// 16 contiguous bytes of one weight row.
+// D[4 (l / 16) + r][l % 16], r < 4 (v_mfma_f32_32x32x16: rows / columns l % 32, K from 8 (l / 32),
+// 16 results per lane). So a lane's B operand for one MFMA is 16 contiguous bytes of one weight
+// row (8 bytes for int8, converted to fp16 in registers).
 //
 // A block of 4 waves computes BM rows x 4 NW columns; wave w owns NW columns and all BM rows.
 // The weights, which no two waves share, go from HBM straight into MFMA operand registers; only
 // the activation tile (BM x 32 per K step, read by all 4 waves) passes through LDS. That halves
 // the LDS traffic per MFMA against staging both operands (the LDS port, 128 bytes per clock per
 // CU, is what bounds a 64 x 64 wave tile with both operands in LDS). K steps pass through a ring
-// of P register stages: the loads of step t + P - 1 are issued while step t is computed, so P - 1
-// steps of weights are in flight per wave. Step t + 1's activation chunks go from their stage to
-// the LDS buffer the MFMAs are not reading (rows padded by 16 bytes, so the fragment reads of 16
-// rows hit distinct banks). Every global load is unconditional (rows past M / N and steps past
-// the end are clamped to valid addresses and never used), and the one barrier per step waits on
-// LDS only, so the in-order memory counter's waits are exact: the wait before step t + 1's
-// LDS store lets the P - 2 younger stages stay in flight.
+// of P register stages of one or two steps each: the loads of stage t + P - 1 are issued while
+// stage t is computed, so P - 1 stages of weights are in flight per wave. Stage t + 1's
+// activation chunks go from their ring slot to the LDS buffer the MFMAs are not reading (rows
+// padded by 16 bytes, so the fragment reads of 16 rows hit distinct banks). Every global load is
+// unconditional (rows past M / N and stages past the end are clamped to valid addresses and never
+// used), and the one barrier per stage waits on LDS only, so the in-order memory counter's waits
+// are exact: the wait before stage t + 1's LDS store lets the P - 2 younger stages stay in flight.
 //
 // Shapes with fewer blocks than the GPU has CUs split K across blocks into fp32 partials that a
 // second pass sums in a fixed order (deterministic). Blocks are renumbered so the blocks that
@@ -89,8 +91,10 @@ __device__ __forceinline__ int row_group(int gx) {
 }
 
 // Ring depth: deeper for tiles with fewer registers per stage, within a budget of 256 registers
-// per lane (two waves per SIMD) for all but the 128 x 64 wave tile.
+// per lane (two waves per SIMD) for all but the 128 x 64 wave tile. ring_depth2: stages of two
+// K steps (one barrier per 64 K), used when K splits into whole 64-wide stages (not for NW = 64).
 constexpr int ring_depth(int bm, int nw) { return nw == 64 ? 4 : (bm == 64 && nw == 16) ? 8 : 6; }
+constexpr int ring_depth2(int) { return 4; }
 
 // int8 weights: 8 signed bytes -> 8 exact fp16 values. Byte u = q + 128 (sign bit flipped) under
 // the fp16 exponent of 1024 reads as 1024 + u; subtracting 1152 leaves q. Bytes 0 and 2 (1 and 3)
@@ -113,7 +117,8 @@ __device__ __forceinline__ u32x4_t perm_f16x8(const uint4& a) {  // a0 a2 a1 a3 
 typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
 
 // WT: weight storage (F16, BF16, or I8PC with fp16 activations and one fp16 scale per weight row).
-template <int WT, int BM, int NW, bool NT, int P = ring_depth(BM, NW), int MF = (NW % 32 == 0 ? 32 : 16)>
+template <int WT, int BM, int NW, bool NT, int P = ring_depth(BM, NW), int MF = (NW % 32 == 0 ? 32 : 16),
+          int SPS = 1>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void gemm_nk_kernel(
     int M, int N, int K, int k_per_split, const uint16_t* __restrict__ X, const void* __restrict__ Wv,
     const uint16_t* __restrict__ scales, void* Y, int y_dtype, float* partial) {
@@ -127,7 +132,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     constexpr int WB = I8 ? 1 : 2;         // bytes per weight
     using breg = typename std::conditional<I8 && MF == 16, uint2, uint4>::type;
     static_assert(AC >= 1 && MI >= 1 && NJ >= 1, "tile too small");
-    __shared__ __attribute__((aligned(16))) uint16_t sa[2][BM * kLds];
+    __shared__ __attribute__((aligned(16))) uint16_t sa[2][SPS][BM * kLds];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     // Renumber blocks so that consecutive ids land on one XCD, then walk them as groups of G row
@@ -142,7 +147,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     const int bz = rest % gy, bn = (rest / gy) % gz, bm = (rest / (gy * gz)) * G + gr;
     const int m0 = bm * BM, nw0 = bn * 4 * NW + wave * NW;
     const int kbeg = bz * k_per_split;
-    const int nsteps = max(0, min(K, kbeg + k_per_split) - kbeg) / BK;
+    const int nsteps = max(0, min(K, kbeg + k_per_split) - kbeg) / (BK * SPS);  // stages of SPS K steps
     const int last = max(nsteps - 1, 0);
 
     // Operand lane layout: lane l holds row / column l % MF and, of MFMA q of the step, the 8
@@ -169,16 +174,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
         aptr[c] = X + (size_t)min(m0 + (idx >> 2), M - 1) * K + kbeg + (idx & 3) * 8;
     }
 
-    uint4 ra[P][AC];
-    breg rb[P][NB];
-    // Step t of this block's K range into a ring stage; steps past the end re-read the last one.
-    auto gload = [&](uint4 (&a)[AC], breg (&b)[NB], int t) {
-        const int k0 = min(t, last) * BK;
+    uint4 ra[P][SPS * AC];
+    breg rb[P][SPS * NB];
+    // Stage t (SPS K steps) of this block's K range into a ring slot; stages past the end re-read
+    // the last one.
+    auto gload = [&](uint4 (&a)[SPS * AC], breg (&b)[SPS * NB], int t) {
 #pragma unroll
-        for (int c = 0; c < AC; c++) a[c] = *reinterpret_cast<const uint4*>(aptr[c] + k0);
+        for (int u = 0; u < SPS; u++) {
+        const int k0 = (min(t, last) * SPS + u) * BK;
 #pragma unroll
-        for (int j = 0; j < NB; j++) {
-            const char* bp = bptr[j] + (size_t)k0 * WB;
+        for (int c = 0; c < AC; c++) a[u * AC + c] = *reinterpret_cast<const uint4*>(aptr[c] + k0);
+#pragma unroll
+        for (int jj = 0; jj < NB; jj++) {
+            const int j = u * NB + jj;
+            const char* bp = bptr[jj] + (size_t)k0 * WB;
             if constexpr (std::is_same<breg, uint2>::value) {
                 const u32x2_t v = NT ? __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(bp))
                                      : *reinterpret_cast<const u32x2_t*>(bp);
@@ -189,14 +198,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
                 b[j] = *reinterpret_cast<const uint4*>(bp);
             }
         }
+        }
     };
-    auto sstore = [&](const uint4 (&a)[AC], int buf) {
+    auto sstore = [&](const uint4 (&a)[SPS * AC], int buf) {
+#pragma unroll
+        for (int u = 0; u < SPS; u++)
 #pragma unroll
         for (int c = 0; c < AC; c++) {
             const int idx = tid + c * 256;
+            const uint4& v = a[u * AC + c];
             // As a vector value: a struct copy would keep the ring in memory instead of registers.
-            *reinterpret_cast<u32x4_t*>(&sa[buf][(idx >> 2) * kLds + (idx & 3) * 8]) =
-                I8 ? perm_f16x8(a[c]) : u32x4_t{a[c].x, a[c].y, a[c].z, a[c].w};
+            *reinterpret_cast<u32x4_t*>(&sa[buf][u][(idx >> 2) * kLds + (idx & 3) * 8]) =
+                I8 ? perm_f16x8(v) : u32x4_t{v.x, v.y, v.z, v.w};
         }
     };
 
@@ -206,9 +219,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
 #pragma unroll
         for (int j = 0; j < NJ; j++) acc[i][j] = acc_t<MF>{};
 
-    auto mma = [&](int buf, const breg (&b)[NB]) {
+    auto mma = [&](int buf, const breg (&bs)[SPS * NB]) {
+#pragma unroll
+        for (int u = 0; u < SPS; u++)
 #pragma unroll
         for (int q = 0; q < S; q++) {
+            const breg* b = bs + u * NB;
             uint4 bq[NJ];
 #pragma unroll
             for (int j = 0; j < NJ; j++) {
@@ -224,7 +240,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
             const int ak = (I8 && MF == 32) ? 16 * (lane / 32) + 8 * q : q * (512 / MF) + lk;
 #pragma unroll
             for (int i = 0; i < MI; i++) {
-                const uint4 af = *reinterpret_cast<const uint4*>(&sa[buf][(i * MF + li) * kLds + ak]);
+                const uint4 af = *reinterpret_cast<const uint4*>(&sa[buf][u][(i * MF + li) * kLds + ak]);
 #pragma unroll
                 for (int j = 0; j < NJ; j++) acc[i][j] = mfma<DT, MF>(af, bq[j], acc[i][j]);
             }
@@ -331,15 +347,32 @@ Plan plan_for(int m, int n, int k, int cus) {
 template <int WT, int BM, int NW>
 int launch_tiles(hipStream_t s, int m, int n, int k, const void* x, const void* w, const uint16_t* scales, void* y,
                  int y_dtype, int splits, float* ws) {
-    const int k_per_split = (k / BK + splits - 1) / splits * BK;
+    constexpr int MF = NW % 32 == 0 ? 32 : 16;
+    // Stages of two K steps where K allows, except the 128 x 64 wave tile (its two-step ring, with
+    // fewer stages to fit the registers, measured slower).
+    constexpr bool kTwo = NW != 64;
+    const bool two = kTwo && k % (2 * BK) == 0;
+    const int unit = two ? 2 * BK : BK;
+    const int k_per_split = (k / unit + splits - 1) / splits * unit;
     // The kernel decodes (row block, split, column block) from the linear block id; the grid only
     // has to hold that many blocks, in the order x = row blocks, y = splits, z = column blocks.
     dim3 grid(ceil_div(m, BM), splits, ceil_div(n, 4 * NW));
     const auto* xp = static_cast<const uint16_t*>(x);
     float* part = splits > 1 ? ws : nullptr;
-    if (grid.x == 1)  // each weight byte is read by one block: stream it past the caches
+    // One row block: each weight byte is read by one block, so it is streamed past the caches.
+    const bool nt = grid.x == 1;
+    if constexpr (kTwo) {
+        constexpr int P2 = ring_depth2(NW);
+        if (two && nt)
+            gemm_nk_kernel<WT, BM, NW, true, P2, MF, 2><<<grid, 256, 0, s>>>(m, n, k, k_per_split, xp, w, scales, y,
+                                                                           y_dtype, part);
+        else if (two)
+            gemm_nk_kernel<WT, BM, NW, false, P2, MF, 2><<<grid, 256, 0, s>>>(m, n, k, k_per_split, xp, w, scales, y,
+                                                                            y_dtype, part);
+    }
+    if (!two && nt)
         gemm_nk_kernel<WT, BM, NW, true><<<grid, 256, 0, s>>>(m, n, k, k_per_split, xp, w, scales, y, y_dtype, part);
-    else
+    else if (!two)
         gemm_nk_kernel<WT, BM, NW, false><<<grid, 256, 0, s>>>(m, n, k, k_per_split, xp, w, scales, y, y_dtype, part);
     int st = launch_status("gemm_nk");
     if (st || splits == 1) return st;
