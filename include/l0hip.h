@@ -263,6 +263,48 @@ int l0h_matrix_project_shared(l0h_device* dev, int rows, const float* x, int cou
 int l0h_matrix_destroy(l0h_matrix* m);
 
 /* ======================================================================
+ * Checkpoint ingest (SafetensorsReader.cs, SafetensorsCheckpoint.cs; host)
+ * ==================================================================== */
+
+typedef struct l0h_safetensors l0h_safetensors;
+
+/* Element types, in SafetensorsDType order (SafetensorsReader.cs:10-25). */
+#define L0H_ST_BOOL 0
+#define L0H_ST_U8 1
+#define L0H_ST_I8 2
+#define L0H_ST_I16 3
+#define L0H_ST_U16 4
+#define L0H_ST_F16 5
+#define L0H_ST_BF16 6
+#define L0H_ST_I32 7
+#define L0H_ST_U32 8
+#define L0H_ST_F32 9
+#define L0H_ST_F64 10
+#define L0H_ST_I64 11
+#define L0H_ST_U64 12
+
+/* SafetensorsCheckpoint.Open (SafetensorsCheckpoint.cs:41-70): a .safetensors file, or a
+ * directory holding model.safetensors.index.json and its shards, else model.safetensors. Every
+ * header is validated as SafetensorsReader.Open does (SafetensorsReader.cs:110-160, :300-430):
+ * L0H_ERR_INVALID_DATA for a malformed file, an index that disagrees with its shards or a tensor
+ * in two shards, L0H_ERR_UNSUPPORTED for an unknown dtype. */
+int l0h_safetensors_open(const char* path, l0h_safetensors** out);
+/* SafetensorsCheckpoint.Dispose. */
+int l0h_safetensors_close(l0h_safetensors* st);
+/* Number of tensors (SafetensorsCheckpoint.Count). */
+int l0h_safetensors_count(const l0h_safetensors* st, int* count);
+/* Tensor `index` in name order (SafetensorsTensorInfo): name, L0H_ST_* dtype, rank and the
+ * first max_rank dimensions; any output may be null. */
+int l0h_safetensors_info(const l0h_safetensors* st, int index, char* name, size_t name_bytes,
+                         int* dtype, int* rank, long long* shape, int max_rank);
+/* Index of `name`, or -1 when absent (SafetensorsCheckpoint.Contains). */
+int l0h_safetensors_find(const l0h_safetensors* st, const char* name, int* index);
+/* SafetensorsReader.ReadFloat32 (SafetensorsReader.cs:188-235): an F32, F16, BF16 or F64 tensor
+ * as fp32; count must equal its element count. */
+int l0h_safetensors_read_f32(const l0h_safetensors* st, const char* name, float* host_dst,
+                             size_t count);
+
+/* ======================================================================
  * LlmModel + LlmDecoderLayer (LlmModel.cs, LlmDecoderLayer.cs): a
  * Llama/Qwen2-style decoder resident on the device.
  * ==================================================================== */
@@ -307,6 +349,12 @@ int l0h_model_init_random(l0h_model* model, uint64_t seed, float std);
  * follows LlmMatrix.FromHuggingFace's rule for Auto precision. */
 int l0h_model_set_tensor(l0h_model* model, const char* name, const float* host_data,
                          size_t count, int sixteen_bit_source);
+/* LlmModel.Load's weight pass (LlmLayerWeights.Load, LlmLayerWeights.cs:110-212; LlmModel.cs:
+ * 55-63): every tensor the config needs, read from the checkpoint as fp32 and stored by
+ * l0h_model_set_tensor (F16 / BF16 sources flagged as 16-bit). lm_head.weight is not read when
+ * the embeddings are tied. L0H_ERR_INVALID_DATA when a tensor is missing or its shape is not the
+ * config's. *loaded (may be null) receives the number of tensors read. */
+int l0h_model_load_safetensors(l0h_model* model, const l0h_safetensors* st, int* loaded);
 /* Reads back a projection as stored, in HuggingFace [out, in] order: storage type, weights
  * (out*in elements of the storage type: int8 / fp16 / bf16 / fp32) and, for int8, fp16 scales. */
 int l0h_model_export_matrix(l0h_model* model, const char* name, int* storage, int* out_dim,

@@ -7,13 +7,13 @@ library is an ImportError, never a CPU fallback."""
 from ._lib import (BF16, F16, F32, I8PC, PRECISION_AUTO, PRECISION_BFLOAT16, PRECISION_FLOAT16,
                    PRECISION_FLOAT32, PRECISION_INT8, DeviceError, InvalidArgumentError, InvalidDataError,
                    InvalidOperationError, L0hError, UnsupportedError, declared_functions, lib)
-from .api import (Buffer, Device, HfConfig, LlmKernelSuite, LlmMatrix, LlmModel, RopeScaling, fits_in_half,
-                  quantize_i8pc, rope_frequencies, runtime_is_available, transpose)
+from .api import (Buffer, Device, HfConfig, LlmKernelSuite, LlmMatrix, LlmModel, RopeScaling, SafetensorsCheckpoint,
+                  fits_in_half, quantize_i8pc, rope_frequencies, runtime_is_available, transpose)
 
 __all__ = [
     "BF16", "F16", "F32", "I8PC", "PRECISION_AUTO", "PRECISION_BFLOAT16", "PRECISION_FLOAT16", "PRECISION_FLOAT32",
     "PRECISION_INT8", "Buffer", "Device", "DeviceError", "HfConfig", "InvalidArgumentError", "InvalidDataError",
     "InvalidOperationError", "L0hError", "LlmKernelSuite", "LlmMatrix", "LlmModel", "RopeScaling",
-    "UnsupportedError", "declared_functions", "fits_in_half", "lib", "quantize_i8pc", "rope_frequencies",
+    "SafetensorsCheckpoint", "UnsupportedError", "declared_functions", "fits_in_half", "lib", "quantize_i8pc", "rope_frequencies",
     "runtime_is_available", "transpose",
 ]

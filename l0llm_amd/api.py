@@ -415,6 +415,63 @@ class HfConfig:
                            s.low_freq_factor, s.high_freq_factor, int(s.truncate))
 
 
+ST_DTYPES = ("BOOL", "U8", "I8", "I16", "U16", "F16", "BF16", "I32", "U32", "F32", "F64", "I64", "U64")
+
+
+class SafetensorsCheckpoint:
+    """SafetensorsCheckpoint (SafetensorsCheckpoint.cs): one .safetensors file, or a directory with
+    model.safetensors.index.json and its shards, else model.safetensors. Host only."""
+
+    def __init__(self, path: str):
+        h = ctypes.c_void_p()
+        check(lib.l0h_safetensors_open(str(path).encode(), ctypes.byref(h)))
+        self.handle = h
+
+    def __len__(self) -> int:
+        n = ctypes.c_int()
+        check(lib.l0h_safetensors_count(self.handle, ctypes.byref(n)))
+        return n.value
+
+    def info(self, index: int) -> tuple[str, str, tuple[int, ...]]:
+        """(name, dtype, shape) of tensor `index` in name order."""
+        name = ctypes.create_string_buffer(1024)
+        dt, rank = ctypes.c_int(), ctypes.c_int()
+        shape = (ctypes.c_longlong * 16)()
+        check(lib.l0h_safetensors_info(self.handle, index, name, 1024, ctypes.byref(dt), ctypes.byref(rank), shape, 16))
+        return name.value.decode(), ST_DTYPES[dt.value], tuple(shape[i] for i in range(rank.value))
+
+    @property
+    def names(self) -> list[str]:
+        return [self.info(i)[0] for i in range(len(self))]
+
+    def __contains__(self, name: str) -> bool:
+        i = ctypes.c_int()
+        check(lib.l0h_safetensors_find(self.handle, name.encode(), ctypes.byref(i)))
+        return i.value >= 0
+
+    def read_float32(self, name: str) -> np.ndarray:
+        """SafetensorsReader.ReadFloat32: F32 / F16 / BF16 / F64 as fp32, in the stored shape."""
+        i = ctypes.c_int()
+        check(lib.l0h_safetensors_find(self.handle, name.encode(), ctypes.byref(i)))
+        if i.value < 0:
+            raise KeyError(name)
+        _, _, shape = self.info(i.value)
+        out = np.empty(shape, dtype=np.float32)
+        check(lib.l0h_safetensors_read_f32(self.handle, name.encode(), out.ctypes.data_as(ctypes.c_void_p), out.size))
+        return out
+
+    def close(self) -> None:
+        if self.handle:
+            check(lib.l0h_safetensors_close(self.handle))
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+
 KERNEL_KINDS = ("embedding", "qkv", "attention", "o_proj", "gate_up", "down", "lm_head", "argmax")
 
 
@@ -447,6 +504,18 @@ class LlmModel:
         a = np.ascontiguousarray(data, dtype=np.float32).reshape(-1)
         check(lib.l0h_model_set_tensor(self.handle, name.encode(), a.ctypes.data_as(ctypes.c_void_p), a.size,
                                        int(sixteen_bit_source)))
+
+    def load_safetensors(self, checkpoint: "SafetensorsCheckpoint | str") -> int:
+        """LlmModel.Load's weight pass from a safetensors checkpoint; returns the tensors read."""
+        own = not isinstance(checkpoint, SafetensorsCheckpoint)
+        ck = SafetensorsCheckpoint(checkpoint) if own else checkpoint
+        try:
+            n = ctypes.c_int()
+            check(lib.l0h_model_load_safetensors(self.handle, ck.handle, ctypes.byref(n)))
+            return n.value
+        finally:
+            if own:
+                ck.close()
 
     def export_matrix(self, name: str) -> tuple[int, np.ndarray, np.ndarray | None]:
         st, n, k = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()

@@ -13,6 +13,7 @@
 // token and position live in device memory, so the whole step is captured once as a HIP graph
 // and replayed (the reference records one command list per token); the argmax can feed the
 // chosen token and the next position back on the device for back-to-back greedy decode.
+#include <algorithm>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -857,6 +858,49 @@ int l0h_model_set_tensor(l0h_model* m, const char* name, const float* host, size
     l0h_free(m->dev, tmp);
     if (tmp_s) l0h_free(m->dev, tmp_s);
     return st;
+}
+
+int l0h_model_load_safetensors(l0h_model* m, const l0h_safetensors* ck, int* loaded) {
+    int st = check_ready(m);
+    if (st) return st;
+    L0H_CHECK_ARG(ck, "checkpoint is null");
+    if (loaded) *loaded = 0;
+    const auto& c = m->cfg;
+    std::vector<std::string> names = {"model.embed_tokens.weight", "model.norm.weight"};
+    if (!c.tie_word_embeddings) names.push_back("lm_head.weight");
+    for (int i = 0; i < c.num_layers; i++) {
+        const std::string p = "model.layers." + std::to_string(i) + ".";
+        for (const char* n : {"input_layernorm.weight", "post_attention_layernorm.weight", "self_attn.q_proj.weight",
+                              "self_attn.k_proj.weight", "self_attn.v_proj.weight", "self_attn.o_proj.weight",
+                              "mlp.gate_proj.weight", "mlp.up_proj.weight", "mlp.down_proj.weight"})
+            names.push_back(p + n);
+        if (c.attention_bias)
+            for (const char* n : {"self_attn.q_proj.bias", "self_attn.k_proj.bias", "self_attn.v_proj.bias"})
+                names.push_back(p + n);
+    }
+    std::vector<float> buf;
+    for (const auto& name : names) {
+        Target t;
+        if ((st = resolve(m, name, t))) return st;
+        std::vector<long long> want;
+        if (t.vec) want = {(long long)t.vec_count};
+        else want = {(long long)t.n, (long long)t.k};
+        int idx = -1, dtype = 0, rank = 0;
+        long long shape[8] = {0};
+        if ((st = l0h_safetensors_find(ck, name.c_str(), &idx))) return st;
+        if (idx < 0) return fail(L0H_ERR_INVALID_DATA, "tensor '" + name + "' is missing from the checkpoint");
+        if ((st = l0h_safetensors_info(ck, idx, nullptr, 0, &dtype, &rank, shape, 8))) return st;
+        if (rank != (int)want.size() || !std::equal(want.begin(), want.end(), shape))
+            return fail(L0H_ERR_INVALID_DATA, "tensor '" + name + "' has a shape other than the config's");
+        size_t count = 1;
+        for (long long d : want) count *= (size_t)d;
+        buf.resize(count);
+        if ((st = l0h_safetensors_read_f32(ck, name.c_str(), buf.data(), count))) return st;
+        const int sixteen = dtype == L0H_ST_F16 || dtype == L0H_ST_BF16;
+        if ((st = l0h_model_set_tensor(m, name.c_str(), buf.data(), count, sixteen))) return st;
+        if (loaded) ++*loaded;
+    }
+    return L0H_OK;
 }
 
 int l0h_model_export_matrix(l0h_model* m, const char* name, int* storage, int* out_dim, int* in_dim, void* host_w,

@@ -387,8 +387,10 @@ def test_recording_matches_eager_and_replays(device, suite):
 
 # ---- MFMA prefill GEMM -------------------------------------------------------------------------
 
+# Stages of two K steps (K % 64 == 0), one K step (K % 64 == 32: (96, 300, 160)), the 128 x 64
+# wave tile (512 x 16384), K splits, ragged M / N, and the any-shape fallback (K % 32 != 0).
 @pytest.mark.parametrize("m,n,k", [(64, 256, 512), (128, 3072, 2048), (512, 2048, 2048), (100, 200, 128),
-                                   (128, 64, 8192), (33, 40, 70)])
+                                   (128, 64, 8192), (33, 40, 70), (96, 300, 160), (512, 1024, 256)])
 @pytest.mark.parametrize("dtype", [l0.BF16, l0.F16])
 def test_gemm_nk_matches_oracle(device, suite, m, n, k, dtype):
     rng = np.random.default_rng(m + n + k)
@@ -421,3 +423,13 @@ def test_gemm_nk_i8pc_matches_oracle(device, suite, m, n, k):
     yb = device.alloc(m * n * 4)
     suite.gemm_nk_i8pc(m, n, k, up(device, x.view(np.uint16)), up(device, q), up(device, sc), yb, l0.F32)
     assert rel_err(yb.read().reshape(m, n), want) < 2e-5
+
+
+def test_gemm_nk_i8pc_rejects_bad_shapes(device, suite):
+    x, w, sc, y = device.alloc(64 * 96 * 2), device.alloc(64 * 96), device.alloc(64 * 2), device.alloc(64 * 64 * 4)
+    with pytest.raises(l0.UnsupportedError):  # K not a multiple of 32
+        suite.gemm_nk_i8pc(64, 64, 80, x, w, sc, y, l0.F32)
+    with pytest.raises(l0.InvalidArgumentError):
+        suite.gemm_nk_i8pc(64, 64, 96, x, w, None, y, l0.F32)
+    with pytest.raises(l0.InvalidArgumentError):
+        suite.gemm_nk_i8pc(0, 64, 96, x, w, sc, y, l0.F32)

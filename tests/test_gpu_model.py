@@ -156,6 +156,56 @@ def test_chunked_prefill_matches_sequential_decode(device, precision, tol):
             assert np.max(np.abs(a - b)) <= 4 * tol * max(1.0, np.max(np.abs(a))), li
 
 
+@pytest.mark.parametrize("name,precision", [("qwen2", l0.PRECISION_INT8), ("llama", l0.PRECISION_BFLOAT16)])
+def test_model_loads_from_safetensors(device, tmp_path, name, precision):
+    """LlmModel.Load's weight pass from a sharded safetensors checkpoint (bf16 tensors, as HF
+    checkpoints ship) stores exactly what set_tensor stores from the same values."""
+    import json
+    import torch
+    from safetensors.torch import save_file
+    d = load_hf(name)
+    ws = {k: torch.from_numpy(np.ascontiguousarray(v, dtype=np.float32)).to(torch.bfloat16) for k, v in d["weights"].items()}
+    if d["cfg"]["tie_word_embeddings"]:
+        ws.pop("lm_head.weight", None)
+    names = sorted(ws)
+    half = len(names) // 2
+    shards = {"model-00001-of-00002.safetensors": names[:half], "model-00002-of-00002.safetensors": names[half:]}
+    for f, ns in shards.items():
+        save_file({n: ws[n] for n in ns}, str(tmp_path / f))
+    wm = {n: f for f, ns in shards.items() for n in ns}
+    (tmp_path / "model.safetensors.index.json").write_text(json.dumps({"metadata": {}, "weight_map": wm}))
+    with load_model(device, {"cfg": d["cfg"], "weights": {}}, precision, l0.F16) as a, \
+            load_model(device, {"cfg": d["cfg"], "weights": {}}, precision, l0.F16) as b:
+        assert a.load_safetensors(tmp_path) == len(names)
+        for n in names:
+            b.set_tensor(n, ws[n].float().numpy(), sixteen_bit_source=True)
+        for n in names:
+            if n.endswith("proj.weight") or n == "lm_head.weight":
+                sa, wa, sca = a.export_matrix(n)
+                sb, wb, scb = b.export_matrix(n)
+                assert sa == sb
+                np.testing.assert_array_equal(wa.view(np.uint8), wb.view(np.uint8))
+                if sca is not None:
+                    np.testing.assert_array_equal(sca, scb)
+        for t, tok in enumerate(d["prompt"][:5]):
+            np.testing.assert_array_equal(a.compute_logits(tok, t), b.compute_logits(tok, t))
+
+
+def test_model_load_rejects_missing_or_misshapen_tensors(device, tmp_path):
+    from safetensors.numpy import save_file
+    d = load_hf("llama")
+    ws = {k: np.ascontiguousarray(v, dtype=np.float32) for k, v in d["weights"].items()}
+    save_file({k: v for k, v in ws.items() if k != "model.norm.weight"}, str(tmp_path / "missing.safetensors"))
+    bad = dict(ws)
+    bad["model.layers.0.mlp.down_proj.weight"] = np.ascontiguousarray(bad["model.layers.0.mlp.down_proj.weight"].T)
+    save_file(bad, str(tmp_path / "transposed.safetensors"))
+    with load_model(device, {"cfg": d["cfg"], "weights": {}}, l0.PRECISION_INT8, l0.F16) as m:
+        with pytest.raises(l0.InvalidDataError):
+            m.load_safetensors(tmp_path / "missing.safetensors")
+        with pytest.raises(l0.InvalidDataError):
+            m.load_safetensors(tmp_path / "transposed.safetensors")
+
+
 def test_generate_greedy_matches_step_loop_and_stops(device):
     d = load_hf("llama")
     with load_model(device, d, l0.PRECISION_INT8, l0.F16) as m:
