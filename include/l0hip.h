@@ -124,7 +124,7 @@ int l0h_gemv_execute_rows(l0h_device* dev, int rows, int out_dim, int in_dim, co
 /* Gemm.Execute(dev, M, N, K, x, W, y) (LlmMatrix.cs:142, :169): fp32 [M,K] x [K,N]. */
 int l0h_gemm_execute(l0h_device* dev, int m, int n, int k, const float* x, const float* w,
                      float* y);
-/* GemvQ8.Execute / ExecuteRows (LlmMatrix.cs:130, :157, :235, :239) in this build's int8 format:
+/* GemvQ8.Execute / ExecuteRows (LlmMatrix.cs:130, :157, :235, :239) in the weight-only int8 format:
  * weight-only int8 [N, K] with one fp16 scale per output row, fp32 x and y. The reference's
  * GemvQ8.Quantize step (activation quantization) has no counterpart: activations stay fp32. */
 int l0h_gemv_q8_execute_rows(l0h_device* dev, int rows, int out_dim, int in_dim, const float* x,
@@ -179,7 +179,7 @@ int l0h_sampling_execute(l0h_device* dev, const float* logits, int* sampled, flo
                          float random_val, int vocab);
 
 /* ======================================================================
- * Weight-streaming kernels in the BASELINE formats (HuggingFace [N, K]
+ * Weight-streaming kernels in the [N, K] weight formats (HuggingFace [N, K]
  * weight layout; the role of Gemv / GemvQ8 / Gemm in LlmMatrix.cs:122-218)
  * ==================================================================== */
 

@@ -224,7 +224,7 @@ class LlmKernelSuite:
         check(lib.l0h_sampling_execute(self.device.handle, _ptr(logits), _ptr(sampled), ctypes.c_float(temperature),
                                        ctypes.c_float(random_val), vocab))
 
-    # BASELINE-format kernels
+    # [N, K] weight-format kernels (int8 weight-only per row, fp16, bf16, fp32)
     def gemv_nk(self, w_dtype, rows, out_dim, in_dim, x, x_dtype, w, scales, y, y_dtype):
         check(lib.l0h_gemv_nk(self.device.handle, w_dtype, rows, out_dim, in_dim, _ptr(x), x_dtype, _ptr(w),
                               _ptr(scales), _ptr(y), y_dtype))

@@ -3,7 +3,7 @@
 // Storage rules follow LlmMatrix.Upload / FromHuggingFace (:44-57, :80-106): int8 when asked
 // for and the shape allows it (out % 4 == 0, in % 32 == 0) and every value fits a half; else
 // half when asked for (Float16) or when the source is 16-bit and fits; else fp32. BFloat16 is
-// this build's addition for bf16 checkpoints kept as bf16. Unlike the reference, which stores
+// an addition for bf16 checkpoints kept as bf16. Unlike the reference, which stores
 // fp paths transposed to [in, out], every storage type keeps the [out, in] order on the device:
 // that is the layout the weight-streaming GEMV reads row by row, so Upload transposes its
 // [in, out] input once on the host.

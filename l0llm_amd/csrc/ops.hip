@@ -1,6 +1,7 @@
-// C-ABI entry points for the LlmKernelSuite operators (reference-shaped, fp32 activations)
-// and for the BASELINE-format kernels. Argument checks mirror the reference's exceptions
-// (LlmMatrix.cs:46-50, LlmDecoderLayer.cs:131-159) as L0H_ERR_* codes.
+// C-ABI entry points for the LlmKernelSuite operators (reference-shaped, fp32 activations) and
+// for the [N, K] weight-format kernels (int8 weight-only per row, fp16, bf16). Argument checks
+// mirror the reference's exceptions (LlmMatrix.cs:46-50, LlmDecoderLayer.cs:131-159) as L0H_ERR_*
+// codes.
 #include "kernels.h"
 
 #include <cmath>

@@ -60,7 +60,7 @@ void orc_quantize_i8pc(const float* w, int N, int K, int8_t* q, uint16_t* s16);
  * y[r, n] = sum_k x[r, k] * W[n, k] (* s[n] for I8PC), fp64 accumulation.
  * W is [N, K] row-major (HuggingFace [out, in]); x is [rows, K] fp32; y is
  * [rows, N] fp32. Semantics of Gemv/GemvQ8 Execute and ExecuteRows
- * (LlmMatrix.cs:122-171), with BASELINE's per-channel int8 format.
+ * (LlmMatrix.cs:122-171), with the weight-only per-row int8 format.
  */
 void orc_gemv_nk(int wdtype, int rows, int N, int K, const float* x, const void* W,
                  const uint16_t* scales, float* y);
