@@ -276,7 +276,7 @@ def main() -> int:
         os.environ["L0H_EAGER_STEP"] = "1"  # read by the library when the model is created
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: the path runs on a single GPU (no sharding or collectives "
-              "in this build); run it with --gpus 1.", file=sys.stderr)
+              "are implemented); run it with --gpus 1.", file=sys.stderr)
         return 2
 
     import l0llm_amd as l0
