@@ -94,6 +94,10 @@ struct l0h_model {
     l0h_model_config cfg{};
     int storage = L0H_I8PC;  // projection storage
     int cache_dtype = L0H_F16;
+    // Activations that only feed a projection (attention output -> O, SwiGLU output -> down):
+    // fp16 for int8 / 16-bit weights (half the bytes those GEMVs stage; finer than the
+    // reference's int8 quantization of the same vectors), fp32 for fp32 weights.
+    int act_dtype = L0H_F32;
     int max_seq = 0;
     int qd = 0, kvd = 0, rot = 0;
     float rope_scale = 1.f;
@@ -315,10 +319,12 @@ double op_bytes(const l0h_model* m, int kind, int position) {
     switch (kind) {
     case L0H_KERNEL_EMBEDDING: return 8.0 * H;
     case L0H_KERNEL_QKV: return gemv_bytes(m, m->qd + 2 * m->kvd, c.hidden_size, 8.0 * H + 4.0 * qd + 2.0 * kvd * ci);
-    case L0H_KERNEL_ATTENTION: return 2.0 * (position + 1) * kvd * ci + 8.0 * qd;
-    case L0H_KERNEL_O_PROJ: return gemv_bytes(m, c.hidden_size, m->qd, 4.0 * qd + 8.0 * H);
-    case L0H_KERNEL_GATE_UP: return gemv_bytes(m, 2 * c.intermediate_size, c.hidden_size, 8.0 * H + 4.0 * I);
-    case L0H_KERNEL_DOWN: return gemv_bytes(m, c.hidden_size, c.intermediate_size, 4.0 * I + 8.0 * H);
+    case L0H_KERNEL_ATTENTION: return 2.0 * (position + 1) * kvd * ci + (4.0 + dtype_size(m->act_dtype)) * qd;
+    case L0H_KERNEL_O_PROJ: return gemv_bytes(m, c.hidden_size, m->qd, dtype_size(m->act_dtype) * qd + 8.0 * H);
+    case L0H_KERNEL_GATE_UP:
+        return gemv_bytes(m, 2 * c.intermediate_size, c.hidden_size, 8.0 * H + dtype_size(m->act_dtype) * I);
+    case L0H_KERNEL_DOWN:
+        return gemv_bytes(m, c.hidden_size, c.intermediate_size, dtype_size(m->act_dtype) * I + 8.0 * H);
     case L0H_KERNEL_LM_HEAD: return gemv_bytes(m, c.vocab_size, c.hidden_size, 8.0 * H + 4.0 * c.vocab_size);
     default: return 4.0 * c.vocab_size;  // argmax reads the logits
     }
@@ -370,7 +376,7 @@ int launch_op(l0h_model* m, hipStream_t s, int kind, int li) {
         a.vc = L.v_cache;
         a.cache_dtype = m->cache_dtype;
         a.out = m->attn;
-        a.out_dtype = L0H_F32;
+        a.out_dtype = m->act_dtype;
         a.batch = 1;
         a.head_dim = c.head_dim;
         a.nh = c.num_attention_heads;
@@ -389,6 +395,7 @@ int launch_op(l0h_model* m, hipStream_t s, int kind, int li) {
         g.n = H;
         g.k = m->qd;
         g.x = m->attn;
+        g.x_dtype = m->act_dtype;
         g.epilogue = EPI_RESIDUAL;
         g.resid = m->hidden;
         return launch_gemv_nk(s, g);
@@ -404,7 +411,7 @@ int launch_op(l0h_model* m, hipStream_t s, int kind, int li) {
         g.eps = c.rms_norm_eps;
         g.epilogue = EPI_SWIGLU;
         g.y = m->act;
-        g.y_dtype = L0H_F32;
+        g.y_dtype = m->act_dtype;
         return launch_gemv_nk(s, g);
     }
     case L0H_KERNEL_DOWN: {  // LlmDecoderLayer.cs:190-194
@@ -414,6 +421,7 @@ int launch_op(l0h_model* m, hipStream_t s, int kind, int li) {
         g.n = H;
         g.k = c.intermediate_size;
         g.x = m->act;
+        g.x_dtype = m->act_dtype;
         g.epilogue = EPI_RESIDUAL;
         g.resid = m->hidden;
         return launch_gemv_nk(s, g);
@@ -685,6 +693,7 @@ int l0h_model_create(l0h_device* dev, const l0h_model_config* cfg, int precision
     m->cfg = c;
     m->storage = storage;
     m->cache_dtype = cache_dtype;
+    m->act_dtype = storage == L0H_F32 ? L0H_F32 : L0H_F16;
     m->max_seq = max_seq_len;
     const char* eager_env = std::getenv("L0H_EAGER_STEP");
     m->eager = eager_env && std::atoi(eager_env) != 0;
