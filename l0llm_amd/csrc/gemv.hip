@@ -38,14 +38,16 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_generic_kernel(const GemvParam
 
 }  // namespace
 
-int gemv_max_blocks(int compute_units) {
-    // L0H_GEMV_BLOCKS_PER_CU overrides the default (0: one block per 4 row groups, no cap).
-    static const int per_cu = [] {
+int gemv_max_blocks(int compute_units, int per_cu) {
+    // L0H_GEMV_BLOCKS_PER_CU overrides every launch's value (tuning; 0: one block per 4 row
+    // groups, no cap).
+    static const int env = [] {
         const char* e = std::getenv("L0H_GEMV_BLOCKS_PER_CU");
-        const int v = e ? std::atoi(e) : 4;
-        return v >= 0 ? v : 4;
+        const int v = e ? std::atoi(e) : -1;
+        return v >= 0 ? v : -1;
     }();
-    return per_cu == 0 ? 0 : std::max(1, compute_units) * per_cu;
+    const int n = env >= 0 ? env : per_cu;
+    return n == 0 ? 0 : std::max(1, compute_units) * n;
 }
 
 int launch_gemv_nk(hipStream_t s, const GemvParams& p0) {

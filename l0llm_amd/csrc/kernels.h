@@ -49,8 +49,11 @@ struct GemvParams {
     int compute_units = 0;  // with max_blocks: caps the grid at the blocks resident in one round
 };
 
-// Persistent-grid size for weight-streaming kernels on a device with `compute_units` CUs.
-int gemv_max_blocks(int compute_units);
+// Persistent-grid size for weight-streaming kernels on a device with `compute_units` CUs:
+// per_cu blocks of 4 waves per CU. Two is the measured best for the 8B decode shapes except the
+// down projection (three): a CU returns data in order, and fewer blocks per CU means fewer
+// blocks whose activation row waits behind a neighbour's weight stream.
+int gemv_max_blocks(int compute_units, int per_cu = 2);
 
 int launch_gemv_nk(hipStream_t s, const GemvParams& p);
 
