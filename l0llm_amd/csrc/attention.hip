@@ -691,11 +691,195 @@ int launch_prefill_tiled(hipStream_t s, const AttnParams& p, int pos0, int token
     return launch_status("attn_prefill_tiled");
 }
 
+// ---------------------------------------------------------------------------------------------
+// Causal prefill on MFMA (fp16 cache): the same block tiling as the fp32 kernel (64 query vectors
+// of one kv head, K / V tiles of 64 positions), with wave w owning query vectors 16 w .. 16 w + 15.
+// Scores are computed transposed, S^T = K Q^T, with v_mfma_f32_16x16x32_f16 (K fragments from LDS,
+// the wave's Q fragments in registers, fp16, pre-scaled by log2(e) / sqrt(d)): lane l then holds,
+// for query l % 16, the 16 positions 16 j + 4 (l / 16) + r of the tile (j, r < 4). Those values,
+// after the online softmax (fp32, the row spread over the 4 lanes l % 16 + 16 g), are exactly a
+// B operand of the P.V MFMA O^T += V^T P^T when its 32 K slots of a chunk c are the positions
+// 32 c + 4 g + e (e < 4) and 32 c + 16 + 4 g + (e - 4) — so V is staged transposed in LDS and each
+// lane reads its V^T operand as two 8-byte runs. O^T accumulates in registers (dims 16 i + 4 g + r
+// of query l % 16). P is rounded to fp16 for the MFMA; the softmax sums stay fp32.
+// ---------------------------------------------------------------------------------------------
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8_t;
+typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+
+__device__ __forceinline__ uint32_t pack_half2(float a, float b) {
+    return (uint32_t)__half_as_ushort(__float2half_rn(a)) | ((uint32_t)__half_as_ushort(__float2half_rn(b)) << 16);
+}
+
+template <int HD, int QT>
+__global__ __launch_bounds__(kBlock) void attn_prefill_mfma_kernel(const AttnParams p, int pos0, int tokens,
+                                                                   int gsize, int tq_tokens) {
+    constexpr int KLD = HD + 8;        // K tile row stride (halves): 16 rows hit distinct banks
+    constexpr int VLD = kPK + 8;       // V^T tile row stride (halves)
+    constexpr int CPR = HD / 8;        // 16-byte chunks per cache row
+    constexpr int NC = kPK * CPR / kBlock;  // chunks per thread per tile (K, and again V)
+    constexpr int KS = HD / 32;        // MFMA K steps over the head dim
+    constexpr int NI = HD / 16;        // 16-dim output sub-tiles
+    static_assert(NC >= 1 && (kPK * CPR) % kBlock == 0, "tile / block mismatch");
+    __shared__ __attribute__((aligned(16))) uint16_t Ks[kPK * KLD];
+    __shared__ __attribute__((aligned(16))) uint16_t Vt[HD * VLD];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lq = lane & 15, lg = lane >> 4;
+    const int g = blockIdx.y;
+    const int t0 = blockIdx.x * tq_tokens;
+    const int t_last = min(t0 + tq_tokens, tokens) - 1;
+    const int kmax = pos0 + t_last;
+    const int row_elems = p.nkv * HD;
+    const uint16_t* kc = static_cast<const uint16_t*>(p.kc);
+    const uint16_t* vc = static_cast<const uint16_t*>(p.vc);
+
+    // This lane's query vector: i = 16 wave + l % 16 -> token t0 + i / gsize, head g gsize + i % gsize.
+    const int qi = wave * 16 + lq;
+    const int qtok = qi / gsize;
+    const bool qvalid = qtok < tq_tokens && t0 + qtok < tokens;
+    const int lim = qvalid ? pos0 + t0 + qtok : -1;
+    const float qscale = 1.4426950408889634f / sqrtf((float)HD);
+    uint4 qf[KS];  // Q[qi][32 kk + 8 lg .. +7] as fp16
+#pragma unroll
+    for (int kk = 0; kk < KS; kk++) {
+        float f[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        if (qvalid)
+            load8<QT>(p.q, (size_t)(t0 + qtok) * p.nh * HD + (size_t)(g * gsize + qi % gsize) * HD + 32 * kk + 8 * lg, f);
+        qf[kk] = make_uint4(pack_half2(f[0] * qscale, f[1] * qscale), pack_half2(f[2] * qscale, f[3] * qscale),
+                            pack_half2(f[4] * qscale, f[5] * qscale), pack_half2(f[6] * qscale, f[7] * qscale));
+    }
+
+    // Tile kt: chunk c of this thread is position (tid + c * kBlock) / CPR, dims 8 * ((...) % CPR).
+    uint4 kr[NC], vr[NC];
+    auto load_tile = [&](int kt) {
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            const int q = tid + c * kBlock, r = q / CPR, col = q % CPR;
+            const int pos = min(kt * kPK + r, kmax);
+            const size_t off = (size_t)pos * row_elems + (size_t)g * HD + col * 8;
+            kr[c] = ld_nt16(kc + off);
+            vr[c] = ld_nt16(vc + off);
+        }
+    };
+    auto store_tile = [&]() {
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            const int q = tid + c * kBlock, r = q / CPR, col = q % CPR;
+            *reinterpret_cast<u32x4_t*>(&Ks[r * KLD + col * 8]) = u32x4_t{kr[c].x, kr[c].y, kr[c].z, kr[c].w};
+            const uint32_t w[4] = {vr[c].x, vr[c].y, vr[c].z, vr[c].w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                Vt[(col * 8 + 2 * e) * VLD + r] = (uint16_t)(w[e] & 0xFFFFu);
+                Vt[(col * 8 + 2 * e + 1) * VLD + r] = (uint16_t)(w[e] >> 16);
+            }
+        }
+    };
+
+    float m = -INFINITY, l = 0.f;
+    f32x4_t o[NI];
+#pragma unroll
+    for (int i = 0; i < NI; i++) o[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    const int ntiles = kmax / kPK + 1;
+    load_tile(0);
+    for (int kt = 0; kt < ntiles; kt++) {
+        __syncthreads();  // the previous tile is no longer read
+        store_tile();
+        if (kt + 1 < ntiles) load_tile(kt + 1);
+        __syncthreads();
+
+        // S^T sub-tiles j: rows = positions 16 j .. 16 j + 15, columns = this wave's 16 queries.
+        f32x4_t st[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            st[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kk = 0; kk < KS; kk++) {
+                const uint4 a = *reinterpret_cast<const uint4*>(&Ks[(16 * j + lq) * KLD + 32 * kk + 8 * lg]);
+                st[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                               __builtin_bit_cast(f16x8_t, qf[kk]), st[j], 0, 0, 0);
+            }
+        }
+        // Online softmax for query l % 16 over the tile's 64 positions (this lane: 16 of them).
+        float mt = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int pos = kt * kPK + 16 * j + 4 * lg + r;
+                if (pos > lim) st[j][r] = -INFINITY;
+                mt = fmaxf(mt, st[j][r]);
+            }
+        mt = fmaxf(mt, __shfl_xor(mt, 16));
+        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        const float mn = fmaxf(m, mt);
+        const float corr = mn == -INFINITY ? 1.f : exp2f(m - mn);
+        float ps = 0.f;
+        uint32_t ph[4][2];  // P as fp16 pairs: sub-tile j, rows r = 0,1 and 2,3
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            float pr[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                pr[r] = mn == -INFINITY ? 0.f : exp2f(st[j][r] - mn);
+                ps += pr[r];
+            }
+            ph[j][0] = pack_half2(pr[0], pr[1]);
+            ph[j][1] = pack_half2(pr[2], pr[3]);
+        }
+        ps += __shfl_xor(ps, 16);
+        ps += __shfl_xor(ps, 32);
+        l = l * corr + ps;
+        m = mn;
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            o[i][0] *= corr;
+            o[i][1] *= corr;
+            o[i][2] *= corr;
+            o[i][3] *= corr;
+        }
+        // O^T[dims][q] += V^T[dims][pos] P^T[pos][q], chunks c of 32 positions.
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+            const uint4 b = make_uint4(ph[2 * c][0], ph[2 * c][1], ph[2 * c + 1][0], ph[2 * c + 1][1]);
+#pragma unroll
+            for (int i = 0; i < NI; i++) {
+                const uint16_t* vrow = &Vt[(16 * i + lq) * VLD + 32 * c + 4 * lg];
+                const uint2 lo = *reinterpret_cast<const uint2*>(vrow);
+                const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 16);
+                const uint4 a = make_uint4(lo.x, lo.y, hi.x, hi.y);
+                o[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                              __builtin_bit_cast(f16x8_t, b), o[i], 0, 0, 0);
+            }
+        }
+    }
+
+    // out[token][head][16 i + 4 lg + r] = O^T / l for this lane's query.
+    if (qvalid) {
+        const int h = g * gsize + qi % gsize;
+        const float inv = l > 0.f ? 1.f / l : 0.f;
+        const size_t base = (size_t)(t0 + qtok) * p.nh * HD + (size_t)h * HD;
+#pragma unroll
+        for (int i = 0; i < NI; i++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) store_act(p.out, p.out_dtype, base + 16 * i + 4 * lg + r, o[i][r] * inv);
+    }
+}
+
+template <int HD, int QT>
+int launch_prefill_mfma(hipStream_t s, const AttnParams& p, int pos0, int tokens) {
+    const int gsize = p.nh / p.nkv;
+    const int tq = kPQ / gsize;
+    dim3 grid(ceil_div(tokens, tq), p.nkv);
+    attn_prefill_mfma_kernel<HD, QT><<<grid, kBlock, 0, s>>>(p, pos0, tokens, gsize, tq);
+    return launch_status("attn_prefill_mfma");
+}
+
 template <int HD>
 int launch_prefill_hd(hipStream_t s, const AttnParams& p, int pos0, int tokens) {
-    if (p.cache_dtype == L0H_F16)
-        return p.q_dtype == L0H_F16 ? launch_prefill_tiled<HD, L0H_F16, L0H_F16>(s, p, pos0, tokens)
-                                    : launch_prefill_tiled<HD, L0H_F16, L0H_F32>(s, p, pos0, tokens);
+    if (p.cache_dtype == L0H_F16)  // MFMA; an fp32 cache keeps the fp32 kernel
+        return p.q_dtype == L0H_F16 ? launch_prefill_mfma<HD, L0H_F16>(s, p, pos0, tokens)
+                                    : launch_prefill_mfma<HD, L0H_F32>(s, p, pos0, tokens);
     return p.q_dtype == L0H_F16 ? launch_prefill_tiled<HD, L0H_F32, L0H_F16>(s, p, pos0, tokens)
                                 : launch_prefill_tiled<HD, L0H_F32, L0H_F32>(s, p, pos0, tokens);
 }
