@@ -24,7 +24,7 @@ GEMV_SHAPES = [
     (1152, 896),    # fused QKV 896 -> 1152
     (896, 4864),    # down-proj
     (6144, 4096),   # Llama-3.1-8B fused QKV
-    (4096, 14336),  # Llama-3.1-8B down-proj
+    (4096, 14336),  # Llama-3.1-8B down-proj (last batch of each row half filled)
     (100, 48),      # small
     (30, 17),       # odd shape: generic path
 ]
