@@ -121,7 +121,7 @@ template <int WT, int BM, int NW, bool NT, int P = ring_depth(BM, NW), int MF = 
           int SPS = 1>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void gemm_nk_kernel(
     int M, int N, int K, int k_per_split, const uint16_t* __restrict__ X, const void* __restrict__ Wv,
-    const uint16_t* __restrict__ scales, void* Y, int y_dtype, float* partial) {
+    const uint16_t* __restrict__ scales, void* Y, int y_dtype, int epi, float* partial) {
     constexpr bool I8 = WT == L0H_I8PC;
     constexpr int DT = I8 ? L0H_F16 : WT;  // MFMA operand type
     constexpr int S = BK * MF / 512;       // MFMAs per K step (k of one MFMA = 512 / MF)
@@ -268,36 +268,69 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     }
 
     // Accumulator register r of lane l holds D[row][l % MF] with row = 4 (l / 16) + r for
-    // MF = 16 and row = 8 (r / 4) + 4 (l / 32) + r % 4 for MF = 32.
+    // MF = 16 and row = 8 (r / 4) + 4 (l / 32) + r % 4 for MF = 32. One loop nest per epilogue
+    // (each fully unrolled, so the accumulators stay in registers).
     constexpr int R = MF == 16 ? 4 : 16;
+    auto each_out = [&](auto&& f) {
 #pragma unroll
-    for (int j = 0; j < NJ; j++) {
-        const int col = nw0 + j * MF + li;
-        const float scale = I8 ? __half2float(__ushort_as_half(scales[min(col, N - 1)])) : 1.f;
+        for (int j = 0; j < NJ; j++) {
+            const int col = nw0 + j * MF + li;
+            const float scale = I8 ? __half2float(__ushort_as_half(scales[min(col, N - 1)])) : 1.f;
 #pragma unroll
-        for (int i = 0; i < MI; i++) {
+            for (int i = 0; i < MI; i++) {
 #pragma unroll
-            for (int r = 0; r < R; r++) {
-                const int rr = MF == 16 ? (lane / 16) * 4 + r : (r / 4) * 8 + (lane / 32) * 4 + (r % 4);
-                const int row = m0 + i * MF + rr;
-                if (row < M && col < N) {
-                    const float v = I8 ? acc[i][j][r] * scale : acc[i][j][r];
-                    if (partial)
-                        partial[((size_t)bz * M + row) * N + col] = v;
-                    else
-                        store_act(Y, y_dtype, (size_t)row * N + col, v);
+                for (int r = 0; r < R; r++) {
+                    const int rr = MF == 16 ? (lane / 16) * 4 + r : (r / 4) * 8 + (lane / 32) * 4 + (r % 4);
+                    f(m0 + i * MF + rr, col, I8 ? acc[i][j][r] * scale : acc[i][j][r]);
                 }
             }
         }
+    };
+    if (partial) {
+        each_out([&](int row, int col, float v) {
+            if (row < M && col < N) partial[((size_t)bz * M + row) * N + col] = v;
+        });
+    } else if (epi == EPI_SWIGLU) {
+        // Column pairs (2c, 2c + 1) sit in lanes (2i, 2i + 1): a DPP swap, executed by every lane,
+        // brings the up value to the gate lane.
+        each_out([&](int row, int col, float v) {
+            const float up = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xf, 0xf, false));
+            if (row < M && col < N && (lane & 1) == 0)
+                store_act(Y, y_dtype, (size_t)row * (N / 2) + col / 2, v / (1.0f + __expf(-v)) * up);
+        });
+    } else if (epi == EPI_RESIDUAL) {
+        each_out([&](int row, int col, float v) {
+            if (row < M && col < N) static_cast<float*>(Y)[(size_t)row * N + col] += v;
+        });
+    } else {
+        each_out([&](int row, int col, float v) {
+            if (row < M && col < N) store_act(Y, y_dtype, (size_t)row * N + col, v);
+        });
     }
 }
 
-__global__ void splitk_reduce_kernel(const float* partial, int splits, size_t mn, void* Y, int y_dtype) {
+// Sum of the K splits' partials in split order, then the epilogue: store, add to fp32 Y, or (one
+// thread per column pair) silu(gate) * up into Y[row][c].
+__global__ void splitk_reduce_kernel(const float* partial, int splits, size_t mn, void* Y, int y_dtype, int epi) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (epi == EPI_SWIGLU) {
+        if (2 * i >= mn) return;
+        float g = 0.f, u = 0.f;
+        for (int z = 0; z < splits; z++) {
+            const float2 t = *reinterpret_cast<const float2*>(partial + (size_t)z * mn + 2 * i);
+            g += t.x;
+            u += t.y;
+        }
+        store_act(Y, y_dtype, i, g / (1.0f + __expf(-g)) * u);
+        return;
+    }
     if (i >= mn) return;
     float s = 0.f;
     for (int z = 0; z < splits; z++) s += partial[(size_t)z * mn + i];
-    store_act(Y, y_dtype, i, s);
+    if (epi == EPI_RESIDUAL)
+        static_cast<float*>(Y)[i] += s;
+    else
+        store_act(Y, y_dtype, i, s);
 }
 
 // Any shape (K not a multiple of 32): one thread per output, fp32 accumulation.
@@ -346,7 +379,7 @@ Plan plan_for(int m, int n, int k, int cus) {
 
 template <int WT, int BM, int NW>
 int launch_tiles(hipStream_t s, int m, int n, int k, const void* x, const void* w, const uint16_t* scales, void* y,
-                 int y_dtype, int splits, float* ws) {
+                 int y_dtype, int epi, int splits, float* ws) {
     constexpr int MF = NW % 32 == 0 ? 32 : 16;
     // Stages of two K steps where K allows, except the 128 x 64 wave tile (its two-step ring, with
     // fewer stages to fit the registers, measured slower).
@@ -365,28 +398,31 @@ int launch_tiles(hipStream_t s, int m, int n, int k, const void* x, const void* 
         constexpr int P2 = ring_depth2(NW);
         if (two && nt)
             gemm_nk_kernel<WT, BM, NW, true, P2, MF, 2><<<grid, 256, 0, s>>>(m, n, k, k_per_split, xp, w, scales, y,
-                                                                           y_dtype, part);
+                                                                           y_dtype, epi, part);
         else if (two)
             gemm_nk_kernel<WT, BM, NW, false, P2, MF, 2><<<grid, 256, 0, s>>>(m, n, k, k_per_split, xp, w, scales, y,
-                                                                            y_dtype, part);
+                                                                            y_dtype, epi, part);
     }
     if (!two && nt)
-        gemm_nk_kernel<WT, BM, NW, true><<<grid, 256, 0, s>>>(m, n, k, k_per_split, xp, w, scales, y, y_dtype, part);
+        gemm_nk_kernel<WT, BM, NW, true><<<grid, 256, 0, s>>>(m, n, k, k_per_split, xp, w, scales, y, y_dtype, epi,
+                                                             part);
     else if (!two)
-        gemm_nk_kernel<WT, BM, NW, false><<<grid, 256, 0, s>>>(m, n, k, k_per_split, xp, w, scales, y, y_dtype, part);
+        gemm_nk_kernel<WT, BM, NW, false><<<grid, 256, 0, s>>>(m, n, k, k_per_split, xp, w, scales, y, y_dtype, epi,
+                                                              part);
     int st = launch_status("gemm_nk");
     if (st || splits == 1) return st;
     const size_t mn = (size_t)m * n;
-    splitk_reduce_kernel<<<ceil_div(mn, 256), 256, 0, s>>>(ws, splits, mn, y, y_dtype);
+    const size_t threads = epi == EPI_SWIGLU ? mn / 2 : mn;
+    splitk_reduce_kernel<<<ceil_div(threads, 256), 256, 0, s>>>(ws, splits, mn, y, y_dtype, epi);
     return launch_status("gemm splitk reduce");
 }
 
 template <int WT>
 int launch_plan(hipStream_t s, const Plan& p, int m, int n, int k, const void* x, const void* w,
-                const uint16_t* scales, void* y, int y_dtype, float* ws) {
+                const uint16_t* scales, void* y, int y_dtype, int epi, float* ws) {
 #define L0H_GEMM_CASE(BM_, NW_)                                                                                  \
     if (p.bm == BM_ && p.nw == NW_)                                                                              \
-        return launch_tiles<WT, BM_, NW_>(s, m, n, k, x, w, scales, y, y_dtype, p.splits, ws);
+        return launch_tiles<WT, BM_, NW_>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws);
     L0H_GEMM_CASE(64, 16)
     L0H_GEMM_CASE(64, 32)
     L0H_GEMM_CASE(64, 64)
@@ -406,8 +442,12 @@ size_t gemm_workspace_bytes(int m, int n, int k, int compute_units) {
 }
 
 int launch_gemm_nk(hipStream_t s, int dtype, int m, int n, int k, const void* x, const void* w,
-                   void* y, int y_dtype, float* ws, size_t ws_bytes, int cus, const uint16_t* scales) {
+                   void* y, int y_dtype, float* ws, size_t ws_bytes, int cus, const uint16_t* scales, int epilogue) {
     if (m <= 0 || n <= 0 || k <= 0) return fail(L0H_ERR_INVALID_ARG, "GEMM sizes must be positive");
+    if (epilogue != EPI_STORE && epilogue != EPI_RESIDUAL && epilogue != EPI_SWIGLU)
+        return fail(L0H_ERR_INVALID_ARG, "GEMM epilogue is store, residual or SwiGLU");
+    if (epilogue == EPI_RESIDUAL && y_dtype != L0H_F32) return fail(L0H_ERR_INVALID_ARG, "residual GEMM output is fp32");
+    if (epilogue == EPI_SWIGLU && n % 2) return fail(L0H_ERR_INVALID_ARG, "SwiGLU GEMM needs an even column count");
     if (dtype != L0H_BF16 && dtype != L0H_F16 && dtype != L0H_I8PC)
         return fail(L0H_ERR_INVALID_ARG, "GEMM weights are F16, BF16 or I8PC");
     const bool aligned = k % BK == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)w & 15) == 0;
@@ -415,6 +455,7 @@ int launch_gemm_nk(hipStream_t s, int dtype, int m, int n, int k, const void* x,
         if (!scales) return fail(L0H_ERR_INVALID_ARG, "int8 GEMM needs the per-row scales");
         if (!aligned) return fail(L0H_ERR_UNSUPPORTED, "int8 GEMM needs K a multiple of 32 and 16-byte aligned operands");
     } else if (!aligned) {
+        if (epilogue != EPI_STORE) return fail(L0H_ERR_UNSUPPORTED, "fused GEMM epilogues need K a multiple of 32");
         const size_t mn = (size_t)m * n;
         gemm_nk_generic_kernel<<<ceil_div(mn, 256), 256, 0, s>>>(dtype, m, n, k, static_cast<const uint16_t*>(x),
                                                                  static_cast<const uint16_t*>(w), y, y_dtype);
@@ -423,9 +464,9 @@ int launch_gemm_nk(hipStream_t s, int dtype, int m, int n, int k, const void* x,
     Plan p = plan_for(m, n, k, cus);
     while (p.splits > 1 && (size_t)p.splits * m * n * sizeof(float) > ws_bytes) p.splits /= 2;
     switch (dtype) {
-    case L0H_BF16: return launch_plan<L0H_BF16>(s, p, m, n, k, x, w, nullptr, y, y_dtype, ws);
-    case L0H_F16: return launch_plan<L0H_F16>(s, p, m, n, k, x, w, nullptr, y, y_dtype, ws);
-    default: return launch_plan<L0H_I8PC>(s, p, m, n, k, x, w, scales, y, y_dtype, ws);
+    case L0H_BF16: return launch_plan<L0H_BF16>(s, p, m, n, k, x, w, nullptr, y, y_dtype, epilogue, ws);
+    case L0H_F16: return launch_plan<L0H_F16>(s, p, m, n, k, x, w, nullptr, y, y_dtype, epilogue, ws);
+    default: return launch_plan<L0H_I8PC>(s, p, m, n, k, x, w, scales, y, y_dtype, epilogue, ws);
     }
 }
 

@@ -119,11 +119,13 @@ bool attention_prefill_tiled(const AttnParams& p);
 
 // MFMA GEMM Y[M,N] = X[M,K] * W[N,K]^T: f16 or bf16 operands, or int8 weights with one fp16
 // scale per row (`scales`) and fp16 activations. Small M splits K into fp32 partials in `ws`
-// (gemm_workspace_bytes) when it fits.
+// (gemm_workspace_bytes) when it fits. Epilogue: EPI_STORE (Y in y_dtype), EPI_RESIDUAL (fp32
+// Y += result) or EPI_SWIGLU (columns interleaved gate/up: Y[m, c] = silu(r[m, 2c]) * r[m, 2c + 1]
+// in y_dtype, Y of width N / 2).
 size_t gemm_workspace_bytes(int m, int n, int k, int compute_units);
 int launch_gemm_nk(hipStream_t s, int dtype, int m, int n, int k, const void* x, const void* w,
                    void* y, int y_dtype, float* ws, size_t ws_bytes, int compute_units,
-                   const uint16_t* scales = nullptr);
+                   const uint16_t* scales = nullptr, int epilogue = EPI_STORE);
 
 // Random init: w[i] ~ N(0, std^2) from (seed, i); stored as dtype (F32/F16/BF16).
 int launch_init_normal(hipStream_t s, void* dst, int dtype, size_t count, uint64_t seed,

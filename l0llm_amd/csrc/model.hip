@@ -78,6 +78,23 @@ __global__ void swiglu_rows_kernel(const float* gu, float* act, size_t n) {
     if (i < n) act[i] = silu(gu[2 * i]) * gu[2 * i + 1];
 }
 
+// RMSNorm of row blockIdx.x of x (fp32, width n) straight into the MFMA GEMM's operand dtype
+// (F16 / BF16): out = x * rsqrt(mean(x^2) + eps) * w, the arithmetic of rmsnorm_kernel.
+__global__ __launch_bounds__(kBlock) void rmsnorm_rows16_kernel(const float* x, const float* w, uint16_t* out,
+                                                                float eps, int n, int dt) {
+    __shared__ float red[kWaves];
+    const float* xr = x + (size_t)blockIdx.x * n;
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < n; i += kBlock) ss += xr[i] * xr[i];
+    ss = block_sum(ss, red);
+    const float inv = rsqrtf(ss / (float)n + eps);
+    uint16_t* o = out + (size_t)blockIdx.x * n;
+    for (int i = threadIdx.x; i < n; i += kBlock) {
+        const float v = xr[i] * inv * w[i];
+        o[i] = dt == L0H_BF16 ? float_to_bf16_bits(v) : __half_as_ushort(__float2half_rn(v));
+    }
+}
+
 // fp32 activations -> the weight dtype (F16 / BF16) for the MFMA GEMM.
 __global__ void to_16bit_kernel(const float* x, uint16_t* y, size_t n, int dt) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -118,7 +135,7 @@ struct l0h_model {
     // chunked prefill (allocated on first use): rows of up to pf_cap tokens
     int pf_cap = 0;
     float *pf_hidden = nullptr, *pf_xn = nullptr, *pf_qkv = nullptr, *pf_q = nullptr, *pf_attn = nullptr,
-          *pf_gu = nullptr, *pf_act = nullptr, *pf_tmp = nullptr, *pf_ws = nullptr;
+          *pf_gu = nullptr, *pf_act = nullptr, *pf_ws = nullptr;
     uint16_t* pf_x16 = nullptr;
     int* pf_ids = nullptr;
     size_t pf_ws_bytes = 0;
@@ -543,7 +560,7 @@ int ensure_prefill(l0h_model* m) {
         return st;
     if (m->storage != L0H_F32) {
         const size_t kmax = std::max<size_t>({H, I, (size_t)m->qd});
-        if ((st = alloc_t(m, T * kmax, &m->pf_x16)) || (st = alloc_t(m, T * H, &m->pf_tmp))) return st;
+        if ((st = alloc_t(m, T * kmax, &m->pf_x16))) return st;
         const int cus = m->dev->compute_units;
         size_t ws = 0;
         for (int t = 64; t <= T; t++) {  // the largest split-K workspace any chunk size asks for
@@ -557,22 +574,10 @@ int ensure_prefill(l0h_model* m) {
     return L0H_OK;
 }
 
-// y = x W^T for T rows: STORE into y (+ bias in stored row order) or RESIDUAL into resid.
-int project_rows(l0h_model* m, hipStream_t s, const Proj& P, const float* x, int T, float* y, const float* bias,
-                 int epilogue, float* resid) {
-    if (prefill_uses_gemm(m, T, P.k)) {
-        const size_t nx = (size_t)T * P.k;
-        const int xdt = m->storage == L0H_BF16 ? L0H_BF16 : L0H_F16;
-        to_16bit_kernel<<<ceil_div(nx, 256), 256, 0, s>>>(x, m->pf_x16, nx, xdt);
-        int st = launch_status("to_16bit");
-        if (st) return st;
-        float* out = epilogue == EPI_RESIDUAL ? m->pf_tmp : y;
-        if ((st = launch_gemm_nk(s, m->storage, T, P.n, P.k, m->pf_x16, P.w, out, L0H_F32, m->pf_ws, m->pf_ws_bytes,
-                                 m->dev->compute_units, P.s)))
-            return st;
-        if (bias && (st = launch_bias_add(s, y, bias, P.n, T))) return st;
-        return epilogue == EPI_RESIDUAL ? launch_add(s, resid, m->pf_tmp, T * P.n) : L0H_OK;
-    }
+// y = x W^T for T rows on the multi-row GEMV (fp32 activations): STORE into y (+ bias) or
+// RESIDUAL into resid.
+int gemv_rows(l0h_model* m, hipStream_t s, const Proj& P, const float* x, int T, float* y, const float* bias,
+              int epilogue, float* resid) {
     GemvParams g;
     g.w_dtype = m->storage;
     g.w = P.w;
@@ -592,18 +597,43 @@ int project_rows(l0h_model* m, hipStream_t s, const Proj& P, const float* x, int
     return launch_gemv_nk(s, g);
 }
 
-// Tokens ids[0, T) at positions pos0 .. pos0 + T - 1 into every layer's cache.
+// y = x16 W^T for T rows on the MFMA GEMM (x16 in the operand dtype) with the GEMM's epilogue:
+// STORE (+ bias, fp32 y), RESIDUAL (fp32 y += result) or SWIGLU (y of width n / 2 in y_dtype).
+int gemm_rows(l0h_model* m, hipStream_t s, const Proj& P, const uint16_t* x16, int T, void* y, int y_dtype,
+              const float* bias, int epilogue) {
+    int st = launch_gemm_nk(s, m->storage, T, P.n, P.k, x16, P.w, y, y_dtype, m->pf_ws, m->pf_ws_bytes,
+                            m->dev->compute_units, P.s, epilogue);
+    if (st || !bias) return st;
+    return launch_bias_add(s, static_cast<float*>(y), bias, P.n, T);
+}
+
+// Tokens ids[0, T) at positions pos0 .. pos0 + T - 1 into every layer's cache. A projection runs
+// on the MFMA GEMM when prefill_uses_gemm holds for its input width; its producer (RMSNorm,
+// attention, the gate|up GEMM's SwiGLU epilogue) then writes that input in the 16-bit operand
+// dtype directly, and O / down add into the residual stream in the GEMM's epilogue.
 int prefill_chunk(l0h_model* m, const int* ids, int pos0, int T) {
     const auto& c = m->cfg;
     hipStream_t s = m->dev->stream;
     const int H = c.hidden_size, I = c.intermediate_size;
+    const bool gemm_h = prefill_uses_gemm(m, T, H);      // q|k|v and gate|up (input: normed rows)
+    const bool gemm_q = prefill_uses_gemm(m, T, m->qd);  // O (input: attention rows)
+    const bool gemm_i = prefill_uses_gemm(m, T, I);      // down (input: SwiGLU rows)
+    const int xdt = m->storage == L0H_BF16 ? L0H_BF16 : L0H_F16;
+    uint16_t* act16 = reinterpret_cast<uint16_t*>(m->pf_gu);  // T x I 16-bit rows in the gate|up buffer
     int st = l0h_write(m->dev, m->pf_ids, 0, ids, (size_t)T * sizeof(int));
     if (st) return st;
     if ((st = launch_embedding(s, m->pf_ids, m->embedding, m->pf_hidden, H, (size_t)T * H))) return st;
+    auto norm = [&](const float* w) {
+        if (!gemm_h) return launch_rmsnorm(s, m->pf_hidden, nullptr, w, m->pf_xn, c.rms_norm_eps, H, T, 0);
+        rmsnorm_rows16_kernel<<<T, kBlock, 0, s>>>(m->pf_hidden, w, m->pf_x16, c.rms_norm_eps, H, xdt);
+        return launch_status("rmsnorm_rows16");
+    };
     for (int li = 0; li < c.num_layers; li++) {
         Layer& L = m->layers[li];
-        if ((st = launch_rmsnorm(s, m->pf_hidden, nullptr, L.input_norm, m->pf_xn, c.rms_norm_eps, H, T, 0))) return st;
-        if ((st = project_rows(m, s, L.qkv, m->pf_xn, T, m->pf_qkv, L.qkv_bias, EPI_STORE, nullptr))) return st;
+        if ((st = norm(L.input_norm))) return st;
+        st = gemm_h ? gemm_rows(m, s, L.qkv, m->pf_x16, T, m->pf_qkv, L0H_F32, L.qkv_bias, EPI_STORE)
+                    : gemv_rows(m, s, L.qkv, m->pf_xn, T, m->pf_qkv, L.qkv_bias, EPI_STORE, nullptr);
+        if (st) return st;
         GemvParams g;
         g.k_cache = L.k_cache;
         g.v_cache = L.v_cache;
@@ -623,8 +653,8 @@ int prefill_chunk(l0h_model* m, const int* ids, int pos0, int T) {
         a.kc = L.k_cache;
         a.vc = L.v_cache;
         a.cache_dtype = m->cache_dtype;
-        a.out = m->pf_attn;
-        a.out_dtype = L0H_F32;
+        a.out = gemm_q ? static_cast<void*>(m->pf_x16) : static_cast<void*>(m->pf_attn);
+        a.out_dtype = gemm_q ? xdt : L0H_F32;
         a.head_dim = c.head_dim;
         a.nh = c.num_attention_heads;
         a.nkv = c.num_key_value_heads;
@@ -632,13 +662,27 @@ int prefill_chunk(l0h_model* m, const int* ids, int pos0, int T) {
         a.splits = 1;  // the query-tiled kernel; other head sizes: one split per token
         if ((st = launch_attention_prefill(s, a, pos0, T))) return st;
         if (li + 1 == c.num_layers) break;
-        if ((st = project_rows(m, s, L.o, m->pf_attn, T, nullptr, nullptr, EPI_RESIDUAL, m->pf_hidden))) return st;
-        if ((st = launch_rmsnorm(s, m->pf_hidden, nullptr, L.post_norm, m->pf_xn, c.rms_norm_eps, H, T, 0))) return st;
-        if ((st = project_rows(m, s, L.gu, m->pf_xn, T, m->pf_gu, nullptr, EPI_STORE, nullptr))) return st;
+        st = gemm_q ? gemm_rows(m, s, L.o, m->pf_x16, T, m->pf_hidden, L0H_F32, nullptr, EPI_RESIDUAL)
+                    : gemv_rows(m, s, L.o, m->pf_attn, T, nullptr, nullptr, EPI_RESIDUAL, m->pf_hidden);
+        if (st) return st;
+        if ((st = norm(L.post_norm))) return st;
         const size_t na = (size_t)T * I;
-        swiglu_rows_kernel<<<ceil_div(na, 256), 256, 0, s>>>(m->pf_gu, m->pf_act, na);
-        if ((st = launch_status("swiglu_rows"))) return st;
-        if ((st = project_rows(m, s, L.down, m->pf_act, T, nullptr, nullptr, EPI_RESIDUAL, m->pf_hidden))) return st;
+        if (gemm_h) {  // SwiGLU in the GEMM epilogue, in the dtype down reads
+            st = gemm_i ? gemm_rows(m, s, L.gu, m->pf_x16, T, act16, xdt, nullptr, EPI_SWIGLU)
+                        : gemm_rows(m, s, L.gu, m->pf_x16, T, m->pf_act, L0H_F32, nullptr, EPI_SWIGLU);
+            if (st) return st;
+        } else {
+            if ((st = gemv_rows(m, s, L.gu, m->pf_xn, T, m->pf_gu, nullptr, EPI_STORE, nullptr))) return st;
+            swiglu_rows_kernel<<<ceil_div(na, 256), 256, 0, s>>>(m->pf_gu, m->pf_act, na);
+            if ((st = launch_status("swiglu_rows"))) return st;
+            if (gemm_i) {  // the gate|up buffer is free again: the 16-bit rows go there
+                to_16bit_kernel<<<ceil_div(na, 256), 256, 0, s>>>(m->pf_act, act16, na, xdt);
+                if ((st = launch_status("to_16bit"))) return st;
+            }
+        }
+        st = gemm_i ? gemm_rows(m, s, L.down, act16, T, m->pf_hidden, L0H_F32, nullptr, EPI_RESIDUAL)
+                    : gemv_rows(m, s, L.down, m->pf_act, T, nullptr, nullptr, EPI_RESIDUAL, m->pf_hidden);
+        if (st) return st;
     }
     return L0H_OK;
 }

@@ -156,6 +156,24 @@ def test_chunked_prefill_matches_sequential_decode(device, precision, tol):
             assert np.max(np.abs(a - b)) <= 4 * tol * max(1.0, np.max(np.abs(a))), li
 
 
+@pytest.mark.parametrize("precision,tol", [(l0.PRECISION_INT8, 1e-2), (l0.PRECISION_FLOAT16, 1e-2)])
+def test_wide_prefill_split_k_epilogues_match_decode(device, precision, tol):
+    """Hidden 4096 over 139 prefill rows: the q|k|v, O and gate|up GEMMs split K in two, so the
+    split-K sums carry the store, residual and SwiGLU epilogues; down (K = 1024) does not split."""
+    cfg = l0.HfConfig(hidden_size=4096, intermediate_size=1024, num_layers=2, num_attention_heads=32,
+                      num_key_value_heads=8, head_dim=128, vocab_size=512, max_position_embeddings=4096,
+                      rms_norm_eps=1e-5, rope_theta=500000.0)
+    prompt = np.random.default_rng(12).integers(0, cfg.vocab_size, 140).tolist()
+    with l0.LlmModel(device, cfg, precision=precision, cache_dtype=l0.F16, max_seq_len=160) as m:
+        m.init_random(99, 0.02)
+        seq = None
+        for i, t in enumerate(prompt):
+            seq = m.compute_logits(t, i)
+        batched = m.prefill(prompt)
+        scale = np.max(np.abs(seq))
+        assert np.max(np.abs(seq - batched)) <= tol * scale, np.max(np.abs(seq - batched)) / scale
+
+
 @pytest.mark.parametrize("name,precision", [("qwen2", l0.PRECISION_INT8), ("llama", l0.PRECISION_BFLOAT16)])
 def test_model_loads_from_safetensors(device, tmp_path, name, precision):
     """LlmModel.Load's weight pass from a sharded safetensors checkpoint (bf16 tensors, as HF
