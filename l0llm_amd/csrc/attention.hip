@@ -21,6 +21,7 @@
 
 #include <cmath>
 #include <cstdlib>
+#include <type_traits>
 
 namespace l0h {
 namespace {
@@ -714,8 +715,10 @@ template <int HD, int QT>
 __global__ __launch_bounds__(kBlock) void attn_prefill_mfma_kernel(const AttnParams p, int pos0, int tokens,
                                                                    int gsize, int tq_tokens) {
     constexpr int KLD = HD + 8;        // K tile row stride (halves): 16 rows hit distinct banks
-    constexpr int VLD = kPK + 8;       // V^T tile row stride (halves)
+    constexpr int VLD = kPK + 4;       // V^T row stride (halves): 34 dwords, so the 16 rows of a P.V
+                                       // operand read, and the 8-byte runs of a store, spread over the banks
     constexpr int CPR = HD / 8;        // 16-byte chunks per cache row
+    constexpr int PPI = 64 / CPR;      // V positions per wave load (quads of 4 positions x CPR columns)
     constexpr int NC = kPK * CPR / kBlock;  // chunks per thread per tile (K, and again V)
     constexpr int KS = HD / 32;        // MFMA K steps over the head dim
     constexpr int NI = HD / 16;        // 16-dim output sub-tiles
@@ -749,16 +752,38 @@ __global__ __launch_bounds__(kBlock) void attn_prefill_mfma_kernel(const AttnPar
                             pack_half2(f[4] * qscale, f[5] * qscale), pack_half2(f[6] * qscale, f[7] * qscale));
     }
 
-    // Tile kt: chunk c of this thread is position (tid + c * kBlock) / CPR, dims 8 * ((...) % CPR).
+    // Tile kt. K: chunk c of this thread is position (tid + c * kBlock) / CPR, dims
+    // 8 ((tid + c * kBlock) % CPR) (a wave reads whole rows). V: lane l of wave w holds, for chunk
+    // c, position 16 w + c PPI + 4 ((l / 4) / CPR) + l % 4 and dims 8 ((l / 4) % CPR) .. +7: the 4
+    // lanes of a quad hold 4 consecutive positions of one 16-byte column, which a 4 x 4 transpose
+    // across the quad turns into 8-byte runs of the transposed tile (4 positions of one dim).
     uint4 kr[NC], vr[NC];
+    const int vq = lane >> 2, vj = lane & 3;
+    const int vcol = vq % CPR, vrow0 = 16 * wave + 4 * (vq / CPR);  // + c PPI: first position of the quad
     auto load_tile = [&](int kt) {
 #pragma unroll
         for (int c = 0; c < NC; c++) {
             const int q = tid + c * kBlock, r = q / CPR, col = q % CPR;
             const int pos = min(kt * kPK + r, kmax);
-            const size_t off = (size_t)pos * row_elems + (size_t)g * HD + col * 8;
-            kr[c] = ld_nt16(kc + off);
-            vr[c] = ld_nt16(vc + off);
+            kr[c] = ld_nt16(kc + (size_t)pos * row_elems + (size_t)g * HD + col * 8);
+            const int vpos = min(kt * kPK + vrow0 + c * PPI + vj, kmax);
+            vr[c] = ld_nt16(vc + (size_t)vpos * row_elems + (size_t)g * HD + vcol * 8);
+        }
+    };
+    // Transpose step across lanes l and l ^ M of a quad (DPP quad_perm), on the 32-bit dim pairs
+    // k and k ^ M: a lane whose bit M differs from k's takes the partner's pair k ^ M.
+    auto quad_step = [&](uint32_t (&w)[4], auto mc) {
+        constexpr int M = decltype(mc)::value;
+        constexpr int CTRL = M == 1 ? 0xB1 : 0x4E;  // quad_perm [1,0,3,2] / [2,3,0,1]
+        const bool upper = (vj & M) != 0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            if (k & M) continue;
+            const uint32_t pa = (uint32_t)__builtin_amdgcn_mov_dpp((int)w[k], CTRL, 0xf, 0xf, false);
+            const uint32_t pb = (uint32_t)__builtin_amdgcn_mov_dpp((int)w[k ^ M], CTRL, 0xf, 0xf, false);
+            const uint32_t a = w[k], b = w[k ^ M];
+            w[k] = upper ? pb : a;
+            w[k ^ M] = upper ? b : pa;
         }
     };
     auto store_tile = [&]() {
@@ -766,12 +791,15 @@ __global__ __launch_bounds__(kBlock) void attn_prefill_mfma_kernel(const AttnPar
         for (int c = 0; c < NC; c++) {
             const int q = tid + c * kBlock, r = q / CPR, col = q % CPR;
             *reinterpret_cast<u32x4_t*>(&Ks[r * KLD + col * 8]) = u32x4_t{kr[c].x, kr[c].y, kr[c].z, kr[c].w};
-            const uint32_t w[4] = {vr[c].x, vr[c].y, vr[c].z, vr[c].w};
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                Vt[(col * 8 + 2 * e) * VLD + r] = (uint16_t)(w[e] & 0xFFFFu);
-                Vt[(col * 8 + 2 * e + 1) * VLD + r] = (uint16_t)(w[e] >> 16);
-            }
+            // w[p] after the transpose: dims 8 vcol + 2 vj, + 1 of position vrow0 + c PPI + p.
+            uint32_t w[4] = {vr[c].x, vr[c].y, vr[c].z, vr[c].w};
+            quad_step(w, std::integral_constant<int, 2>{});
+            quad_step(w, std::integral_constant<int, 1>{});
+            const int d = 8 * vcol + 2 * vj, p0 = vrow0 + c * PPI;
+            *reinterpret_cast<u32x2_t*>(&Vt[d * VLD + p0]) =
+                u32x2_t{(w[0] & 0xFFFFu) | (w[1] << 16), (w[2] & 0xFFFFu) | (w[3] << 16)};
+            *reinterpret_cast<u32x2_t*>(&Vt[(d + 1) * VLD + p0]) =
+                u32x2_t{(w[0] >> 16) | (w[1] & 0xFFFF0000u), (w[2] >> 16) | (w[3] & 0xFFFF0000u)};
         }
     };
 

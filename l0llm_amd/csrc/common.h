@@ -109,6 +109,7 @@ __device__ inline void store_act(void* p, int dt, size_t i, float v) {
 }
 
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
 
 // 16-byte streaming load that bypasses cache retention (weights and KV rows are read once).
 __device__ __forceinline__ uint4 ld_nt16(const void* p) {

@@ -114,8 +114,6 @@ __device__ __forceinline__ u32x4_t perm_f16x8(const uint4& a) {  // a0 a2 a1 a3 
                    (a.z >> 16) | (a.w & 0xFFFF0000u)};
 }
 
-typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
-
 // WT: weight storage (F16, BF16, or I8PC with fp16 activations and one fp16 scale per weight row).
 template <int WT, int BM, int NW, bool NT, int P = ring_depth(BM, NW), int MF = (NW % 32 == 0 ? 32 : 16),
           int SPS = 1>
@@ -359,11 +357,15 @@ struct Plan {
 // while each split keeps at least 64 K steps (no split needs none). When no tile gets there, the smallest tile is split
 // further, down to two rings of K steps per split.
 Plan plan_for(int m, int n, int k, int cus) {
+    // From 512 rows the 128 x 32 tile comes first: its registers leave room for two waves per SIMD
+    // (the 128 x 64 tile holds one), and it measured as fast or faster at M = 512 and 2047
+    // (int8 q|k|v 4096 -> 6144 at M = 2047: 138 us against 167 us).
     static const int tiles[][2] = {{128, 64}, {128, 32}, {128, 16}, {64, 64}, {64, 32}, {64, 16}};
+    static const int tiles_tall[][2] = {{128, 32}, {128, 64}, {128, 16}, {64, 64}, {64, 32}, {64, 16}};
     const int steps = k / BK;
     const size_t want = (size_t)cus * 3 / 4;
     auto blocks = [&](int bm, int nw) { return (size_t)ceil_div(n, 4 * nw) * ceil_div(m, bm); };
-    for (const auto& t : tiles) {
+    for (const auto& t : (m >= 512 ? tiles_tall : tiles)) {
         if (m <= 64 && t[0] == 128) continue;
         if (m > 64 && t[0] == 64 && t[1] == 64) continue;
         const size_t b = blocks(t[0], t[1]);

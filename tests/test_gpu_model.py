@@ -128,7 +128,8 @@ CHUNKED = [(l0.PRECISION_INT8, 1e-2), (l0.PRECISION_FLOAT32, 2e-3), (l0.PRECISIO
 
 
 @pytest.mark.parametrize("precision,tol", CHUNKED)
-def test_chunked_prefill_matches_sequential_decode(device, precision, tol):
+def test_chunked_prefill_matches_sequential_decode(device, precision, tol, monkeypatch):
+    monkeypatch.setenv("L0H_PREFILL_CHUNK", "256")  # read at model creation: 299 rows -> chunks of 256 and 43
     cfg = l0.HfConfig(hidden_size=256, intermediate_size=512, num_layers=3, num_attention_heads=4,
                       num_key_value_heads=2, head_dim=64, vocab_size=512, max_position_embeddings=4096,
                       rms_norm_eps=1e-5, rope_theta=500000.0, attention_bias=True)
