@@ -254,7 +254,19 @@ def cpu_baseline(model, cfg, tokens: int, position: int) -> dict:
     return dict(value=round(tokens / dt, 4), unit="tokens/s", cores=orc.num_threads(), kind="port",
                 sample=f"{tokens} decode tokens of the same int8 model (all 32 layers + lm_head + argmax) at "
                        f"positions {position + 1}..{position + tokens}, fp64-accumulating C oracle, "
-                       f"{orc.num_threads()} OpenMP threads")
+                       f"{orc.num_threads()} OpenMP threads",
+                cpu_model=host_cpu_model(), host_cpus=len(os.sched_getaffinity(0)))
+
+
+def host_cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def main() -> int:
