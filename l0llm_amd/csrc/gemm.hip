@@ -8,9 +8,9 @@
 // 16 results per lane). So a lane's B operand for one MFMA is 16 contiguous bytes of one weight
 // row (8 bytes for int8, converted to fp16 in registers).
 //
-// A block of 4 waves computes BM rows x 4 NW columns; wave w owns NW columns and all BM rows.
+// A block of 4 (or 8) waves computes BM rows x 4 (8) NW columns; wave w owns NW columns and all BM rows.
 // The weights, which no two waves share, go from HBM straight into MFMA operand registers; only
-// the activation tile (BM x 32 per K step, read by all 4 waves) passes through LDS. That halves
+// the activation tile (BM x 32 per K step, read by all the waves) passes through LDS. That halves
 // the LDS traffic per MFMA against staging both operands (the LDS port, 128 bytes per clock per
 // CU, is what bounds a 64 x 64 wave tile with both operands in LDS). K steps pass through a ring
 // of P register stages of one or two steps each: the loads of stage t + P - 1 are issued while
@@ -115,9 +115,10 @@ __device__ __forceinline__ u32x4_t perm_f16x8(const uint4& a) {  // a0 a2 a1 a3 
 }
 
 // WT: weight storage (F16, BF16, or I8PC with fp16 activations and one fp16 scale per weight row).
+// NWV: waves per block (each owns NW columns), so one activation tile in LDS feeds NWV * NW columns.
 template <int WT, int BM, int NW, bool NT, int P = ring_depth(BM, NW), int MF = (NW % 32 == 0 ? 32 : 16),
-          int SPS = 1>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void gemm_nk_kernel(
+          int SPS = 1, int NWV = 4>
+__global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(1, 2))) void gemm_nk_kernel(
     int M, int N, int K, int k_per_split, const uint16_t* __restrict__ X, const void* __restrict__ Wv,
     const uint16_t* __restrict__ scales, void* Y, int y_dtype, int epi, float* partial) {
     constexpr bool I8 = WT == L0H_I8PC;
@@ -126,7 +127,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     constexpr int MI = BM / MF;            // MF-row A fragments
     constexpr int NJ = NW / MF;            // MF-column B fragments per wave
     constexpr int NB = I8 ? NJ : NJ * S;   // B registers per stage (int8: one covers the step)
-    constexpr int AC = BM * BK / 8 / 256;  // 16-byte A chunks per thread per step
+    constexpr int AC = BM * BK / 8 / (64 * NWV);  // 16-byte A chunks per thread per step
     constexpr int WB = I8 ? 1 : 2;         // bytes per weight
     using breg = typename std::conditional<I8 && MF == 16, uint2, uint4>::type;
     static_assert(AC >= 1 && MI >= 1 && NJ >= 1, "tile too small");
@@ -143,7 +144,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     const int G = row_group(gx);
     const int gr = lin % G, rest = lin / G;
     const int bz = rest % gy, bn = (rest / gy) % gz, bm = (rest / (gy * gz)) * G + gr;
-    const int m0 = bm * BM, nw0 = bn * 4 * NW + wave * NW;
+    const int m0 = bm * BM, nw0 = bn * NWV * NW + wave * NW;
     const int kbeg = bz * k_per_split;
     const int nsteps = max(0, min(K, kbeg + k_per_split) - kbeg) / (BK * SPS);  // stages of SPS K steps
     const int last = max(nsteps - 1, 0);
@@ -168,7 +169,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     const uint16_t* aptr[AC];
 #pragma unroll
     for (int c = 0; c < AC; c++) {
-        const int idx = tid + c * 256;
+        const int idx = tid + c * (64 * NWV);
         aptr[c] = X + (size_t)min(m0 + (idx >> 2), M - 1) * K + kbeg + (idx & 3) * 8;
     }
 
@@ -203,7 +204,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
         for (int u = 0; u < SPS; u++)
 #pragma unroll
         for (int c = 0; c < AC; c++) {
-            const int idx = tid + c * 256;
+            const int idx = tid + c * (64 * NWV);
             const uint4& v = a[u * AC + c];
             // As a vector value: a struct copy would keep the ring in memory instead of registers.
             *reinterpret_cast<u32x4_t*>(&sa[buf][u][(idx >> 2) * kLds + (idx & 3) * 8]) =
@@ -348,50 +349,60 @@ __global__ void gemm_nk_generic_kernel(int dt, int M, int N, int K, const uint16
 }
 
 struct Plan {
-    int bm = 128, nw = 64, splits = 1;
+    int bm = 128, nw = 64, splits = 1, waves = 4;
 };
 
-// Tile and split-K choice (from a sweep over the Llama-3.2-1B prefill shapes and square ones on
+// Tile and split-K choice (from sweeps over the Llama-3.2-1B and Llama-3.1-8B prefill shapes on
 // MI355X). Tiles are tried from the largest (fewest L1 bytes per flop) down; a tile is taken with
 // the smallest power-of-two K split that gives about one block per CU (3/4 of the CUs or more)
-// while each split keeps at least 64 K steps (no split needs none). When no tile gets there, the smallest tile is split
-// further, down to two rings of K steps per split.
+// while each split keeps at least 64 K steps (no split needs none). When no tile gets there, the
+// smallest tile is split further, down to two rings of K steps per split.
 Plan plan_for(int m, int n, int k, int cus) {
-    // From 512 rows the 128 x 32 tile comes first: its registers leave room for two waves per SIMD
-    // (the 128 x 64 tile holds one), and it measured as fast or faster at M = 512 and 2047
-    // (int8 q|k|v 4096 -> 6144 at M = 2047: 138 us against 167 us).
-    static const int tiles[][2] = {{128, 64}, {128, 32}, {128, 16}, {64, 64}, {64, 32}, {64, 16}};
-    static const int tiles_tall[][2] = {{128, 32}, {128, 64}, {128, 16}, {64, 64}, {64, 32}, {64, 16}};
+    // From 512 rows the 128-row tiles with 32 columns per wave come first: their registers leave
+    // room for two waves per SIMD (the 64-column wave tile holds one). Eight such waves per block
+    // share one activation tile across 256 columns, halving the activation bytes each block pulls
+    // from L2 (what bounds these shapes): int8 at M = 2047, gate|up 4096 -> 28672 takes 528 us
+    // against 616 us with four waves and 633 us with the 128 x 64 tile.
+    struct Tile {
+        int bm, nw, waves;
+    };
+    static const Tile tiles[] = {{128, 64, 4}, {128, 32, 4}, {128, 16, 4}, {64, 64, 4}, {64, 32, 4}, {64, 16, 4}};
+    static const Tile tiles_tall[] = {{128, 32, 8}, {128, 32, 4}, {128, 64, 4}, {128, 16, 4},
+                                      {64, 64, 4},  {64, 32, 4},  {64, 16, 4}};
     const int steps = k / BK;
     const size_t want = (size_t)cus * 3 / 4;
-    auto blocks = [&](int bm, int nw) { return (size_t)ceil_div(n, 4 * nw) * ceil_div(m, bm); };
-    for (const auto& t : (m >= 512 ? tiles_tall : tiles)) {
-        if (m <= 64 && t[0] == 128) continue;
-        if (m > 64 && t[0] == 64 && t[1] == 64) continue;
-        const size_t b = blocks(t[0], t[1]);
+    auto blocks = [&](const Tile& t) { return (size_t)ceil_div(n, t.waves * t.nw) * ceil_div(m, t.bm); };
+    const Tile* list = m >= 512 ? tiles_tall : tiles;
+    const int count = m >= 512 ? (int)(sizeof(tiles_tall) / sizeof(Tile)) : (int)(sizeof(tiles) / sizeof(Tile));
+    for (int ti = 0; ti < count; ti++) {
+        const Tile& t = list[ti];
+        if (m <= 64 && t.bm == 128) continue;
+        if (m > 64 && t.bm == 64 && t.nw == 64) continue;
+        const size_t b = blocks(t);
         for (int s = 1; s <= kMaxSplits && (s == 1 || steps / s >= 64); s *= 2)
-            if (b * s >= want) return Plan{t[0], t[1], s};
+            if (b * s >= want) return Plan{t.bm, t.nw, s, t.waves};
     }
-    Plan p{64, 16, 1};
-    const size_t b = blocks(p.bm, p.nw);
+    Plan p{64, 16, 1, 4};
+    const size_t b = blocks(Tile{p.bm, p.nw, p.waves});
     while (p.splits < kMaxSplits && b * p.splits < want && steps / (p.splits * 2) >= 2 * ring_depth(p.bm, p.nw))
         p.splits *= 2;
     return p;
 }
 
-template <int WT, int BM, int NW>
+template <int WT, int BM, int NW, int NWV = 4>
 int launch_tiles(hipStream_t s, int m, int n, int k, const void* x, const void* w, const uint16_t* scales, void* y,
                  int y_dtype, int epi, int splits, float* ws) {
     constexpr int MF = NW % 32 == 0 ? 32 : 16;
     // Stages of two K steps where K allows, except the 128 x 64 wave tile (its two-step ring, with
-    // fewer stages to fit the registers, measured slower).
+    // fewer stages to fit the registers, measured slower) and eight-wave blocks below K = 8192
+    // (one-step stages measured faster there: int8 gate|up 528 us against 559 us).
     constexpr bool kTwo = NW != 64;
-    const bool two = kTwo && k % (2 * BK) == 0;
+    const bool two = kTwo && k % (2 * BK) == 0 && (NWV == 4 || k >= 8192);
     const int unit = two ? 2 * BK : BK;
     const int k_per_split = (k / unit + splits - 1) / splits * unit;
     // The kernel decodes (row block, split, column block) from the linear block id; the grid only
     // has to hold that many blocks, in the order x = row blocks, y = splits, z = column blocks.
-    dim3 grid(ceil_div(m, BM), splits, ceil_div(n, 4 * NW));
+    dim3 grid(ceil_div(m, BM), splits, ceil_div(n, NWV * NW));
     const auto* xp = static_cast<const uint16_t*>(x);
     float* part = splits > 1 ? ws : nullptr;
     // One row block: each weight byte is read by one block, so it is streamed past the caches.
@@ -399,18 +410,19 @@ int launch_tiles(hipStream_t s, int m, int n, int k, const void* x, const void* 
     if constexpr (kTwo) {
         constexpr int P2 = ring_depth2(NW);
         if (two && nt)
-            gemm_nk_kernel<WT, BM, NW, true, P2, MF, 2><<<grid, 256, 0, s>>>(m, n, k, k_per_split, xp, w, scales, y,
-                                                                           y_dtype, epi, part);
+            gemm_nk_kernel<WT, BM, NW, true, P2, MF, 2, NWV><<<grid, 64 * NWV, 0, s>>>(m, n, k, k_per_split, xp, w,
+                                                                                      scales, y, y_dtype, epi, part);
         else if (two)
-            gemm_nk_kernel<WT, BM, NW, false, P2, MF, 2><<<grid, 256, 0, s>>>(m, n, k, k_per_split, xp, w, scales, y,
-                                                                            y_dtype, epi, part);
+            gemm_nk_kernel<WT, BM, NW, false, P2, MF, 2, NWV><<<grid, 64 * NWV, 0, s>>>(m, n, k, k_per_split, xp, w,
+                                                                                       scales, y, y_dtype, epi, part);
     }
+    constexpr int P1 = NWV == 8 ? 4 : ring_depth(BM, NW);
     if (!two && nt)
-        gemm_nk_kernel<WT, BM, NW, true><<<grid, 256, 0, s>>>(m, n, k, k_per_split, xp, w, scales, y, y_dtype, epi,
-                                                             part);
+        gemm_nk_kernel<WT, BM, NW, true, P1, MF, 1, NWV><<<grid, 64 * NWV, 0, s>>>(m, n, k, k_per_split, xp, w, scales,
+                                                                                   y, y_dtype, epi, part);
     else if (!two)
-        gemm_nk_kernel<WT, BM, NW, false><<<grid, 256, 0, s>>>(m, n, k, k_per_split, xp, w, scales, y, y_dtype, epi,
-                                                              part);
+        gemm_nk_kernel<WT, BM, NW, false, P1, MF, 1, NWV><<<grid, 64 * NWV, 0, s>>>(m, n, k, k_per_split, xp, w, scales,
+                                                                                    y, y_dtype, epi, part);
     int st = launch_status("gemm_nk");
     if (st || splits == 1) return st;
     const size_t mn = (size_t)m * n;
@@ -422,8 +434,10 @@ int launch_tiles(hipStream_t s, int m, int n, int k, const void* x, const void* 
 template <int WT>
 int launch_plan(hipStream_t s, const Plan& p, int m, int n, int k, const void* x, const void* w,
                 const uint16_t* scales, void* y, int y_dtype, int epi, float* ws) {
+    if (p.bm == 128 && p.nw == 32 && p.waves == 8)
+        return launch_tiles<WT, 128, 32, 8>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws);
 #define L0H_GEMM_CASE(BM_, NW_)                                                                                  \
-    if (p.bm == BM_ && p.nw == NW_)                                                                              \
+    if (p.bm == BM_ && p.nw == NW_ && p.waves == 4)                                                              \
         return launch_tiles<WT, BM_, NW_>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws);
     L0H_GEMM_CASE(64, 16)
     L0H_GEMM_CASE(64, 32)
