@@ -499,7 +499,9 @@ __global__ __launch_bounds__(kBlock) void attn_prefill_tiled_kernel(const AttnPa
 
     const int tid = threadIdx.x, ti = tid >> 4, tj = tid & 15;
     const int g = blockIdx.y;
-    const int t0 = blockIdx.x * tq_tokens;
+    // Query tiles in reverse: the last tokens see the most positions, so the longest blocks are
+    // dispatched first and the short ones fill in behind them.
+    const int t0 = (gridDim.x - 1 - blockIdx.x) * tq_tokens;
     const int t_last = min(t0 + tq_tokens, tokens) - 1;
     const int kmax = pos0 + t_last;  // last key position any query of the tile sees
     const int row_elems = p.nkv * HD;
@@ -729,7 +731,9 @@ __global__ __launch_bounds__(kBlock) void attn_prefill_mfma_kernel(const AttnPar
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int lq = lane & 15, lg = lane >> 4;
     const int g = blockIdx.y;
-    const int t0 = blockIdx.x * tq_tokens;
+    // Query tiles in reverse: the last tokens see the most positions, so the longest blocks are
+    // dispatched first and the short ones fill in behind them.
+    const int t0 = (gridDim.x - 1 - blockIdx.x) * tq_tokens;
     const int t_last = min(t0 + tq_tokens, tokens) - 1;
     const int kmax = pos0 + t_last;
     const int row_elems = p.nkv * HD;
