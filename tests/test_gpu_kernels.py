@@ -312,11 +312,12 @@ def test_attention_decode_batched_fp16(device, suite, batch, seq):
 
 # (head_dim, q heads, kv heads, pos0, tokens, max_seq, cache): query-tiled kernels for head_dim 64
 # and 128 (fp32 VALU for fp32 caches, MFMA for fp16 caches; group sizes 7, 4, 8 and 1, ragged last
-# tiles, chunks starting mid-cache), split decode kernel per token for the other head sizes.
+# tiles, chunks starting mid-cache, chunks over 1024 tokens), split decode kernel per token for the
+# other head sizes.
 PREFILL = [(64, 14, 2, 9, 8, 32, l0.F32), (128, 32, 8, 0, 200, 256, l0.F16), (128, 32, 8, 100, 77, 300, l0.F16),
            (64, 16, 2, 5, 130, 200, l0.F32), (128, 8, 8, 63, 65, 200, l0.F16), (128, 16, 2, 1, 1, 4, l0.F32),
            (32, 8, 2, 3, 10, 20, l0.F32), (16, 4, 2, 0, 40, 48, l0.F16), (64, 14, 2, 9, 70, 100, l0.F16),
-           (64, 16, 2, 0, 130, 200, l0.F16)]
+           (64, 16, 2, 0, 130, 200, l0.F16), (128, 8, 8, 0, 1030, 1100, l0.F16), (64, 14, 2, 5, 1030, 1100, l0.F16)]
 
 
 @pytest.mark.parametrize("hd,nh,nkv,pos0,T,max_seq,cache", PREFILL)
