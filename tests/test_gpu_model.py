@@ -288,7 +288,15 @@ LLAMA8B = l0.HfConfig(hidden_size=4096, intermediate_size=14336, num_layers=32, 
                       rms_norm_eps=1e-5, rope_theta=500000.0)
 
 
-@pytest.mark.parametrize("hf,steps", [(QWEN05, 6), (LLAMA8B, 4)], ids=["qwen2.5-0.5b-4layers", "llama3.1-8b"])
+# Odd shapes: hidden 320 (20 int8 chunks per row), 5 q heads on 1 kv head, an odd vocabulary (a
+# partial last row group), biases.
+ODD = l0.HfConfig(hidden_size=320, intermediate_size=960, num_layers=2, num_attention_heads=5,
+                  num_key_value_heads=1, head_dim=64, vocab_size=777, max_position_embeddings=4096,
+                  rms_norm_eps=1e-6, rope_theta=10000.0, attention_bias=True)
+
+
+@pytest.mark.parametrize("hf,steps", [(QWEN05, 6), (LLAMA8B, 4), (ODD, 8)],
+                         ids=["qwen2.5-0.5b-4layers", "llama3.1-8b", "odd-320-5q1kv-777"])
 def test_random_int8_model_matches_oracle(device, hf, steps):
     """Int8 per-channel random-init model at the real shapes: the device's weights are read
     back and the oracle runs the same steps; logits agree and greedy ids agree unless the
@@ -307,3 +315,17 @@ def test_random_int8_model_matches_oracle(device, hf, steps):
             if gnext != onext:
                 assert orc.top2_margin(olg) < 1e-3 * np.max(np.abs(olg)), (t, gnext, onext)
             tok = onext
+
+
+def test_odd_shapes_chunked_prefill_matches_decode(device, monkeypatch):
+    """The odd-shaped model in 64-token chunks (the MFMA GEMM at its smallest M, with the K = 320
+    and 960 rows and the 448-row q|k|v, then a 21-token chunk on the multi-row GEMV)."""
+    monkeypatch.setenv("L0H_PREFILL_CHUNK", "64")
+    prompt = np.random.default_rng(21).integers(0, ODD.vocab_size, 150).tolist()
+    with _random_model(device, ODD, 160, seed=5) as m:
+        seq = None
+        for i, t in enumerate(prompt):
+            seq = m.compute_logits(t, i)
+        batched = m.prefill(prompt)
+        scale = np.max(np.abs(seq))
+        assert np.max(np.abs(seq - batched)) <= 1e-2 * scale, np.max(np.abs(seq - batched)) / scale
