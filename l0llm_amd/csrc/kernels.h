@@ -50,9 +50,10 @@ struct GemvParams {
 };
 
 // Persistent-grid size for weight-streaming kernels on a device with `compute_units` CUs:
-// per_cu blocks of 4 waves per CU. Two is the measured best for the 8B decode shapes except the
-// down projection (three): a CU returns data in order, and fewer blocks per CU means fewer
-// blocks whose activation row waits behind a neighbour's weight stream.
+// per_cu blocks of 4 waves per CU. Two is the measured best for the 8B decode shapes: a CU
+// returns data in order, and fewer blocks per CU means fewer blocks whose activation row waits
+// behind a neighbour's weight stream. A launch is further capped at the blocks per CU that its
+// LDS tile allows (two for the 56-64 KiB tiles of a 14336-wide down projection).
 int gemv_max_blocks(int compute_units, int per_cu = 2);
 
 int launch_gemv_nk(hipStream_t s, const GemvParams& p);

@@ -434,7 +434,6 @@ int launch_op(l0h_model* m, hipStream_t s, int kind, int li) {
     }
     case L0H_KERNEL_DOWN: {  // LlmDecoderLayer.cs:190-194
         Layer& L = m->layers[li];
-        g.max_blocks = gemv_max_blocks(m->dev->compute_units, 3);
         g.w = L.down.w;
         g.scales = L.down.s;
         g.n = H;
