@@ -32,6 +32,12 @@ constexpr int kGroupMax = 8;  // q heads per kv head
 constexpr int kUnroll = 4;    // positions per slot per step
 constexpr int kMaxSplits = 256;
 
+// 2^x as one v_exp_f32. exp2f wraps the instruction in a range reduction (compare, select, add,
+// ldexp) so that results below 2^-126 come out as denormals instead of zero; every softmax weight
+// here is summed against a running total of at least 1, where such a value changes nothing, and
+// for x >= -126 both give the same bits.
+__device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
+
 template <int CTRL, int ROW_MASK>
 __device__ __forceinline__ float dpp_src(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, false));
@@ -219,10 +225,10 @@ __global__ __launch_bounds__(kBlock) void attn_split_kernel(const AttnParams p, 
 #pragma unroll
             for (int u = 0; u < U; u++) mx = fmaxf(mx, sc[u][h]);
             const float ref = mx == -INFINITY ? 0.f : mx;  // no valid position yet: keep zeros
-            const float c = exp2f(m[h] - ref);
+            const float c = exp2_hw(m[h] - ref);
             float pr[U];
 #pragma unroll
-            for (int u = 0; u < U; u++) pr[u] = exp2f(sc[u][h] - ref);
+            for (int u = 0; u < U; u++) pr[u] = exp2_hw(sc[u][h] - ref);
             float lsum = l[h] * c;
 #pragma unroll
             for (int u = 0; u < U; u++) lsum += pr[u];
@@ -266,7 +272,7 @@ __global__ __launch_bounds__(kBlock) void attn_split_kernel(const AttnParams p, 
 #pragma unroll
     for (int h = 0; h < G; h++) {
         const float M = slot_reduce<LPP, true>(m[h]);
-        const float c = M == -INFINITY ? 0.f : exp2f(m[h] - M);
+        const float c = M == -INFINITY ? 0.f : exp2_hw(m[h] - M);
         const float lw = slot_reduce<LPP, false>(l[h] * c);
 #pragma unroll
         for (int d = 0; d < 8; d++) acc[h][d] = slot_reduce<LPP, false>(acc[h][d] * c);
@@ -293,7 +299,7 @@ __global__ __launch_bounds__(kBlock) void attn_split_kernel(const AttnParams p, 
         float num = 0.f, den = 0.f;
 #pragma unroll
         for (int w = 0; w < kWaves; w++) {
-            const float c = M == -INFINITY ? 0.f : exp2f(s_m[w][h] - M);
+            const float c = M == -INFINITY ? 0.f : exp2_hw(s_m[w][h] - M);
             num = fmaf(c, s_acc[w][h][d], num);
             den = fmaf(c, s_l[w][h], den);
         }
@@ -348,7 +354,7 @@ __global__ __launch_bounds__(kBlock) void attn_merge_kernel(const AttnParams p) 
         for (int u = 0; u < 8; u++)
             if (s0 + u * J < S) mx = fmaxf(mx, ms[u]);
         if (mx != -INFINITY) {
-            const float cs = exp2f(M - mx);  // 0 while M is still -inf
+            const float cs = exp2_hw(M - mx);  // 0 while M is still -inf
             num.x *= cs;
             num.y *= cs;
             num.z *= cs;
@@ -357,7 +363,7 @@ __global__ __launch_bounds__(kBlock) void attn_merge_kernel(const AttnParams p) 
 #pragma unroll
             for (int u = 0; u < 8; u++) {
                 if (s0 + u * J < S && ms[u] != -INFINITY) {
-                    const float w = exp2f(ms[u] - mx);
+                    const float w = exp2_hw(ms[u] - mx);
                     num.x = fmaf(w, v[u].x, num.x);
                     num.y = fmaf(w, v[u].y, num.y);
                     num.z = fmaf(w, v[u].z, num.z);
@@ -381,7 +387,7 @@ __global__ __launch_bounds__(kBlock) void attn_merge_kernel(const AttnParams p) 
         if (Mt != -INFINITY) {
 #pragma unroll
             for (int i = 0; i < J; i++) {
-                const float w = s_mx[i][cl] == -INFINITY ? 0.f : exp2f(s_mx[i][cl] - Mt);
+                const float w = s_mx[i][cl] == -INFINITY ? 0.f : exp2_hw(s_mx[i][cl] - Mt);
                 const float4 u = s_num[i][cl];
                 t.x = fmaf(w, u.x, t.x);
                 t.y = fmaf(w, u.y, t.y);
@@ -620,11 +626,11 @@ __global__ __launch_bounds__(kBlock) void attn_prefill_tiled_kernel(const AttnPa
                 mt = fmaxf(mt, sc[a][b]);
             }
             const float mn = fmaxf(m[a], row16_max(mt));
-            const float corr = mn == -INFINITY ? 1.f : exp2f(m[a] - mn);  // 0 while m is -inf
+            const float corr = mn == -INFINITY ? 1.f : exp2_hw(m[a] - mn);  // 0 while m is -inf
             float ps = 0.f;
 #pragma unroll
             for (int b = 0; b < 4; b++) {
-                const float pr = mn == -INFINITY ? 0.f : exp2f(sc[a][b] - mn);
+                const float pr = mn == -INFINITY ? 0.f : exp2_hw(sc[a][b] - mn);
                 Ps[(ti + 16 * a) * SLD + tj + 16 * b] = pr;
                 ps += pr;
             }
@@ -845,7 +851,7 @@ __global__ __launch_bounds__(kBlock) void attn_prefill_mfma_kernel(const AttnPar
         mt = fmaxf(mt, __shfl_xor(mt, 16));
         mt = fmaxf(mt, __shfl_xor(mt, 32));
         const float mn = fmaxf(m, mt);
-        const float corr = mn == -INFINITY ? 1.f : exp2f(m - mn);
+        const float corr = mn == -INFINITY ? 1.f : exp2_hw(m - mn);
         float ps = 0.f;
         uint32_t ph[4][2];  // P as fp16 pairs: sub-tile j, rows r = 0,1 and 2,3
 #pragma unroll
@@ -853,7 +859,7 @@ __global__ __launch_bounds__(kBlock) void attn_prefill_mfma_kernel(const AttnPar
             float pr[4];
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                pr[r] = mn == -INFINITY ? 0.f : exp2f(st[j][r] - mn);
+                pr[r] = mn == -INFINITY ? 0.f : exp2_hw(st[j][r] - mn);
                 ps += pr[r];
             }
             ph[j][0] = pack_half2(pr[0], pr[1]);
