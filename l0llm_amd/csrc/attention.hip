@@ -219,28 +219,45 @@ __global__ __launch_bounds__(kBlock) void attn_split_kernel(const AttnParams p, 
         float vf[U][8];
 #pragma unroll
         for (int u = 0; u < U; u++) v[u].get(vf[u]);
+        float mxs[G], ref[G];
+        bool grew = false;
 #pragma unroll
         for (int h = 0; h < G; h++) {
             float mx = m[h];
 #pragma unroll
             for (int u = 0; u < U; u++) mx = fmaxf(mx, sc[u][h]);
-            const float ref = mx == -INFINITY ? 0.f : mx;  // no valid position yet: keep zeros
-            const float c = exp2_hw(m[h] - ref);
+            grew |= mx > m[h];
+            mxs[h] = mx;
+            ref[h] = mx == -INFINITY ? 0.f : mx;  // no valid position yet: keep zeros
+        }
+        // Rescale only when a running maximum moved somewhere in the wave: otherwise every factor
+        // is 2^0 = 1 (or 0 on a slot still all zeros) and the products would change no bit.
+        if (__builtin_amdgcn_ballot_w64(grew)) {
+#pragma unroll
+            for (int h = 0; h < G; h++) {
+                const float c = exp2_hw(m[h] - ref[h]);
+                l[h] *= c;
+#pragma unroll
+                for (int d = 0; d < 8; d++) acc[h][d] *= c;
+                m[h] = mxs[h];
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < G; h++) {
             float pr[U];
 #pragma unroll
-            for (int u = 0; u < U; u++) pr[u] = exp2_hw(sc[u][h] - ref);
-            float lsum = l[h] * c;
+            for (int u = 0; u < U; u++) pr[u] = exp2_hw(sc[u][h] - ref[h]);
+            float lsum = l[h];
 #pragma unroll
             for (int u = 0; u < U; u++) lsum += pr[u];
             l[h] = lsum;
 #pragma unroll
             for (int d = 0; d < 8; d++) {
-                float a = acc[h][d] * c;
+                float a = acc[h][d];
 #pragma unroll
                 for (int u = 0; u < U; u++) a = fmaf(pr[u], vf[u][d], a);
                 acc[h][d] = a;
             }
-            m[h] = mx;
         }
     };
 
