@@ -943,9 +943,10 @@ int launch_prefill_hd(hipStream_t s, const AttnParams& p, int pos0, int tokens) 
 
 int attention_default_splits(int batch, int nkv, int max_len, int compute_units) {
     // Positions per split: at least two steps (128 positions at head_dim 128), so a block
-    // overlaps its second step's loads with the first step's compute, and about one block per CU
-    // in total (measured: 134 MB of K/V at batch 1 x 32768 or batch 8 x 4096 positions take
-    // 28.7 us against 33.7 us at two blocks per CU); at most kMaxSplits.
+    // overlaps its second step's loads with the first step's compute; at most kMaxSplits. Blocks
+    // per CU: two while every split still gets at least 2048 positions (long streams: batch 8 x
+    // 32768 positions, 1.07 GB of K/V, 195-200 us against 200-206 us at one), else one (batch 1
+    // x 32768 or batch 8 x 4096, 134 MB: 28.7 us against 33.7 us at two).
     // L0H_ATTN_SPLIT_POSITIONS overrides the minimum and L0H_ATTN_BLOCKS_PER_CU the blocks per CU
     // (tuning).
     static const int min_pos = [] {
@@ -953,15 +954,21 @@ int attention_default_splits(int batch, int nkv, int max_len, int compute_units)
         const int v = e ? std::atoi(e) : 128;
         return v > 0 ? v : 128;
     }();
-    static const int per_cu = [] {
+    static const int per_cu_env = [] {
         const char* e = std::getenv("L0H_ATTN_BLOCKS_PER_CU");
-        const int v = e ? std::atoi(e) : 1;
-        return v > 0 ? v : 1;
+        const int v = e ? std::atoi(e) : 0;
+        return v > 0 ? v : 0;
     }();
-    const int target =
-        (int)ceil_div((size_t)per_cu * std::max(compute_units, 1), (size_t)std::max(batch * nkv, 1));
-    const int by_len = (int)ceil_div((size_t)std::max(max_len, 1), (size_t)min_pos);
-    return std::max(1, std::min(kMaxSplits, std::min(target, by_len)));
+    const int len = std::max(max_len, 1);
+    auto splits_for = [&](int per_cu) {
+        const int target =
+            (int)ceil_div((size_t)per_cu * std::max(compute_units, 1), (size_t)std::max(batch * nkv, 1));
+        const int by_len = (int)ceil_div((size_t)len, (size_t)min_pos);
+        return std::max(1, std::min(kMaxSplits, std::min(target, by_len)));
+    };
+    if (per_cu_env) return splits_for(per_cu_env);
+    const int two = splits_for(2);
+    return len / two >= 2048 ? two : splits_for(1);
 }
 
 size_t attention_partials_bytes(const AttnParams& p) {
