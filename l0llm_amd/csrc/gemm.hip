@@ -362,13 +362,17 @@ Plan plan_for(int m, int n, int k, int cus) {
     // room for two waves per SIMD (the 64-column wave tile holds one). Eight such waves per block
     // share one activation tile across 256 columns, halving the activation bytes each block pulls
     // from L2 (what bounds these shapes): int8 at M = 2047, gate|up 4096 -> 28672 takes 528 us
-    // against 616 us with four waves and 633 us with the 128 x 64 tile.
+    // against 616 us with four waves and 633 us with the 128 x 64 tile. From 1024 rows, 256-row
+    // blocks of the same eight waves (256 x 256, a third less L2 traffic per flop) come first
+    // where they still make 3/4 of a block per CU: int8 q|k|v 4096 -> 6144 at M = 2047 in 120 us
+    // against 130 us, gate|up 533 us against 549 us (at N = 4096, 128 such blocks leave half the
+    // CUs idle: 115 us against 82 us, so the 128-row tile stays).
     struct Tile {
         int bm, nw, waves;
     };
     static const Tile tiles[] = {{128, 64, 4}, {128, 32, 4}, {128, 16, 4}, {64, 64, 4}, {64, 32, 4}, {64, 16, 4}};
-    static const Tile tiles_tall[] = {{128, 32, 8}, {128, 32, 4}, {128, 64, 4}, {128, 16, 4},
-                                      {64, 64, 4},  {64, 32, 4},  {64, 16, 4}};
+    static const Tile tiles_tall[] = {{256, 32, 8}, {128, 32, 8}, {128, 32, 4}, {128, 64, 4},
+                                      {128, 16, 4}, {64, 64, 4},  {64, 32, 4},  {64, 16, 4}};
     const int steps = k / BK;
     const size_t want = (size_t)cus * 3 / 4;
     auto blocks = [&](const Tile& t) { return (size_t)ceil_div(n, t.waves * t.nw) * ceil_div(m, t.bm); };
@@ -377,6 +381,7 @@ Plan plan_for(int m, int n, int k, int cus) {
     for (int ti = 0; ti < count; ti++) {
         const Tile& t = list[ti];
         if (m <= 64 && t.bm == 128) continue;
+        if (t.bm == 256 && m < 1024) continue;
         if (m > 64 && t.bm == 64 && t.nw == 64) continue;
         const size_t b = blocks(t);
         for (int s = 1; s <= kMaxSplits && (s == 1 || steps / s >= 64); s *= 2)
@@ -394,10 +399,10 @@ int launch_tiles(hipStream_t s, int m, int n, int k, const void* x, const void* 
                  int y_dtype, int epi, int splits, float* ws) {
     constexpr int MF = NW % 32 == 0 ? 32 : 16;
     // Stages of two K steps where K allows, except the 128 x 64 wave tile (its two-step ring, with
-    // fewer stages to fit the registers, measured slower) and eight-wave blocks below K = 8192
-    // (one-step stages measured faster there: int8 gate|up 528 us against 559 us).
+    // fewer stages to fit the registers, measured slower) and 128-row eight-wave blocks below
+    // K = 8192 (one-step stages measured faster there: int8 gate|up 528 us against 559 us).
     constexpr bool kTwo = NW != 64;
-    const bool two = kTwo && k % (2 * BK) == 0 && (NWV == 4 || k >= 8192);
+    const bool two = kTwo && k % (2 * BK) == 0 && (NWV == 4 || BM == 256 || k >= 8192);
     const int unit = two ? 2 * BK : BK;
     const int k_per_split = (k / unit + splits - 1) / splits * unit;
     // The kernel decodes (row block, split, column block) from the linear block id; the grid only
@@ -408,7 +413,7 @@ int launch_tiles(hipStream_t s, int m, int n, int k, const void* x, const void* 
     // One row block: each weight byte is read by one block, so it is streamed past the caches.
     const bool nt = grid.x == 1;
     if constexpr (kTwo) {
-        constexpr int P2 = ring_depth2(NW);
+        constexpr int P2 = BM == 256 ? 3 : ring_depth2(NW);  // 256 rows: three stages fit the registers
         if (two && nt)
             gemm_nk_kernel<WT, BM, NW, true, P2, MF, 2, NWV><<<grid, 64 * NWV, 0, s>>>(m, n, k, k_per_split, xp, w,
                                                                                       scales, y, y_dtype, epi, part);
@@ -434,6 +439,8 @@ int launch_tiles(hipStream_t s, int m, int n, int k, const void* x, const void* 
 template <int WT>
 int launch_plan(hipStream_t s, const Plan& p, int m, int n, int k, const void* x, const void* w,
                 const uint16_t* scales, void* y, int y_dtype, int epi, float* ws) {
+    if (p.bm == 256 && p.nw == 32 && p.waves == 8)
+        return launch_tiles<WT, 256, 32, 8>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws);
     if (p.bm == 128 && p.nw == 32 && p.waves == 8)
         return launch_tiles<WT, 128, 32, 8>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws);
 #define L0H_GEMM_CASE(BM_, NW_)                                                                                  \
