@@ -74,6 +74,30 @@ __device__ __forceinline__ float slot_reduce(float v) {
     return op(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
 }
 
+// Lane j of each 16-lane row, in every lane of that row (DPP row_newbcast).
+template <int J>
+__device__ __forceinline__ float row_lane(float v) {
+    return dpp_src<0x150 + J, 0xf>(v);
+}
+
+// Reduce-scatter of 16 values over a 16-lane row: on return, lane r of the row holds the sum over
+// the row's 16 lanes of x[r]. Four pairings, each a DPP lane permutation that is an XOR of the
+// lane index (row_mirror r ^ 15, row_half_mirror r ^ 7, quad_perm [3,2,1,0] r ^ 3, [1,0,3,2]
+// r ^ 1); at each, a lane keeps the half of its values whose index bit (3, 2, 1, 0) equals its
+// own lane bit and adds its partner's copy of that half. 45 VALU operations, against 64 for 16
+// separate butterflies, and each score is then held by one lane instead of sixteen.
+__device__ __forceinline__ float row_reduce_scatter16(const float (&x)[16], int r) {
+    float y[8], z[4], w[2];
+    const bool b3 = r & 8, b2 = r & 4, b1 = r & 2, b0 = r & 1;
+#pragma unroll
+    for (int i = 0; i < 8; i++) y[i] = (b3 ? x[i + 8] : x[i]) + dpp_src<0x140, 0xf>(b3 ? x[i] : x[i + 8]);
+#pragma unroll
+    for (int i = 0; i < 4; i++) z[i] = (b2 ? y[i + 4] : y[i]) + dpp_src<0x141, 0xf>(b2 ? y[i] : y[i + 4]);
+#pragma unroll
+    for (int i = 0; i < 2; i++) w[i] = (b1 ? z[i + 2] : z[i]) + dpp_src<0x1B, 0xf>(b1 ? z[i] : z[i + 2]);
+    return (b0 ? w[1] : w[0]) + dpp_src<0xB1, 0xf>(b0 ? w[0] : w[1]);
+}
+
 template <int CT>
 struct CacheRow;
 template <>
@@ -142,8 +166,9 @@ __device__ __forceinline__ void split_range(const AttnParams& p, int seq_len_ste
 }
 
 // QT: q dtype, G: q heads per kv head rounded up to a power of two (heads >= p.nh / p.nkv are
-// computed on clamped inputs and not written).
-template <int HD, int CT, int QT, int G>
+// computed on clamped inputs and not written). SC: the reduce-scattered softmax where the shape
+// allows it (head_dim 128, four heads per kv head).
+template <int HD, int CT, int QT, int G, bool SC = false>
 __global__ __launch_bounds__(kBlock) void attn_split_kernel(const AttnParams p, int seq_len_step,
                                                             size_t cache_batch_stride) {
     constexpr int LPP = HD / 8;     // lanes per position
@@ -200,7 +225,71 @@ __global__ __launch_bounds__(kBlock) void attn_split_kernel(const AttnParams p, 
 #pragma unroll
         for (int d = 0; d < 8; d++) acc[h][d] = 0.f;
     }
+    // Four heads x four positions per slot over a 16-lane row (head_dim 128, the Llama-3 shapes):
+    // the 16 partial dot products are reduce-scattered, so lane r of the row owns the score of
+    // position r / 4, head r % 4, and keeps the running max and sum of head r % 4; the softmax
+    // then costs one exponential per lane and step instead of twenty.
+    constexpr bool kScatter = SC && LPP == 16 && G == 4 && U == 4;
+    const int rl = lane & 15;
+    float mh = -INFINITY, lh = 0.f;
+    auto compute_scatter = [&](const CacheRow<CT> (&k)[U], const CacheRow<CT> (&v)[U], int step) {
+        float x[16];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            float kf[8];
+            k[u].get(kf);
+#pragma unroll
+            for (int h = 0; h < G; h++) {
+                float s = 0.f;
+#pragma unroll
+                for (int d = 0; d < 8; d++) s = fmaf(qr[h][d], kf[d], s);
+                x[u * G + h] = s;
+            }
+        }
+        const float s = row_reduce_scatter16(x, rl);
+        const bool valid = step * NG * U + (rl >> 2) * NG + slot < n;
+        const float sc = valid ? s : -INFINITY;
+        float mx = fmaxf(sc, dpp_src<0x124, 0xf>(sc));  // row_ror:4, then :8: the head's 4 positions
+        mx = fmaxf(mx, dpp_src<0x128, 0xf>(mx));
+        const float mnew = fmaxf(mh, mx);
+        const float ref = mnew == -INFINITY ? 0.f : mnew;  // no valid position yet: keep zeros
+        // Rescale only when a running maximum moved somewhere in the wave (else the factor is 1).
+        if (__builtin_amdgcn_ballot_w64(mnew > mh)) {
+            const float c = exp2_hw(mh - ref);
+            lh *= c;
+            const float cb[4] = {row_lane<0>(c), row_lane<1>(c), row_lane<2>(c), row_lane<3>(c)};
+#pragma unroll
+            for (int h = 0; h < G; h++)
+#pragma unroll
+                for (int d = 0; d < 8; d++) acc[h][d] *= cb[h];
+            mh = mnew;
+        }
+        const float pr = exp2_hw(sc - ref);
+        float ps = pr + dpp_src<0x124, 0xf>(pr);
+        ps += dpp_src<0x128, 0xf>(ps);
+        lh += ps;
+        const float pb[16] = {row_lane<0>(pr),  row_lane<1>(pr),  row_lane<2>(pr),  row_lane<3>(pr),
+                              row_lane<4>(pr),  row_lane<5>(pr),  row_lane<6>(pr),  row_lane<7>(pr),
+                              row_lane<8>(pr),  row_lane<9>(pr),  row_lane<10>(pr), row_lane<11>(pr),
+                              row_lane<12>(pr), row_lane<13>(pr), row_lane<14>(pr), row_lane<15>(pr)};
+        float vf[U][8];
+#pragma unroll
+        for (int u = 0; u < U; u++) v[u].get(vf[u]);
+#pragma unroll
+        for (int h = 0; h < G; h++)
+#pragma unroll
+            for (int d = 0; d < 8; d++) {
+                float a = acc[h][d];
+#pragma unroll
+                for (int u = 0; u < U; u++) a = fmaf(pb[u * G + h], vf[u][d], a);
+                acc[h][d] = a;
+            }
+    };
     auto compute = [&](const CacheRow<CT> (&k)[U], const CacheRow<CT> (&v)[U], int step) {
+        if constexpr (kScatter) {
+            compute_scatter(k, v, step);
+            return;
+        }
         float sc[U][G];
 #pragma unroll
         for (int u = 0; u < U; u++) {
@@ -282,6 +371,16 @@ __global__ __launch_bounds__(kBlock) void attn_split_kernel(const AttnParams p, 
             load(ka, va, s + 1);
             compute(kb, vb, s);
             s++;
+        }
+    }
+
+    if constexpr (kScatter) {  // lane h of each row holds head h's running max and sum
+        const float mv[4] = {row_lane<0>(mh), row_lane<1>(mh), row_lane<2>(mh), row_lane<3>(mh)};
+        const float lv[4] = {row_lane<0>(lh), row_lane<1>(lh), row_lane<2>(lh), row_lane<3>(lh)};
+#pragma unroll
+        for (int h = 0; h < G; h++) {
+            m[h] = mv[h];
+            l[h] = lv[h];
         }
     }
 
@@ -425,7 +524,22 @@ __global__ __launch_bounds__(kBlock) void attn_merge_kernel(const AttnParams p) 
 template <int HD, int CT, int QT, int G>
 int launch_g(hipStream_t s, const AttnParams& p, int seq_len_step, size_t cache_batch_stride) {
     dim3 grid(p.splits, p.nkv, p.batch);
-    attn_split_kernel<HD, CT, QT, G><<<grid, kBlock, 0, s>>>(p, seq_len_step, cache_batch_stride);
+    // The reduce-scattered softmax has fewer VALU operations but longer dependent chains per step.
+    // Measured on the 8B shapes: faster for short splits (decode at 2048 positions: 10.4 against
+    // 10.9 us per layer; up to 256 positions per split) and for long ones at two blocks per CU
+    // (batch 8 x 32768: 183 against 192 us), 3-4 % slower at one block per CU with 512-1024
+    // positions per split (batch 1 x 32768, batch 8 x 4096), where one wave per SIMD cannot hide
+    // those chains.
+    if constexpr (HD == 128 && G == 4) {
+        const int per_split = p.max_seq_len / std::max(p.splits, 1);
+        if (per_split <= 256 || per_split >= 2048) {
+            attn_split_kernel<HD, CT, QT, G, true><<<grid, kBlock, 0, s>>>(p, seq_len_step, cache_batch_stride);
+        } else {
+            attn_split_kernel<HD, CT, QT, G, false><<<grid, kBlock, 0, s>>>(p, seq_len_step, cache_batch_stride);
+        }
+    } else {
+        attn_split_kernel<HD, CT, QT, G><<<grid, kBlock, 0, s>>>(p, seq_len_step, cache_batch_stride);
+    }
     int st = launch_status("attention");
     if (st || p.splits == 1) return st;
     constexpr int NC = G * HD / 4, CB = NC < 32 ? NC : 32;

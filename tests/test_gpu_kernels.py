@@ -269,9 +269,11 @@ def test_kv_store_bit_exact(device, suite, cache):
 
 # ---- attention ---------------------------------------------------------------------------------
 
+# Head dim 128 with four heads per kv head runs the reduce-scattered softmax for splits of up to
+# 256 positions (512, 4096, 2049) and the per-slot one for 375 positions per split (12000).
 ATTN = [(64, 14, 2, 37, l0.F32), (64, 14, 2, 1, l0.F16), (128, 32, 8, 512, l0.F16), (128, 32, 8, 4096, l0.F16),
         (128, 32, 8, 2049, l0.F32), (128, 8, 8, 300, l0.F16), (16, 4, 2, 50, l0.F16), (32, 8, 2, 100, l0.F32),
-        (64, 16, 2, 700, l0.F16)]
+        (64, 16, 2, 700, l0.F16), (128, 32, 8, 12000, l0.F16)]
 
 
 @pytest.mark.parametrize("hd,nh,nkv,seq,cache", ATTN)
@@ -292,9 +294,10 @@ def test_attention_decode_matches_oracle(device, suite, hd, nh, nkv, seq, cache)
     np.testing.assert_array_equal(ob.read(), out)
 
 
-@pytest.mark.parametrize("batch,seq", [(8, 512), (1, 32768)])
+@pytest.mark.parametrize("batch,seq", [(8, 512), (1, 32768), (8, 8192)])
 def test_attention_decode_batched_fp16(device, suite, batch, seq):
-    """GQA 32q/8kv/128, fp16 q/K/V, fp16 out, fp32 softmax."""
+    """GQA 32q/8kv/128, fp16 q/K/V, fp16 out, fp32 softmax. Splits of 128 (8 x 512) and 2048
+    (8 x 8192) positions take the reduce-scattered softmax, 1024 (1 x 32768) the per-slot one."""
     rng = np.random.default_rng(batch * seq)
     hd, nh, nkv = 128, 32, 8
     kf = rng.normal(0, 1, (batch, seq, nkv * hd)).astype(np.float16)
