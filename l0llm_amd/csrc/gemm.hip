@@ -363,10 +363,12 @@ Plan plan_for(int m, int n, int k, int cus) {
     // share one activation tile across 256 columns, halving the activation bytes each block pulls
     // from L2 (what bounds these shapes): int8 at M = 2047, gate|up 4096 -> 28672 takes 528 us
     // against 616 us with four waves and 633 us with the 128 x 64 tile. From 1024 rows, 256-row
-    // blocks of the same eight waves (256 x 256, a third less L2 traffic per flop) come first
-    // where they still make 3/4 of a block per CU: int8 q|k|v 4096 -> 6144 at M = 2047 in 120 us
-    // against 130 us, gate|up 533 us against 549 us (at N = 4096, 128 such blocks leave half the
-    // CUs idle: 115 us against 82 us, so the 128-row tile stays).
+    // blocks of the same eight waves (256 x 256, a third less L2 traffic per flop) are taken
+    // without a K split where they make 3/4 of a block per CU and need no more rounds of blocks
+    // over the CUs, counted in 128-row block units, than the 128-row tile: int8 at M = 2047,
+    // q|k|v 4096 -> 6144 (192 blocks, one round, against 384 in two) 122 us against 134 us;
+    // gate|up -> 28672 (896 blocks in 3.5 rounds against 1792 in 7) would take 539 us against
+    // 531 us; at N = 4096 (128 blocks) O takes 123 us, 100 us with K split in two, against 86 us.
     struct Tile {
         int bm, nw, waves;
     };
@@ -381,9 +383,15 @@ Plan plan_for(int m, int n, int k, int cus) {
     for (int ti = 0; ti < count; ti++) {
         const Tile& t = list[ti];
         if (m <= 64 && t.bm == 128) continue;
-        if (t.bm == 256 && m < 1024) continue;
         if (m > 64 && t.bm == 64 && t.nw == 64) continue;
         const size_t b = blocks(t);
+        if (t.bm == 256) {
+            if (m < 1024 || b < want) continue;
+            const size_t cu = (size_t)std::max(cus, 1);
+            const size_t r256 = 2 * ((b + cu - 1) / cu), r128 = (blocks(Tile{128, 32, 8}) + cu - 1) / cu;
+            if (r256 <= r128) return Plan{256, 32, 1, 8};
+            continue;
+        }
         for (int s = 1; s <= kMaxSplits && (s == 1 || steps / s >= 64); s *= 2)
             if (b * s >= want) return Plan{t.bm, t.nw, s, t.waves};
     }

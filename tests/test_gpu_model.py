@@ -175,13 +175,13 @@ def test_wide_prefill_split_k_epilogues_match_decode(device, precision, tol):
         assert np.max(np.abs(seq - batched)) <= tol * scale, np.max(np.abs(seq - batched)) / scale
 
 
-@pytest.mark.parametrize("tokens", [600, 1030])
+@pytest.mark.parametrize("tokens", [600, 2048])
 @pytest.mark.parametrize("precision,tol", [(l0.PRECISION_INT8, 1e-2), (l0.PRECISION_BFLOAT16, 5e-2)])
 def test_tall_prefill_eight_wave_tiles_match_decode(device, precision, tol, tokens):
     """599 prefill rows at hidden 4096, intermediate 8192: the GEMMs take the eight-wave 128-row
-    tiles (gate|up one-step stages; down, K = 8192, two-step stages with K split in four). 1029
-    rows: gate|up (N = 16384) takes the 256 x 256 blocks with the SwiGLU epilogue over a ragged
-    last row block, the other three GEMMs the 128-row tiles."""
+    tiles (gate|up one-step stages; down, K = 8192, two-step stages with K split in four). 2047
+    rows: q|k|v (N = 6144) and gate|up (N = 16384, SwiGLU epilogue) take the 256 x 256 blocks
+    with a ragged last row block, O and down the 128-row tiles."""
     cfg = l0.HfConfig(hidden_size=4096, intermediate_size=8192, num_layers=1, num_attention_heads=32,
                       num_key_value_heads=8, head_dim=128, vocab_size=256, max_position_embeddings=4096,
                       rms_norm_eps=1e-5, rope_theta=500000.0)
