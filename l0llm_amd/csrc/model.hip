@@ -84,15 +84,37 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_rows16_kernel(const float* x, 
                                                                 float eps, int n, int dt) {
     __shared__ float red[kWaves];
     const float* xr = x + (size_t)blockIdx.x * n;
+    auto cvt = [&](float v) { return dt == L0H_BF16 ? float_to_bf16_bits(v) : __half_as_ushort(__float2half_rn(v)); };
+    if (n % 4 == 0 && n <= 16 * kBlock) {  // block-uniform: the row in registers, 16-byte loads
+        const int n4 = n / 4;
+        float4 v[4];
+        float ss = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int i = threadIdx.x + j * kBlock;
+            v[j] = i < n4 ? reinterpret_cast<const float4*>(xr)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+            ss += v[j].x * v[j].x + v[j].y * v[j].y + v[j].z * v[j].z + v[j].w * v[j].w;
+        }
+        ss = block_sum(ss, red);
+        const float inv = rsqrtf(ss / (float)n + eps);
+        uint2* o = reinterpret_cast<uint2*>(out + (size_t)blockIdx.x * n);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int i = threadIdx.x + j * kBlock;
+            if (i < n4) {
+                const float4 wv = reinterpret_cast<const float4*>(w)[i];
+                o[i] = make_uint2((uint32_t)cvt(v[j].x * inv * wv.x) | ((uint32_t)cvt(v[j].y * inv * wv.y) << 16),
+                                  (uint32_t)cvt(v[j].z * inv * wv.z) | ((uint32_t)cvt(v[j].w * inv * wv.w) << 16));
+            }
+        }
+        return;
+    }
     float ss = 0.f;
     for (int i = threadIdx.x; i < n; i += kBlock) ss += xr[i] * xr[i];
     ss = block_sum(ss, red);
     const float inv = rsqrtf(ss / (float)n + eps);
     uint16_t* o = out + (size_t)blockIdx.x * n;
-    for (int i = threadIdx.x; i < n; i += kBlock) {
-        const float v = xr[i] * inv * w[i];
-        o[i] = dt == L0H_BF16 ? float_to_bf16_bits(v) : __half_as_ushort(__float2half_rn(v));
-    }
+    for (int i = threadIdx.x; i < n; i += kBlock) o[i] = cvt(xr[i] * inv * w[i]);
 }
 
 // fp32 activations -> the weight dtype (F16 / BF16) for the MFMA GEMM.
