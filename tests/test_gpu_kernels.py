@@ -270,10 +270,11 @@ def test_kv_store_bit_exact(device, suite, cache):
 # ---- attention ---------------------------------------------------------------------------------
 
 # Head dim 128 with four heads per kv head runs the reduce-scattered softmax for splits of up to
-# 256 positions (512, 4096, 2049) and the per-slot one for 375 positions per split (12000).
+# 256 positions (512, 4096, 2049; 24 / 8 heads: three per group padded to four) and the per-slot
+# one for 375 positions per split (12000).
 ATTN = [(64, 14, 2, 37, l0.F32), (64, 14, 2, 1, l0.F16), (128, 32, 8, 512, l0.F16), (128, 32, 8, 4096, l0.F16),
         (128, 32, 8, 2049, l0.F32), (128, 8, 8, 300, l0.F16), (16, 4, 2, 50, l0.F16), (32, 8, 2, 100, l0.F32),
-        (64, 16, 2, 700, l0.F16), (128, 32, 8, 12000, l0.F16)]
+        (64, 16, 2, 700, l0.F16), (128, 32, 8, 12000, l0.F16), (128, 24, 8, 700, l0.F16)]
 
 
 @pytest.mark.parametrize("hd,nh,nkv,seq,cache", ATTN)
