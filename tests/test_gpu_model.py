@@ -196,6 +196,23 @@ def test_tall_prefill_eight_wave_tiles_match_decode(device, precision, tol, toke
         assert np.max(np.abs(seq - batched)) <= tol * scale, np.max(np.abs(seq - batched)) / scale
 
 
+def test_wide_hidden_prefill_residual_256_tiles_match_decode(device):
+    """Hidden 8192 at 2047 prefill rows: O (8192 x 8192) and down (8192 x 2048) take the 256 x 256
+    GEMM blocks with the residual epilogue (q|k|v and gate|up the 128-row tiles)."""
+    cfg = l0.HfConfig(hidden_size=8192, intermediate_size=2048, num_layers=1, num_attention_heads=64,
+                      num_key_value_heads=8, head_dim=128, vocab_size=256, max_position_embeddings=4096,
+                      rms_norm_eps=1e-5, rope_theta=500000.0)
+    prompt = np.random.default_rng(17).integers(0, cfg.vocab_size, 2048).tolist()
+    with l0.LlmModel(device, cfg, precision=l0.PRECISION_INT8, cache_dtype=l0.F16, max_seq_len=2088) as m:
+        m.init_random(91, 0.02)
+        seq = None
+        for i, t in enumerate(prompt):
+            seq = m.compute_logits(t, i)
+        batched = m.prefill(prompt)
+        scale = np.max(np.abs(seq))
+        assert np.max(np.abs(seq - batched)) <= 1e-2 * scale, np.max(np.abs(seq - batched)) / scale
+
+
 @pytest.mark.parametrize("name,precision", [("qwen2", l0.PRECISION_INT8), ("llama", l0.PRECISION_BFLOAT16)])
 def test_model_loads_from_safetensors(device, tmp_path, name, precision):
     """LlmModel.Load's weight pass from a sharded safetensors checkpoint (bf16 tensors, as HF
