@@ -94,7 +94,8 @@ int l0h_abort_recording(l0h_device* dev);
 /* Launches the command list of the last l0h_end_recording again, `count` times back to back on
  * the device's stream, and reports the mean HIP-event time of one replay in milliseconds (the
  * reference re-records a list per token, LlmModel.cs:417-443; replaying one is the same work
- * without the recording). L0H_ERR_INVALID_OP when nothing has been recorded. */
+ * without the recording). L0H_ERR_INVALID_OP when nothing has been recorded, or when memory the
+ * recording may use was freed or moved since (l0h_free, workspace or scratch growth). */
 int l0h_replay_recording(l0h_device* dev, int count, float* ms_per_replay);
 /* ComputeDevice.IsRecording (LlmModel.cs:353, :417). */
 int l0h_is_recording(l0h_device* dev, int* out);
@@ -124,10 +125,29 @@ int l0h_gemv_execute_rows(l0h_device* dev, int rows, int out_dim, int in_dim, co
 /* Gemm.Execute(dev, M, N, K, x, W, y) (LlmMatrix.cs:142, :169): fp32 [M,K] x [K,N]. */
 int l0h_gemm_execute(l0h_device* dev, int m, int n, int k, const float* x, const float* w,
                      float* y);
-/* GemvQ8.Execute / ExecuteRows (LlmMatrix.cs:130, :157, :235, :239) in the weight-only int8 format:
- * weight-only int8 [N, K] with one fp16 scale per output row, fp32 x and y. The reference's
- * GemvQ8.Quantize step (activation quantization) has no counterpart: activations stay fp32. */
-int l0h_gemv_q8_execute_rows(l0h_device* dev, int rows, int out_dim, int in_dim, const float* x,
+/* LlmGemvQ8Kernel.GroupSize (LlmMatrix.cs:29-31; LlmModel.cs:142): 32, the K granularity of the
+ * int8 path (Supports asks K % 32 == 0; the activation scratch rounds its width up to it). */
+int l0h_gemv_q8_group_size(void);
+/* LlmKernelSuite.EnsureQ8Scratch(device, rows, cols) (LlmModel.cs:139-144): the device's int8
+ * activation scratch of at least rows x cols fp32 values. Must run before recording starts when it
+ * has to grow (L0H_ERR_INVALID_OP inside a recording). */
+int l0h_q8_scratch_ensure(l0h_device* dev, int rows, int cols);
+/* LlmKernelSuite.Q8Scratch and its RowCapacity (LlmMatrix.cs:242-251): the scratch pointer (NULL
+ * before l0h_q8_scratch_ensure), its rows and its columns. */
+int l0h_q8_scratch(l0h_device* dev, float** scratch, int* row_capacity, int* cols);
+/* GemvQ8.Quantize(dev, rows, inDim, x, scratch) (LlmMatrix.cs:129, :156, :201): stages rows x inDim
+ * activations in the scratch for the following Execute calls. The weight-only int8 format keeps
+ * activations in fp32, so staging is a copy (the reference quantizes them to int8 here).
+ * L0H_ERR_INVALID_OP when the device's own scratch is too small (RequireScratch, :244-251). */
+int l0h_gemv_q8_quantize(l0h_device* dev, int rows, int in_dim, const float* x, float* scratch);
+/* GemvQ8.Execute(dev, outDim, inDim, scratch, words, scales, y) (LlmMatrix.cs:130, :235): y[N] =
+ * (W[N, K] . scratch[K]) * scales[N]. words: int8 [N, K] row-major (four weights per 32-bit word,
+ * little-endian, as l0h_quantize_i8pc writes them); scales: fp16 [N], one per output row. */
+int l0h_gemv_q8_execute(l0h_device* dev, int out_dim, int in_dim, const float* scratch, const int8_t* w,
+                        const uint16_t* scales, float* y);
+/* GemvQ8.ExecuteRows(dev, rows, outDim, inDim, scratch, words, scales, y) (LlmMatrix.cs:157, :239):
+ * the same for `rows` staged rows, W read once per group of up to 8 rows. */
+int l0h_gemv_q8_execute_rows(l0h_device* dev, int rows, int out_dim, int in_dim, const float* scratch,
                              const int8_t* w, const uint16_t* scales, float* y);
 
 /* RMSNorm.Execute(dev, x, residual, w, out, eps, n, rows, addResidual)
@@ -157,6 +177,11 @@ int l0h_kv_cache_store_execute(l0h_device* dev, const float* k, const float* v, 
 int l0h_kv_cache_store_execute_rows(l0h_device* dev, const float* k, const float* v,
                                     void* k_cache, void* v_cache, int cache_dtype, int pos0,
                                     int kv_dim, int tokens);
+/* Sizes the device's split-reduction workspace for decode attention at this shape, before a
+ * recording starts (the attention counterpart of EnsureQ8Scratch, LlmModel.cs:139-144). Attention
+ * recorded without it still runs: with as many sequence splits as the workspace holds. */
+int l0h_attention_reserve(l0h_device* dev, int batch, int n_heads, int n_kv_heads, int head_dim,
+                          int max_seq_len);
 /* Attention.Execute(dev, q, K$, V$, out, headDim, nH, nKv, seqLen, maxSeqLen)
  * (LlmDecoderLayer.cs:325-327). Split-K over the sequence: no 15,000-token limit. */
 int l0h_attention_execute(l0h_device* dev, const float* q, const void* k_cache,

@@ -168,9 +168,41 @@ class LlmKernelSuite:
     def gemm_execute(self, m, n, k, x, w, y):
         check(lib.l0h_gemm_execute(self.device.handle, m, n, k, _ptr(x), _ptr(w), _ptr(y)))
 
-    def gemv_q8_execute_rows(self, rows, out_dim, in_dim, x, words, scales, y):
-        check(lib.l0h_gemv_q8_execute_rows(self.device.handle, rows, out_dim, in_dim, _ptr(x), _ptr(words),
+    # GemvQ8 in the weight-only int8 format (LlmMatrix.cs:29-31, :128-130, :155-157, :201, :235-251)
+    @staticmethod
+    def q8_group_size() -> int:
+        """LlmGemvQ8Kernel.GroupSize."""
+        return lib.l0h_gemv_q8_group_size()
+
+    def ensure_q8_scratch(self, rows: int, cols: int) -> None:
+        """LlmKernelSuite.EnsureQ8Scratch(device, rows, cols) (LlmModel.cs:139-144)."""
+        check(lib.l0h_q8_scratch_ensure(self.device.handle, rows, cols))
+
+    @property
+    def q8_scratch(self) -> "Buffer | None":
+        """LlmKernelSuite.Q8Scratch; its row_capacity attribute is RowCapacity."""
+        ptr, rows, cols = ctypes.c_void_p(), ctypes.c_int(), ctypes.c_int()
+        check(lib.l0h_q8_scratch(self.device.handle, ctypes.byref(ptr), ctypes.byref(rows), ctypes.byref(cols)))
+        if not ptr.value:
+            return None
+        buf = Buffer(self.device, rows.value * cols.value * 4, ptr=ptr.value, owned=False)
+        buf.row_capacity = rows.value
+        buf.cols = cols.value
+        return buf
+
+    def gemv_q8_quantize(self, rows, in_dim, x, scratch):
+        check(lib.l0h_gemv_q8_quantize(self.device.handle, rows, in_dim, _ptr(x), _ptr(scratch)))
+
+    def gemv_q8_execute(self, out_dim, in_dim, scratch, words, scales, y):
+        check(lib.l0h_gemv_q8_execute(self.device.handle, out_dim, in_dim, _ptr(scratch), _ptr(words), _ptr(scales),
+                                      _ptr(y)))
+
+    def gemv_q8_execute_rows(self, rows, out_dim, in_dim, scratch, words, scales, y):
+        check(lib.l0h_gemv_q8_execute_rows(self.device.handle, rows, out_dim, in_dim, _ptr(scratch), _ptr(words),
                                            _ptr(scales), _ptr(y)))
+
+    def attention_reserve(self, batch, n_heads, n_kv, head_dim, max_seq_len):
+        check(lib.l0h_attention_reserve(self.device.handle, batch, n_heads, n_kv, head_dim, max_seq_len))
 
     def rmsnorm_execute(self, x, residual, w, out, eps, n, rows, add_residual):
         check(lib.l0h_rmsnorm_execute(self.device.handle, _ptr(x), _ptr(residual), _ptr(w), _ptr(out),

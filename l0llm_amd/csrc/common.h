@@ -49,6 +49,9 @@ struct l0h_device {
     int compute_units = 0;
     bool recording = false;
     hipGraphExec_t cached_exec = nullptr;  // reused by l0h_end_recording via hipGraphExecUpdate
+    // Set when the kept graph was dropped because memory it may address was freed or moved
+    // (l0h_free, workspace growth): l0h_replay_recording then refuses until a new recording.
+    bool recording_dropped = false;
     // Split-reduction workspace (attention partials, argmax partials), grown on demand
     // outside recording; like LlmKernelSuite.EnsureQ8Scratch it must be sized before a
     // recording starts (LlmModel.cs:139-144).
@@ -56,6 +59,10 @@ struct l0h_device {
     size_t workspace_bytes = 0;
     unsigned* tickets = nullptr;  // self-resetting completion counters (zeroed once)
     size_t ticket_count = 0;
+    // Activation scratch of the int8 GEMV (LlmKernelSuite.Q8Scratch, LlmModel.cs:139-144):
+    // q8_rows x q8_cols fp32, grown by l0h_q8_scratch_ensure outside recording.
+    float* q8_scratch = nullptr;
+    int q8_rows = 0, q8_cols = 0;
     std::mutex mu;
 };
 
@@ -66,6 +73,9 @@ int use_device(l0h_device* dev);
 // Makes sure the workspace holds `bytes` and `tickets` counters. Fails while recording
 // if growth would be needed.
 int ensure_workspace(l0h_device* dev, size_t bytes, size_t tickets);
+// Drops the kept executable graph of the last recording (it may address memory that is about
+// to be freed or moved); l0h_replay_recording refuses until the next recording.
+void drop_recording(l0h_device* dev);
 
 // ---------------------------------------------------------------- dtypes --
 
@@ -106,6 +116,13 @@ __device__ inline void store_act(void* p, int dt, size_t i, float v) {
     } else {
         static_cast<uint16_t*>(p)[i] = float_to_bf16_bits(v);
     }
+}
+
+// store_act, with fp16 saturating at +-65504 instead of overflowing to inf: for activations that
+// must become a 16-bit MFMA operand (NaN stays NaN).
+__device__ inline void store_act_sat(void* p, int dt, size_t i, float v) {
+    if (dt == L0H_F16 && fabsf(v) > 65504.f) v = copysignf(65504.f, v);
+    store_act(p, dt, i, v);
 }
 
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));

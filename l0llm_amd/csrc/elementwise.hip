@@ -241,9 +241,11 @@ __global__ __launch_bounds__(kBlock) void init_i8pc_kernel(int8_t* q, uint16_t* 
     if (lane == 0) red[wave] = amax;
     __syncthreads();
     amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    const __half sh = __float2half_rn(amax / 127.0f);
-    const float s = __half2float(sh);
-    if (threadIdx.x == 0) scales[row] = __half_as_ushort(sh);
+    uint16_t sh = __half_as_ushort(__float2half_rn(amax / 127.0f));
+    if ((sh & 0x7fffu) == 0 && amax > 0.f) sh = 0x0001u;  // non-zero row: scale 2^-24 at least
+    if ((sh & 0x7fffu) >= 0x7c00u) sh = 0x7bffu;          // and 65504 at most
+    const float s = __half2float(__ushort_as_half(sh));
+    if (threadIdx.x == 0) scales[row] = sh;
     for (int i = threadIdx.x; i < k; i += kBlock) {
         float v = s > 0.f ? rintf(rng_normal(seed, base + i) * stddev / s) : 0.f;
         v = fminf(127.f, fmaxf(-127.f, v));

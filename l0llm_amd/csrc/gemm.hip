@@ -295,7 +295,7 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(1, 2))
         each_out([&](int row, int col, float v) {
             const float up = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xf, 0xf, false));
             if (row < M && col < N && (lane & 1) == 0)
-                store_act(Y, y_dtype, (size_t)row * (N / 2) + col / 2, v / (1.0f + __expf(-v)) * up);
+                store_act_sat(Y, y_dtype, (size_t)row * (N / 2) + col / 2, v / (1.0f + __expf(-v)) * up);
         });
     } else if (epi == EPI_RESIDUAL) {
         each_out([&](int row, int col, float v) {
@@ -320,7 +320,7 @@ __global__ void splitk_reduce_kernel(const float* partial, int splits, size_t mn
             g += t.x;
             u += t.y;
         }
-        store_act(Y, y_dtype, i, g / (1.0f + __expf(-g)) * u);
+        store_act_sat(Y, y_dtype, i, g / (1.0f + __expf(-g)) * u);
         return;
     }
     if (i >= mn) return;

@@ -62,13 +62,15 @@ int launch_gemv_nk(hipStream_t s, const GemvParams& p0) {
                          ((uintptr_t)p0.norm_w & 15) == 0 && ((size_t)p0.k * xsize) % 16 == 0;
     const bool pairs = p0.epilogue == EPI_SWIGLU || p0.epilogue == EPI_QKV;
     if (pairs && p0.n % 2) return fail(L0H_ERR_INVALID_ARG, "paired-row epilogues need an even row count");
-    const bool fits = k_pad_max * sizeof(float) <= kLdsBudget;
+    // Per activation row: the fp32 tile, plus one int8 bias term per 16 values.
+    const size_t row_tile = (k_pad_max + (p0.w_dtype == L0H_I8PC ? k_pad_max / 16 : 0)) * sizeof(float);
+    const bool fits = row_tile <= kLdsBudget;
     if (fused) {
         if (!aligned || !fits || p0.m != 1 || p0.x_dtype != L0H_F32 || (p0.epilogue != EPI_STORE && !p0.norm_w) ||
             (p0.epilogue == EPI_QKV && (p0.rotary_dim > 2 * kMaxRotaryHalf || p0.rotary_dim < 2)))
             return fail(L0H_ERR_UNSUPPORTED,
                         "fused GEMV needs one fp32 activation row with the RMSNorm prologue, K a multiple of the "
-                        "load width and a zero-padded row of at most 64 KiB");
+                        "load width and a zero-padded row that fits the LDS tile (16384 values)");
     }
     if (!aligned || !fits) {
         if (fused) return fail(L0H_ERR_UNSUPPORTED, "fused GEMV shape not supported");
@@ -82,7 +84,7 @@ int launch_gemv_nk(hipStream_t s, const GemvParams& p0) {
     while (done < p0.m) {
         const int left = p0.m - done;
         int mr = left >= 8 ? 8 : left >= 4 ? 4 : left >= 2 ? 2 : 1;
-        while (mr > 1 && (size_t)mr * k_pad_max * sizeof(float) > kLdsBudget) mr >>= 1;
+        while (mr > 1 && (size_t)mr * row_tile > kLdsBudget) mr >>= 1;
         GemvParams p = p0;
         p.m = mr;
         p.x = static_cast<const char*>(p0.x) + (size_t)done * p.k * xsize;
@@ -103,13 +105,108 @@ int launch_gemv_nk(hipStream_t s, const GemvParams& p0) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// Reference [K, N] layout (Gemv.Execute / Gemm.Execute): y[r, n] = sum_k x[r, k] * W[k, n].
-// Each thread owns 4 adjacent columns; the 4 waves of a block split K and reduce in LDS.
+// Reference [K, N] layout (Gemv.Execute / ExecuteRows, Gemm.Execute): y[r, n] = sum_k x[r, k] W[k, n].
+//
+// Fast path (N a multiple of the load width, 16-byte aligned W): lane l of a wave reads the
+// 16-byte chunk t * 64 + l of a weight row, i.e. EPC = 8 fp16 (4 fp32) adjacent columns, so one
+// wave instruction streams 1 KiB of one row. Block (column tile t, K slice s) covers 64 chunks
+// of columns and the rows [s * KS, (s + 1) * KS); its 4 waves take every fourth row of the slice,
+// with U rows in flight per lane. The slice's activations are staged in LDS (zero past K; the
+// clamped rows there add nothing), the waves reduce through LDS in a fixed order, and a split K
+// leaves per-slice partials [S, rows, N] that a second kernel sums in slice order. The slice
+// count fills the GPU: about two blocks per CU over the column tiles.
 // ---------------------------------------------------------------------------------------------
 namespace {
+constexpr int kKnUnroll = 8;           // weight rows in flight per lane
+constexpr int kKnLds = 160 * 1024;  // LDS bytes a block may use
+
+template <int WT, int MR>
+__global__ __launch_bounds__(kBlock) void gemv_kn_tile_kernel(int N, int K, int ks, const float* x, const void* w,
+                                                              float* out) {
+    constexpr int EPC = WT == L0H_F16 ? 8 : 4;
+    extern __shared__ float kn_smem[];
+    float* xs = kn_smem;                   // [MR][ks]
+    float* red = kn_smem + (size_t)MR * ks;  // [kWaves][MR * EPC][64]
+    const int CN = N / EPC;
+    const int t = blockIdx.x, sl = blockIdx.y;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int k0 = sl * ks;
+    const int c = t * 64 + lane;
+    const int cc = min(c, CN - 1);
+    for (int i = threadIdx.x; i < MR * ks; i += kBlock) {
+        const int mr = i / ks, kk = k0 + (i - mr * ks);
+        xs[i] = kk < K ? x[(size_t)mr * K + kk] : 0.f;
+    }
+    __syncthreads();
+    float acc[MR][EPC];
+#pragma unroll
+    for (int mr = 0; mr < MR; mr++)
+#pragma unroll
+        for (int e = 0; e < EPC; e++) acc[mr][e] = 0.f;
+    const uint4* wp = static_cast<const uint4*>(w) + cc;
+    const int rows = ks / kWaves;  // rows of this wave (ks is a multiple of kWaves * kKnUnroll)
+    for (int j0 = 0; j0 < rows; j0 += kKnUnroll) {
+        uint4 wv[kKnUnroll];
+#pragma unroll
+        for (int u = 0; u < kKnUnroll; u++) {
+            const int kk = min(k0 + (j0 + u) * kWaves + wave, K - 1);
+            wv[u] = ld_nt16(wp + (size_t)kk * CN);
+        }
+#pragma unroll
+        for (int u = 0; u < kKnUnroll; u++) {
+            float f[EPC];
+            const uint32_t d[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
+            if constexpr (WT == L0H_F16) {
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const float2 h = __half22float2(__builtin_bit_cast(__half2, d[q]));
+                    f[2 * q] = h.x;
+                    f[2 * q + 1] = h.y;
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; q++) f[q] = __uint_as_float(d[q]);
+            }
+            const int j = (j0 + u) * kWaves + wave;
+#pragma unroll
+            for (int mr = 0; mr < MR; mr++) {
+                const float xv = xs[mr * ks + j];
+#pragma unroll
+                for (int e = 0; e < EPC; e++) acc[mr][e] = fmaf(xv, f[e], acc[mr][e]);
+            }
+        }
+    }
+#pragma unroll
+    for (int mr = 0; mr < MR; mr++)
+#pragma unroll
+        for (int e = 0; e < EPC; e++) red[((size_t)wave * MR * EPC + mr * EPC + e) * 64 + lane] = acc[mr][e];
+    __syncthreads();
+    // Fixed-order sum of the four waves; thread i finishes (row, column) pairs i, i + 256, ...
+    for (int i = threadIdx.x; i < MR * EPC * 64; i += kBlock) {
+        const int l = i & 63, me = i >> 6, mr = me / EPC, e = me - mr * EPC;
+        float v = red[(size_t)me * 64 + l];
+#pragma unroll
+        for (int ww = 1; ww < kWaves; ww++) v += red[((size_t)ww * MR * EPC + me) * 64 + l];
+        const int col = (t * 64 + l) * EPC + e;
+        if (t * 64 + l < CN) out[((size_t)sl * MR + mr) * N + col] = v;
+    }
+}
+
+// y[r, n] = sum over slices s (in order) of part[s, r, n].
+__global__ void kn_slice_sum_kernel(const float* part, float* y, int splits, size_t count) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= count) return;
+    float v = part[i];
+    for (int s = 1; s < splits; s++) v += part[(size_t)s * count + i];
+    y[i] = v;
+}
+
+// Any shape (N not a multiple of the load width, unaligned buffers): each thread owns 4
+// adjacent columns, the 4 waves of a block split K and reduce in LDS.
 template <int WT>
-__global__ __launch_bounds__(kBlock) void gemv_kn_kernel(int rows, int N, int K, const float* x,
-                                                         const void* w, float* y) {
+__global__ __launch_bounds__(kBlock) void gemv_kn_generic_kernel(int N, int K, const float* x, const void* w,
+                                                                 float* y) {
     __shared__ float4 part[kWaves][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int col = (blockIdx.x * 64 + lane) * 4;
@@ -152,19 +249,95 @@ __global__ __launch_bounds__(kBlock) void gemv_kn_kernel(int rows, int N, int K,
             if (col + j < N) yr[col + j] = tv[j];
     }
 }
+
+template <int WT, int MR>
+int launch_kn_tile(hipStream_t s, int n, int k, int ks, int splits, const float* x, const void* w, float* out) {
+    constexpr int EPC = WT == L0H_F16 ? 8 : 4;
+    const unsigned tiles = ceil_div((size_t)(n / EPC), 64);
+    const size_t shmem = ((size_t)MR * ks + (size_t)kWaves * MR * EPC * 64) * sizeof(float);
+    auto kern = gemv_kn_tile_kernel<WT, MR>;
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, kKnLds);
+    if (attr != hipSuccess) return fail(L0H_ERR_DEVICE, std::string("hipFuncSetAttribute: ") + hipGetErrorString(attr));
+    kern<<<dim3(tiles, splits), kBlock, shmem, s>>>(n, k, ks, x, w, out);
+    return launch_status("gemv_kn_tile");
+}
+
+template <int WT>
+int launch_kn_rows(hipStream_t s, int mr, int n, int k, int ks, int splits, const float* x, const void* w, float* out) {
+    switch (mr) {
+    case 1: return launch_kn_tile<WT, 1>(s, n, k, ks, splits, x, w, out);
+    case 2: return launch_kn_tile<WT, 2>(s, n, k, ks, splits, x, w, out);
+    case 4: return launch_kn_tile<WT, 4>(s, n, k, ks, splits, x, w, out);
+    default: return launch_kn_tile<WT, 8>(s, n, k, ks, splits, x, w, out);
+    }
+}
 }  // namespace
 
-int launch_gemv_kn(hipStream_t s, int rows, int n, int k, const float* x, const void* w,
-                   int w_dtype, float* y) {
+KnPlan plan_gemv_kn(int rows, int n, int k, int w_dtype, int compute_units, size_t ws_bytes) {
+    const int epc = w_dtype == L0H_F16 ? 8 : 4;
+    const int tiles = (int)ceil_div((size_t)(n / epc), 64);
+    constexpr int step = kWaves * kKnUnroll;  // rows of a slice come in whole unrolled steps
+    // About two blocks per CU over the column tiles.
+    const int target = (int)ceil_div((size_t)2 * std::max(compute_units, 1), (size_t)std::max(tiles, 1));
+    KnPlan pl;
+    for (int mr = rows >= 8 ? 8 : rows >= 4 ? 4 : rows >= 2 ? 2 : 1;; mr >>= 1) {
+        // The slice's activations and the wave reduction share the block's LDS.
+        const int max_ks = ((kKnLds / 4 - kWaves * mr * epc * 64) / mr) / step * step;
+        const int min_splits = (int)ceil_div((size_t)k, (size_t)max_ks);
+        const size_t per_split = (size_t)mr * n * sizeof(float);
+        const int cap = (int)std::min<size_t>(ws_bytes / per_split, 1 << 20);  // slices the workspace holds
+        if (min_splits > 1 && min_splits > cap && mr > 1) continue;  // fewer rows per launch
+        int splits = std::max(1, std::min(target, (k + step - 1) / step));
+        if (splits > 1 && splits > cap) splits = std::max(1, cap);
+        splits = std::max(splits, min_splits);
+        pl.mr = mr;
+        pl.ks = std::min(max_ks, (int)ceil_div((size_t)ceil_div((size_t)k, (size_t)splits), (size_t)step) * step);
+        pl.splits = (int)ceil_div((size_t)k, (size_t)pl.ks);
+        return pl;
+    }
+}
+
+size_t gemv_kn_workspace_bytes(const KnPlan& pl, int n) {
+    return pl.splits > 1 ? (size_t)pl.splits * pl.mr * n * sizeof(float) : 0;
+}
+
+bool gemv_kn_fast(int n, int w_dtype, const void* w, const float* x) {
+    const int epc = w_dtype == L0H_F16 ? 8 : 4;
+    return n % epc == 0 && ((uintptr_t)w & 15) == 0 && ((uintptr_t)x & 3) == 0;
+}
+
+int launch_gemv_kn(hipStream_t s, int rows, int n, int k, const float* x, const void* w, int w_dtype, float* y,
+                   float* ws, size_t ws_bytes, int compute_units) {
     if (rows <= 0 || n <= 0 || k <= 0) return fail(L0H_ERR_INVALID_ARG, "sizes must be positive");
-    dim3 grid(ceil_div(n, 256), rows);
-    if (w_dtype == L0H_F16)
-        gemv_kn_kernel<L0H_F16><<<grid, kBlock, 0, s>>>(rows, n, k, x, w, y);
-    else if (w_dtype == L0H_F32)
-        gemv_kn_kernel<L0H_F32><<<grid, kBlock, 0, s>>>(rows, n, k, x, w, y);
-    else
-        return fail(L0H_ERR_INVALID_ARG, "Gemv.Execute weights are F32 or F16");
-    return launch_status("gemv_kn");
+    if (w_dtype != L0H_F16 && w_dtype != L0H_F32) return fail(L0H_ERR_INVALID_ARG, "Gemv.Execute weights are F32 or F16");
+    if (!gemv_kn_fast(n, w_dtype, w, x)) {
+        dim3 grid(ceil_div(n, 256), rows);
+        if (w_dtype == L0H_F16)
+            gemv_kn_generic_kernel<L0H_F16><<<grid, kBlock, 0, s>>>(n, k, x, w, y);
+        else
+            gemv_kn_generic_kernel<L0H_F32><<<grid, kBlock, 0, s>>>(n, k, x, w, y);
+        return launch_status("gemv_kn_generic");
+    }
+    for (int done = 0; done < rows;) {
+        // Slices beyond what the workspace holds are merged (or fewer rows run per launch).
+        const KnPlan pl = plan_gemv_kn(rows - done, n, k, w_dtype, compute_units, ws ? ws_bytes : 0);
+        if (gemv_kn_workspace_bytes(pl, n) > (ws ? ws_bytes : 0))
+            return fail(L0H_ERR_INVALID_OP, "the split-reduction workspace cannot hold this [K, N] GEMV's partials");
+        const float* xr = x + (size_t)done * k;
+        float* yr = y + (size_t)done * n;
+        float* out = pl.splits > 1 ? ws : yr;
+        int st = w_dtype == L0H_F16 ? launch_kn_rows<L0H_F16>(s, pl.mr, n, k, pl.ks, pl.splits, xr, w, out)
+                                    : launch_kn_rows<L0H_F32>(s, pl.mr, n, k, pl.ks, pl.splits, xr, w, out);
+        if (st) return st;
+        if (pl.splits > 1) {
+            const size_t count = (size_t)pl.mr * n;
+            kn_slice_sum_kernel<<<ceil_div(count, 256), 256, 0, s>>>(ws, yr, pl.splits, count);
+            if ((st = launch_status("gemv_kn slice sum"))) return st;
+        }
+        done += pl.mr;
+    }
+    return L0H_OK;
 }
 
 }  // namespace l0h

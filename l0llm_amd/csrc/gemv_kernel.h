@@ -21,9 +21,11 @@
 // the first weight item is requested: a CU's memory pipeline returns data in order, so the
 // activations come back ahead of the weight stream and are staged while it is in flight; the
 // staging barriers wait on LDS only, never on the weight loads. Dequantisation
-// happens in registers (int8: bytes biased by +128 and converted with v_cvt_f32_ubyteN, the bias
-// removed after the reduction with sum(x), the per-row scale applied once), accumulation is
-// fp32, and the cross-lane sum uses DPP.
+// happens in registers (int8: bytes biased by +128 and converted with v_cvt_f32_ubyteN; the bias
+// is removed chunk by chunk: the dot product of every 16-byte chunk starts from -128 times the
+// sum of its 16 activations, staged in LDS next to them, so the accumulator only ever holds
+// sum(q * x) and a large activation mean cannot cancel it; the per-row scale is applied once),
+// accumulation is fp32, and the cross-lane sum uses DPP.
 #pragma once
 
 #include <cstdlib>
@@ -35,7 +37,9 @@ namespace {
 
 constexpr int kWaves = 4;
 constexpr int kBlock = 64 * kWaves;
-constexpr size_t kLdsBudget = 64 * 1024;  // activation tile per block
+// Activation tile per block: up to 16384 fp32 values, plus for int8 weights one bias term per
+// 16 values (two blocks per CU still fit the 160 KiB of LDS).
+constexpr size_t kLdsBudget = 72 * 1024;
 constexpr int kMaxRotaryHalf = 128;       // cos/sin table entries per block (rotary_dim <= 256)
 
 template <int CTRL, int ROW_MASK>
@@ -121,7 +125,7 @@ struct WTraits<L0H_F32> {
 };
 
 // acc += dot(chunk, x). For int8 the bytes are biased by +128 and converted with
-// v_cvt_f32_ubyteN; the bias is removed after the reduction using sum(x).
+// v_cvt_f32_ubyteN; the caller starts acc at -128 * sum(x) of the chunk.
 template <int WT>
 __device__ __forceinline__ void chunk_fma(const uint4& w, const float* x, float& acc) {
     const uint32_t d[4] = {w.x, w.y, w.z, w.w};
@@ -273,12 +277,28 @@ __device__ __forceinline__ Side load_side(const GemvParams& p, int group, int la
 // WT weight type, R rows per wave item, U chunks per row per lane in an item, MR activation
 // rows, KX 16-byte activation chunks staged per thread (MR == 1), NORM: RMSNorm prologue,
 // EPI: EPI_STORE (store or residual, chosen at run time), EPI_SWIGLU or EPI_QKV.
+// Sum of v over aligned groups of G lanes (G = 1, 2, 4 or 16), left in every lane of the group.
+template <int G>
+__device__ __forceinline__ float lane_group_sum(float v) {
+    if constexpr (G == 2 || G == 4) v += dpp_src<0xB1, 0xf>(v);  // quad_perm [1,0,3,2]
+    if constexpr (G == 4) v += dpp_src<0x4E, 0xf>(v);            // quad_perm [2,3,0,1]
+    if constexpr (G == 16) {
+        v += dpp_src<0x128, 0xf>(v);  // row_ror:8
+        v += dpp_src<0x124, 0xf>(v);  // row_ror:4
+        v += dpp_src<0x122, 0xf>(v);  // row_ror:2
+        v += dpp_src<0x121, 0xf>(v);  // row_ror:1
+    }
+    return v;
+}
+
 template <int WT, int R, int U, int MR, int KX, bool NORM, int EPI>
 __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p, int k_pad) {
     extern __shared__ float4 smem4[];
     float* xs = reinterpret_cast<float*>(smem4);  // [MR, k_pad], zero past K
+    // int8: [MR, k_pad / 16] bias terms, -128 * (sum of the 16 activations of each weight chunk)
+    float* xc = xs + (size_t)MR * k_pad;
+    const int kc_pad = k_pad / 16;
     __shared__ float red[2 * kWaves];
-    __shared__ float xsum_s[MR];
     __shared__ float rope_cs[EPI == EPI_QKV ? kMaxRotaryHalf : 1];
     __shared__ float rope_sn[EPI == EPI_QKV ? kMaxRotaryHalf : 1];
     constexpr int EPC = WTraits<WT>::kElems;
@@ -309,15 +329,13 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p, int
 #pragma unroll
         for (int mr = 0; mr < MR; mr++) {
             float* dst = xs + (size_t)mr * k_pad;
-            float xsum = 0.f;
-            for (int i = tid; i < k_pad; i += kBlock) {
+            for (int i = tid; i < k_pad; i += kBlock) {  // k_pad is a multiple of kBlock
                 const float v = i < K ? load_act(p.x, p.x_dtype, (size_t)mr * K + i) : 0.f;
                 dst[i] = v;
-                xsum += v;
-            }
-            if constexpr (WT == L0H_I8PC) {
-                xsum = block_sum(xsum, red);
-                if (tid == 0) xsum_s[mr] = xsum;
+                if constexpr (WT == L0H_I8PC) {  // the 16 values of chunk i / 16 sit in one DPP row
+                    const float cs = lane_group_sum<16>(v);
+                    if ((i & 15) == 0) xc[(size_t)mr * kc_pad + (i >> 4)] = -128.0f * cs;
+                }
             }
         }
     }
@@ -355,53 +373,59 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p, int
 
     // ---- stage the one activation row (and RMSNorm) in LDS ----
     if constexpr (MR == 1) {
-        // One pass: sum of squares (RMSNorm) and the sum of the values the dot products will use
-        // (the int8 bias correction), reduced together; then x * scale * w goes to LDS.
-        float ss = 0.f, xw = 0.f;
+        // RMSNorm: the sum of squares of the row (x is fp32 here: 4 values per chunk, matching
+        // the 4 norm weights); then x * scale * w goes to LDS.
+        float scale = 1.f;
+        if constexpr (NORM) {
+            float ss = 0.f;
 #pragma unroll
-        for (int i = 0; i < KX; i++) {
-            float f[8];
-            const int n = chunk_to_float(xr[i], xdt, f);
-            if (i * kBlock + tid < nxc) {
-                if constexpr (NORM) {  // x is fp32 here: 4 values, matching the 4 norm weights
-                    const float nw[4] = {__uint_as_float(nr[i].x), __uint_as_float(nr[i].y), __uint_as_float(nr[i].z),
-                                         __uint_as_float(nr[i].w)};
+            for (int i = 0; i < KX; i++) {
+                float f[8];
+                (void)chunk_to_float(xr[i], xdt, f);
+                if (i * kBlock + tid < nxc) {
 #pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        ss += f[e] * f[e];
-                        xw += f[e] * nw[e];
-                    }
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 8; e++)
-                        if (e < n) xw += f[e];
+                    for (int e = 0; e < 4; e++) ss += f[e] * f[e];
                 }
             }
-        }
-        float scale = 1.f;
-        if constexpr (NORM || WT == L0H_I8PC) {
-            const float2 t = block_sum2(ss, xw, red);
-            if constexpr (NORM) scale = rsqrtf(t.x / (float)K + p.eps);
-            if (tid == 0) xsum_s[0] = scale * t.y;
+            // LDS-only barriers inside: the first weight item stays in flight.
+            scale = rsqrtf(block_sum2(ss, 0.f, red).x / (float)K + p.eps);
         }
 #pragma unroll
         for (int i = 0; i < KX; i++) {
             const int idx = i * kBlock + tid;
+            float f[8];
+            const int n = chunk_to_float(xr[i], xdt, f);
+            if constexpr (NORM) {
+                f[0] *= scale * __uint_as_float(nr[i].x);
+                f[1] *= scale * __uint_as_float(nr[i].y);
+                f[2] *= scale * __uint_as_float(nr[i].z);
+                f[3] *= scale * __uint_as_float(nr[i].w);
+            }
             if (idx < nxc) {
-                float f[8];
-                const int n = chunk_to_float(xr[i], xdt, f);
-                if constexpr (NORM) {
-                    f[0] *= scale * __uint_as_float(nr[i].x);
-                    f[1] *= scale * __uint_as_float(nr[i].y);
-                    f[2] *= scale * __uint_as_float(nr[i].z);
-                    f[3] *= scale * __uint_as_float(nr[i].w);
-                }
 #pragma unroll
                 for (int e = 0; e < 8; e++)
                     if (e < n) xs[idx * n + e] = f[e];
             }
+            if constexpr (WT == L0H_I8PC) {
+                // A weight chunk covers 16 activations: 4 fp32 or 2 16-bit activation chunks, held
+                // by that many adjacent lanes (every lane takes part in the DPP sum).
+                float cs = 0.f;
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                    if (e < n) cs += f[e];
+                cs = idx < nxc ? cs : 0.f;
+                if (xdt == L0H_F32) {
+                    cs = lane_group_sum<4>(cs);
+                    if (idx < nxc && (idx & 3) == 0) xc[idx >> 2] = -128.0f * cs;
+                } else {
+                    cs = lane_group_sum<2>(cs);
+                    if (idx < nxc && (idx & 1) == 0) xc[idx >> 1] = -128.0f * cs;
+                }
+            }
         }
         for (int i = K + tid; i < k_pad; i += kBlock) xs[i] = 0.f;
+        if constexpr (WT == L0H_I8PC)
+            for (int c = K / 16 + tid; c < kc_pad; c += kBlock) xc[c] = 0.f;
     }
     if constexpr (EPI == EPI_QKV) {
         // cos/sin of this position for every rotated pair, once per block (accurate sincos of
@@ -438,8 +462,18 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p, int
                     xv[4 * q + 2] = t.z;
                     xv[4 * q + 3] = t.w;
                 }
+                if constexpr (WT == L0H_I8PC) {
+                    const float corr = xc[(size_t)mr * kc_pad + c];
 #pragma unroll
-                for (int r = 0; r < R; r++) chunk_fma<WT>(w[u][r], xv, acc[mr][r]);
+                    for (int r = 0; r < R; r++) {
+                        float t = corr;
+                        chunk_fma<WT>(w[u][r], xv, t);
+                        acc[mr][r] += t;
+                    }
+                } else {
+#pragma unroll
+                    for (int r = 0; r < R; r++) chunk_fma<WT>(w[u][r], xv, acc[mr][r]);
+                }
             }
         }
     };
@@ -463,7 +497,7 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p, int
                     const int row = r0 + r;
                     if (lane == mr * R + r && row < N) {
                         float v = sums[mr][r];
-                        if constexpr (WT == L0H_I8PC) v = (v - 128.0f * xsum_s[mr]) * half_bits(sd.s0);
+                        if constexpr (WT == L0H_I8PC) v *= half_bits(sd.s0);
                         v += sd.b0;
                         if (p.epilogue == EPI_STORE)
                             store_act(p.y, p.y_dtype, (size_t)mr * N + row, v);
@@ -478,8 +512,8 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p, int
                 if (lane == j && row + 1 < N) {
                     float v0 = sums[0][2 * j], v1 = sums[0][2 * j + 1];
                     if constexpr (WT == L0H_I8PC) {
-                        v0 = (v0 - 128.0f * xsum_s[0]) * half_bits(sd.s0);
-                        v1 = (v1 - 128.0f * xsum_s[0]) * half_bits(sd.s1);
+                        v0 *= half_bits(sd.s0);
+                        v1 *= half_bits(sd.s1);
                     }
                     v0 += sd.b0;
                     v1 += sd.b1;
@@ -552,13 +586,20 @@ int padded_k(int k) {
     return nb * KB * EPC;
 }
 
+// Dynamic LDS of the fast kernel: the activation tile (+ the int8 bias terms, one per 16 values).
+template <int WT>
+size_t tile_bytes(int mr, int k_pad) {
+    const size_t per_row = (size_t)k_pad + (WT == L0H_I8PC ? k_pad / 16 : 0);
+    return (size_t)mr * per_row * sizeof(float);
+}
+
 template <int WT, int R, int U, int MR, int KX, bool NORM, int EPI>
 int launch_fast(hipStream_t s, const GemvParams& p) {
     const int k_pad = padded_k<WT, U>(p.k);
-    const size_t shmem = (size_t)MR * k_pad * sizeof(float);
+    const size_t shmem = tile_bytes<WT>(MR, k_pad);
     if (shmem > kLdsBudget) return fail(L0H_ERR_UNSUPPORTED, "GEMV activation tile exceeds LDS");
     auto kern = gemv_nk_kernel<WT, R, U, MR, KX, NORM, EPI>;
-    // The dynamic tile may reach 64 KiB on top of the static LDS: raise the limit once.
+    // The dynamic tile may reach kLdsBudget on top of the static LDS: raise the limit once.
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsBudget);
     if (attr != hipSuccess) return fail(L0H_ERR_DEVICE, std::string("hipFuncSetAttribute: ") + hipGetErrorString(attr));
@@ -613,7 +654,7 @@ int dispatch_mr(hipStream_t s, const GemvParams& p, int mr) {
         case 4: return dispatch_one<WT, R, U, 4>(s, p);
         case 8: return dispatch_one<WT, R, U, 8>(s, p);
         case 16: return dispatch_one<WT, R, U, 16>(s, p);
-        default: return fail(L0H_ERR_UNSUPPORTED, "GEMV activation row exceeds 64 KiB");
+        default: return fail(L0H_ERR_UNSUPPORTED, "GEMV activation row exceeds the LDS tile");
         }
     }
     if (mr == 2) return launch_fast<WT, R, U, 2, 1, false, EPI_STORE>(s, p);

@@ -82,6 +82,15 @@ void parallel_rows(size_t n, F body) {
     for (auto& th : pool) th.join();
 }
 
+// The fp16 row scale kept finite and non-zero for a non-zero row: a scale that rounds to 0
+// (max|w| below ~3.8e-6) becomes the smallest subnormal 2^-24, one that overflows (max|w| above
+// ~8.3e6) becomes 65504, so q * scale never meets 0 * inf.
+uint16_t clamp_scale_bits(uint16_t sh, float amax) {
+    if ((sh & 0x7fffu) == 0 && amax > 0.f) return 0x0001u;
+    if ((sh & 0x7fffu) >= 0x7c00u) return 0x7bffu;
+    return sh;
+}
+
 // Per-output-channel rule (the role of LlmQ8Quantizer.QuantizeOutIn, LlmMatrix.cs:89-94).
 void quantize_rows(const float* w, int n, int k, int8_t* q, uint16_t* s) {
     parallel_rows((size_t)n, [&](size_t b, size_t e) {
@@ -89,7 +98,7 @@ void quantize_rows(const float* w, int n, int k, int8_t* q, uint16_t* s) {
             const float* row = w + r * (size_t)k;
             float amax = 0.f;
             for (int i = 0; i < k; i++) amax = std::fmax(amax, std::fabs(row[i]));
-            const uint16_t sh = host_f32_to_f16(amax / 127.0f);
+            const uint16_t sh = clamp_scale_bits(host_f32_to_f16(amax / 127.0f), amax);
             const float sc = host_f16_to_f32(sh);
             s[r] = sh;
             int8_t* qr = q + r * (size_t)k;

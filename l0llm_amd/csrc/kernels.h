@@ -53,14 +53,25 @@ struct GemvParams {
 // per_cu blocks of 4 waves per CU. Two is the measured best for the 8B decode shapes: a CU
 // returns data in order, and fewer blocks per CU means fewer blocks whose activation row waits
 // behind a neighbour's weight stream. A launch is further capped at the blocks per CU that its
-// LDS tile allows (two for the 56-64 KiB tiles of a 14336-wide down projection).
+// LDS tile allows (two for the 60-68 KiB tiles of a 14336-wide int8 down projection).
 int gemv_max_blocks(int compute_units, int per_cu = 2);
 
 int launch_gemv_nk(hipStream_t s, const GemvParams& p);
 
-// Reference layout [K, N] GEMV / GEMM (Gemv.Execute, Gemm.Execute).
+// Reference layout [K, N] GEMV / GEMM (Gemv.Execute, Gemm.Execute): rows in groups of up to 8,
+// K split into `splits` slices of `ks` rows whose fp32 partials go to `ws` (the launcher uses
+// fewer slices when `ws_bytes` cannot hold them).
+struct KnPlan {
+    int mr = 1;      // activation rows per launch
+    int ks = 0;      // weight rows per K slice
+    int splits = 1;  // K slices
+};
+// ws_bytes caps the slices (fewer slices, or fewer rows per launch, when it is small).
+KnPlan plan_gemv_kn(int rows, int n, int k, int w_dtype, int compute_units, size_t ws_bytes);
+size_t gemv_kn_workspace_bytes(const KnPlan& plan, int n);
+bool gemv_kn_fast(int n, int w_dtype, const void* w, const float* x);
 int launch_gemv_kn(hipStream_t s, int rows, int n, int k, const float* x, const void* w,
-                   int w_dtype, float* y);
+                   int w_dtype, float* y, float* ws, size_t ws_bytes, int compute_units);
 
 // Element-wise operators.
 int launch_rmsnorm(hipStream_t s, float* x, const float* residual, const float* w, float* out,

@@ -117,10 +117,10 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_rows16_kernel(const float* x, 
     for (int i = threadIdx.x; i < n; i += kBlock) o[i] = cvt(xr[i] * inv * w[i]);
 }
 
-// fp32 activations -> the weight dtype (F16 / BF16) for the MFMA GEMM.
+// fp32 activations -> the weight dtype (F16 / BF16) for the MFMA GEMM (fp16 saturating).
 __global__ void to_16bit_kernel(const float* x, uint16_t* y, size_t n, int dt) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) y[i] = dt == L0H_BF16 ? float_to_bf16_bits(x[i]) : __half_as_ushort(__float2half_rn(x[i]));
+    if (i < n) store_act_sat(y, dt, i, x[i]);
 }
 
 }  // namespace
@@ -133,9 +133,12 @@ struct l0h_model {
     l0h_model_config cfg{};
     int storage = L0H_I8PC;  // projection storage
     int cache_dtype = L0H_F16;
-    // Activations that only feed a projection (attention output -> O, SwiGLU output -> down):
-    // fp16 for int8 / 16-bit weights (half the bytes those GEMVs stage; finer than the
-    // reference's int8 quantization of the same vectors), fp32 for fp32 weights.
+    // Activations that only feed a projection. The attention output (O's input) is a convex
+    // combination of cached V rows, so it cannot leave the cache's range: fp16 next to an fp16
+    // cache (half the bytes O stages), fp32 otherwise. The SwiGLU output (down's input) is
+    // unbounded and stays fp32, as the reference keeps it (an fp16 copy would overflow to inf
+    // above 65504).
+    int attn_dtype = L0H_F32;
     int act_dtype = L0H_F32;
     int max_seq = 0;
     int qd = 0, kvd = 0, rot = 0;
@@ -359,8 +362,8 @@ double op_bytes(const l0h_model* m, int kind, int position) {
     switch (kind) {
     case L0H_KERNEL_EMBEDDING: return 8.0 * H;
     case L0H_KERNEL_QKV: return gemv_bytes(m, m->qd + 2 * m->kvd, c.hidden_size, 8.0 * H + 4.0 * qd + 2.0 * kvd * ci);
-    case L0H_KERNEL_ATTENTION: return 2.0 * (position + 1) * kvd * ci + (4.0 + dtype_size(m->act_dtype)) * qd;
-    case L0H_KERNEL_O_PROJ: return gemv_bytes(m, c.hidden_size, m->qd, dtype_size(m->act_dtype) * qd + 8.0 * H);
+    case L0H_KERNEL_ATTENTION: return 2.0 * (position + 1) * kvd * ci + (4.0 + dtype_size(m->attn_dtype)) * qd;
+    case L0H_KERNEL_O_PROJ: return gemv_bytes(m, c.hidden_size, m->qd, dtype_size(m->attn_dtype) * qd + 8.0 * H);
     case L0H_KERNEL_GATE_UP:
         return gemv_bytes(m, 2 * c.intermediate_size, c.hidden_size, 8.0 * H + dtype_size(m->act_dtype) * I);
     case L0H_KERNEL_DOWN:
@@ -416,7 +419,7 @@ int launch_op(l0h_model* m, hipStream_t s, int kind, int li) {
         a.vc = L.v_cache;
         a.cache_dtype = m->cache_dtype;
         a.out = m->attn;
-        a.out_dtype = m->act_dtype;
+        a.out_dtype = m->attn_dtype;
         a.batch = 1;
         a.head_dim = c.head_dim;
         a.nh = c.num_attention_heads;
@@ -435,7 +438,7 @@ int launch_op(l0h_model* m, hipStream_t s, int kind, int li) {
         g.n = H;
         g.k = m->qd;
         g.x = m->attn;
-        g.x_dtype = m->act_dtype;
+        g.x_dtype = m->attn_dtype;
         g.epilogue = EPI_RESIDUAL;
         g.resid = m->hidden;
         return launch_gemv_nk(s, g);
@@ -763,7 +766,8 @@ int l0h_model_create(l0h_device* dev, const l0h_model_config* cfg, int precision
     m->cfg = c;
     m->storage = storage;
     m->cache_dtype = cache_dtype;
-    m->act_dtype = storage == L0H_F32 ? L0H_F32 : L0H_F16;
+    m->attn_dtype = storage != L0H_F32 && cache_dtype == L0H_F16 ? L0H_F16 : L0H_F32;
+    m->act_dtype = L0H_F32;
     m->max_seq = max_seq_len;
     const char* eager_env = std::getenv("L0H_EAGER_STEP");
     m->eager = eager_env && std::atoi(eager_env) != 0;

@@ -4,25 +4,60 @@
 // codes.
 #include "kernels.h"
 
+#include <algorithm>
 #include <cmath>
+#include <cstdint>
 #include <vector>
 
 namespace l0h {
 
 // Upper bound on activation rows per ExecuteRows call (LlmGemvKernel.MaxRows).
 constexpr int kMaxRows = 8;
+// K granularity of the int8 path (LlmGemvQ8Kernel.GroupSize): Supports asks K % 32 == 0 and the
+// activation scratch rounds its row width up to it (LlmModel.cs:139-144).
+constexpr int kQ8Group = 32;
+
+// Split count for a decode attention call. Inside a recording the workspace cannot grow, so the
+// sequence is split into as many parts as the workspace already holds (l0h_attention_reserve
+// sizes it beforehand for the default count).
+int attention_splits_for(l0h_device* dev, const AttnParams& p0) {
+    AttnParams p = p0;
+    p.splits = attention_default_splits(p.batch, p.nkv, p.max_seq_len, dev->compute_units);
+    if (dev->recording && p.splits > 1 && attention_partials_bytes(p) > dev->workspace_bytes) {
+        AttnParams one = p0;
+        one.splits = 1;
+        p.splits = (int)std::max<size_t>(1, dev->workspace_bytes / std::max<size_t>(1, attention_partials_bytes(one)));
+    }
+    return p.splits;
+}
 
 int attention_run(l0h_device* dev, AttnParams p, bool prefill, int pos0, int tokens) {
     if (prefill) {
         p.batch = tokens;
         if (attention_prefill_tiled(p)) return launch_attention_prefill(dev->stream, p, pos0, tokens);
     }
-    p.splits = attention_default_splits(p.batch, p.nkv, p.max_seq_len, dev->compute_units);
-    const size_t bytes = attention_partials_bytes(p);
-    int st = ensure_workspace(dev, bytes, 0);
-    if (st) return st;
-    p.partials = static_cast<float*>(dev->workspace);
+    p.splits = attention_splits_for(dev, p);
+    if (p.splits > 1) {
+        int st = ensure_workspace(dev, attention_partials_bytes(p), 0);
+        if (st) return st;
+        p.partials = static_cast<float*>(dev->workspace);
+    }
     return prefill ? launch_attention_prefill(dev->stream, p, pos0, tokens) : launch_attention_decode(dev->stream, p);
+}
+
+// Reference-layout GEMV: grows the workspace for the split-K partials when it may (outside a
+// recording); inside one, the launcher uses fewer slices.
+int gemv_kn_run(l0h_device* dev, int rows, int n, int k, const float* x, const void* w, int w_dtype, float* y) {
+    if (!dev->recording && gemv_kn_fast(n, w_dtype, w, x)) {
+        const KnPlan pl = plan_gemv_kn(rows, n, k, w_dtype, dev->compute_units, SIZE_MAX);
+        const size_t need = gemv_kn_workspace_bytes(pl, n);
+        if (need) {
+            int st = ensure_workspace(dev, need, 0);
+            if (st) return st;
+        }
+    }
+    return launch_gemv_kn(dev->stream, rows, n, k, x, w, w_dtype, y, static_cast<float*>(dev->workspace),
+                          dev->workspace_bytes, dev->compute_units);
 }
 
 }  // namespace l0h
@@ -53,19 +88,82 @@ int l0h_gemv_execute_rows(l0h_device* dev, int rows, int out_dim, int in_dim, co
     L0H_ENTER(dev);
     L0H_CHECK_ARG(x && w && y, "null buffer");
     L0H_CHECK_ARG(rows > 0 && out_dim > 0 && in_dim > 0, "sizes must be positive");
-    return launch_gemv_kn(dev->stream, rows, out_dim, in_dim, x, w, w_dtype, y);
+    L0H_CHECK_ARG(w_dtype == L0H_F16 || w_dtype == L0H_F32, "Gemv.Execute weights are F32 or F16");
+    return gemv_kn_run(dev, rows, out_dim, in_dim, x, w, w_dtype, y);
 }
 
 int l0h_gemm_execute(l0h_device* dev, int m, int n, int k, const float* x, const float* w, float* y) {
     L0H_ENTER(dev);
     L0H_CHECK_ARG(x && w && y, "null buffer");
     L0H_CHECK_ARG(m > 0 && n > 0 && k > 0, "sizes must be positive");
-    return launch_gemv_kn(dev->stream, m, n, k, x, w, L0H_F32, y);
+    return gemv_kn_run(dev, m, n, k, x, w, L0H_F32, y);
 }
 
-int l0h_gemv_q8_execute_rows(l0h_device* dev, int rows, int out_dim, int in_dim, const float* x,
+int l0h_gemv_q8_group_size(void) { return kQ8Group; }
+
+int l0h_q8_scratch_ensure(l0h_device* dev, int rows, int cols) {
+    L0H_ENTER(dev);
+    L0H_CHECK_ARG(rows > 0 && cols > 0, "rows and cols must be positive");
+    if (rows <= dev->q8_rows && cols <= dev->q8_cols) return L0H_OK;
+    if (dev->recording)
+        return fail(L0H_ERR_INVALID_OP, "the int8 activation scratch must be sized before recording starts");
+    const int r = std::max(rows, dev->q8_rows), c = std::max(cols, dev->q8_cols);
+    L0H_HIP_TRY(hipStreamSynchronize(dev->stream));
+    drop_recording(dev);  // the kept graph may address the old scratch
+    float* p = nullptr;
+    hipError_t e = hipMalloc(&p, (size_t)r * c * sizeof(float));
+    if (e != hipSuccess)
+        return fail(e == hipErrorOutOfMemory ? L0H_ERR_OUT_OF_MEMORY : L0H_ERR_DEVICE,
+                    std::string("int8 activation scratch: ") + hipGetErrorString(e));
+    if (dev->q8_scratch) (void)hipFree(dev->q8_scratch);
+    dev->q8_scratch = p;
+    dev->q8_rows = r;
+    dev->q8_cols = c;
+    return L0H_OK;
+}
+
+int l0h_q8_scratch(l0h_device* dev, float** scratch, int* row_capacity, int* cols) {
+    L0H_CHECK_ARG(dev && scratch, "null argument");
+    *scratch = dev->q8_scratch;
+    if (row_capacity) *row_capacity = dev->q8_rows;
+    if (cols) *cols = dev->q8_cols;
+    return L0H_OK;
+}
+
+int l0h_gemv_q8_quantize(l0h_device* dev, int rows, int in_dim, const float* x, float* scratch) {
+    L0H_ENTER(dev);
+    L0H_CHECK_ARG(x && scratch, "null buffer");
+    L0H_CHECK_ARG(rows > 0 && in_dim > 0, "sizes must be positive");
+    if (scratch == dev->q8_scratch && (rows > dev->q8_rows || in_dim > dev->q8_cols))
+        return fail(L0H_ERR_INVALID_OP, "activation scratch holds " + std::to_string(dev->q8_rows) + " rows of " +
+                                            std::to_string(dev->q8_cols) + " values; " + std::to_string(rows) +
+                                            " rows of " + std::to_string(in_dim) + " were asked for");
+    return launch_copy(dev->stream, x, scratch, (size_t)rows * in_dim);
+}
+
+int l0h_gemv_q8_execute(l0h_device* dev, int out_dim, int in_dim, const float* scratch, const int8_t* w,
+                        const uint16_t* scales, float* y) {
+    return l0h_gemv_q8_execute_rows(dev, 1, out_dim, in_dim, scratch, w, scales, y);
+}
+
+int l0h_gemv_q8_execute_rows(l0h_device* dev, int rows, int out_dim, int in_dim, const float* scratch,
                              const int8_t* w, const uint16_t* scales, float* y) {
-    return l0h_gemv_nk(dev, L0H_I8PC, rows, out_dim, in_dim, x, L0H_F32, w, scales, y, L0H_F32);
+    return l0h_gemv_nk(dev, L0H_I8PC, rows, out_dim, in_dim, scratch, L0H_F32, w, scales, y, L0H_F32);
+}
+
+int l0h_attention_reserve(l0h_device* dev, int batch, int n_heads, int n_kv_heads, int head_dim, int max_seq_len) {
+    L0H_ENTER(dev);
+    L0H_CHECK_ARG(batch > 0 && n_heads > 0 && n_kv_heads > 0 && head_dim > 0 && max_seq_len > 0,
+                  "sizes must be positive");
+    L0H_CHECK_ARG(n_heads % n_kv_heads == 0, "n_heads must be a multiple of n_kv_heads");
+    AttnParams p;
+    p.batch = batch;
+    p.nh = n_heads;
+    p.nkv = n_kv_heads;
+    p.head_dim = head_dim;
+    p.max_seq_len = max_seq_len;
+    p.splits = attention_default_splits(batch, n_kv_heads, max_seq_len, dev->compute_units);
+    return p.splits > 1 ? ensure_workspace(dev, attention_partials_bytes(p), 0) : L0H_OK;
 }
 
 int l0h_rmsnorm_execute(l0h_device* dev, float* x, const float* residual, const float* w, float* out,

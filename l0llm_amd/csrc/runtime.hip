@@ -13,16 +13,6 @@
 
 namespace l0h {
 
-static thread_local std::string g_last_error;
-
-void set_error(const std::string& msg) { g_last_error = msg; }
-void clear_error() { g_last_error.clear(); }
-
-int fail(int code, const std::string& msg) {
-    set_error(msg);
-    return code;
-}
-
 int launch_status(const char* what) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(L0H_ERR_DEVICE, std::string(what) + ": " + hipGetErrorString(e));
@@ -60,12 +50,20 @@ static int zero_fill(hipStream_t s, void* p, size_t bytes) {
     return launch_status("zero fill");
 }
 
+void drop_recording(l0h_device* dev) {
+    if (!dev->cached_exec) return;
+    (void)hipGraphExecDestroy(dev->cached_exec);
+    dev->cached_exec = nullptr;
+    dev->recording_dropped = true;
+}
+
 int ensure_workspace(l0h_device* dev, size_t bytes, size_t tickets) {
     if (bytes > dev->workspace_bytes) {
         if (dev->recording)
             return fail(L0H_ERR_INVALID_OP,
                         "split-reduction workspace must be sized before recording starts");
         L0H_HIP_TRY(hipStreamSynchronize(dev->stream));
+        drop_recording(dev);  // the kept graph may address the old workspace
         if (dev->workspace) L0H_HIP_TRY(hipFree(dev->workspace));
         dev->workspace = nullptr;
         dev->workspace_bytes = 0;
@@ -77,6 +75,7 @@ int ensure_workspace(l0h_device* dev, size_t bytes, size_t tickets) {
         if (dev->recording)
             return fail(L0H_ERR_INVALID_OP, "completion counters must be sized before recording starts");
         L0H_HIP_TRY(hipStreamSynchronize(dev->stream));
+        drop_recording(dev);
         if (dev->tickets) L0H_HIP_TRY(hipFree(dev->tickets));
         dev->tickets = nullptr;
         dev->ticket_count = 0;
@@ -164,6 +163,7 @@ int l0h_device_close(l0h_device* dev) {
     if (dev->cached_exec) (void)hipGraphExecDestroy(dev->cached_exec);
     if (dev->workspace) (void)hipFree(dev->workspace);
     if (dev->tickets) (void)hipFree(dev->tickets);
+    if (dev->q8_scratch) (void)hipFree(dev->q8_scratch);
     if (dev->stream) (void)hipStreamDestroy(dev->stream);
     if (dev->upload) (void)hipStreamDestroy(dev->upload);
     delete dev;
@@ -204,6 +204,7 @@ int l0h_free(l0h_device* dev, void* ptr) {
     if (st) return st;
     if (dev->recording) return fail(L0H_ERR_INVALID_OP, "cannot free while recording");
     L0H_HIP_TRY(hipStreamSynchronize(dev->stream));
+    drop_recording(dev);  // the kept graph may address this buffer
     L0H_HIP_TRY(hipFree(ptr));
     return L0H_OK;
 }
@@ -283,6 +284,7 @@ int l0h_end_recording(l0h_device* dev) {
             return fail(L0H_ERR_DEVICE, std::string("hipGraphInstantiate: ") + hipGetErrorString(e));
         }
     }
+    dev->recording_dropped = false;
     hipError_t e = hipGraphLaunch(dev->cached_exec, dev->stream);
     (void)hipGraphDestroy(graph);
     if (e != hipSuccess) return fail(L0H_ERR_DEVICE, std::string("hipGraphLaunch: ") + hipGetErrorString(e));
@@ -295,7 +297,10 @@ int l0h_replay_recording(l0h_device* dev, int count, float* ms_per_replay) {
     if (st) return st;
     L0H_CHECK_ARG(count > 0 && ms_per_replay, "count must be positive and ms_per_replay non-null");
     if (dev->recording) return fail(L0H_ERR_INVALID_OP, "the device is recording");
-    if (!dev->cached_exec) return fail(L0H_ERR_INVALID_OP, "nothing has been recorded");
+    if (!dev->cached_exec)
+        return fail(L0H_ERR_INVALID_OP, dev->recording_dropped
+                                            ? "memory used by the last recording was freed or moved since; record again"
+                                            : "nothing has been recorded");
     hipEvent_t a = nullptr, b = nullptr;
     L0H_HIP_TRY(hipEventCreate(&a));
     hipError_t e = hipEventCreate(&b);
@@ -339,7 +344,5 @@ int l0h_synchronize(l0h_device* dev) {
     L0H_HIP_TRY(hipStreamSynchronize(dev->stream));
     return L0H_OK;
 }
-
-const char* l0h_last_error(void) { return g_last_error.c_str(); }
 
 }  // extern "C"

@@ -3,9 +3,10 @@
 //
 // A file is an 8-byte little-endian header length, a JSON header mapping tensor names to
 // {dtype, shape, data_offsets} (plus an optional "__metadata__" object), then the data section.
-// Opening validates the header the way the reference does: the declared length fits the file and
+// Opening validates the header against the format: the announced length fits the file and
 // 100 MB, every entry has a known dtype, a non-negative shape whose byte size matches its
-// data_offsets, offsets inside the data section, no name twice and no two tensors overlapping.
+// data_offsets, offsets inside the data section, no name twice and no two tensors sharing bytes
+// (the checks SafetensorsReader.Open makes; the validator here is organised its own way).
 // Tensors are read with pread in 1 MiB chunks and converted to fp32 (F32, F16, BF16, F64 sources).
 // A directory opens model.safetensors.index.json (its weight_map names the shard of every
 // tensor; shards and index must agree) or else model.safetensors.
@@ -287,8 +288,61 @@ struct File {
     }
 };
 
-int bad(const std::string& path, const std::string& what) { return fail(L0H_ERR_INVALID_DATA, "'" + path + "' " + what); }
+int bad(const std::string& path, const std::string& what) { return fail(L0H_ERR_INVALID_DATA, "'" + path + "': " + what); }
 
+const char* kind_name(Json::Kind k) {
+    static const char* const names[] = {"null", "boolean", "number", "string", "array", "object"};
+    return names[k];
+}
+
+bool is_count(const Json& j) { return j.kind == Json::Number && j.integral && j.ival >= 0; }
+
+// Checks one header entry against the format: {"dtype": one of the 13 type names, "shape": a list
+// of non-negative integers, "data_offsets": [begin, end] inside the data section with end - begin
+// equal to the element count times the element size}. Returns "" and fills t, or what is wrong.
+// A dtype the format does not define sets *unknown_dtype instead.
+std::string check_entry(const std::string& name, const Json& e, long long data_len, TensorInfo& t,
+                        std::string* unknown_dtype) {
+    if (e.kind != Json::Object) return std::string("entry is a ") + kind_name(e.kind) + ", not an object";
+    const Json* dt = member(e, "dtype");
+    const Json* sh = member(e, "shape");
+    const Json* off = member(e, "data_offsets");
+    if (!dt || dt->kind != Json::String) return "\"dtype\" is missing or not a string";
+    if (!sh || sh->kind != Json::Array) return "\"shape\" is missing or not a list";
+    if (!off || off->kind != Json::Array || off->items.size() != 2 || !is_count(off->items[0]) ||
+        !is_count(off->items[1]))
+        return "\"data_offsets\" is not a pair of non-negative integers";
+    t.name = name;
+    t.dtype = -1;
+    for (int i = 0; i < (int)(sizeof kDtypeSizes / sizeof kDtypeSizes[0]); i++)
+        if (dt->str == kDtypeNames[i]) t.dtype = i;
+    if (t.dtype < 0) {
+        *unknown_dtype = dt->str;
+        return "";
+    }
+    t.count = 1;
+    for (const Json& d : sh->items) {
+        if (!is_count(d)) return "a dimension of \"shape\" is not a non-negative integer";
+        if (d.ival != 0 && t.count > INT64_MAX / d.ival) return "the element count does not fit 64 bits";
+        t.count *= d.ival;
+        t.shape.push_back(d.ival);
+    }
+    const long long begin = off->items[0].ival, end = off->items[1].ival;
+    if (end < begin || end > data_len)
+        return "bytes " + std::to_string(begin) + ".." + std::to_string(end) + " are not within the " +
+               std::to_string(data_len) + "-byte data section";
+    const int es = kDtypeSizes[t.dtype];
+    if (t.count > INT64_MAX / es) return "the byte size does not fit 64 bits";
+    if (end - begin != t.count * es)
+        return std::to_string(t.count) + " x " + kDtypeNames[t.dtype] + " needs " + std::to_string(t.count * es) +
+               " bytes; data_offsets give " + std::to_string(end - begin);
+    t.offset = begin;
+    t.bytes = end - begin;
+    return "";
+}
+
+// Reads the 8-byte length prefix and the JSON header, then every entry; the data extents of the
+// tensors must be pairwise disjoint (checked by one sweep in offset order).
 int open_file(const std::string& path, std::unique_ptr<File>& out) {
     auto f = std::make_unique<File>();
     f->path = path;
@@ -297,70 +351,50 @@ int open_file(const std::string& path, std::unique_ptr<File>& out) {
     struct stat sb;
     if (::fstat(f->fd, &sb) != 0) return fail(L0H_ERR_INVALID_ARG, "cannot stat '" + path + "'");
     const long long size = (long long)sb.st_size;
-    if (size < 8) return bad(path, "is too small to be a safetensors file (" + std::to_string(size) + " bytes)");
-    unsigned char lb[8];
-    if (::pread(f->fd, lb, 8, 0) != 8) return bad(path, "cannot be read");
-    uint64_t declared = 0;
-    for (int i = 7; i >= 0; i--) declared = (declared << 8) | lb[i];
-    if (declared > (uint64_t)kMaxHeaderBytes || (long long)declared > size - 8)
-        return bad(path, "declares a header of " + std::to_string(declared) + " bytes, which does not fit the " +
-                             std::to_string(size) + "-byte file");
-    std::string header((size_t)declared, '\0');
-    if (declared && ::pread(f->fd, &header[0], (size_t)declared, 8) != (ssize_t)declared) return bad(path, "cannot be read");
-    f->data_start = 8 + (long long)declared;
+    if (size < 8) return bad(path, std::to_string(size) + " bytes is shorter than the 8-byte length prefix");
+    unsigned char prefix[8];
+    if (::pread(f->fd, prefix, 8, 0) != 8) return bad(path, "read error in the length prefix");
+    uint64_t hlen = 0;
+    for (int i = 7; i >= 0; i--) hlen = (hlen << 8) | prefix[i];  // little-endian u64
+    if (hlen > (uint64_t)kMaxHeaderBytes)
+        return bad(path, "the length prefix announces " + std::to_string(hlen) + " header bytes (limit " +
+                             std::to_string(kMaxHeaderBytes) + ")");
+    if ((long long)hlen > size - 8)
+        return bad(path, "the length prefix announces " + std::to_string(hlen) + " header bytes; only " +
+                             std::to_string(size - 8) + " follow it");
+    std::string header((size_t)hlen, '\0');
+    if (hlen && ::pread(f->fd, &header[0], (size_t)hlen, 8) != (ssize_t)hlen) return bad(path, "read error in the header");
+    f->data_start = 8 + (long long)hlen;
     const long long data_len = size - f->data_start;
 
     Json root;
     std::string jerr;
-    if (!JsonParser(header.data(), header.size()).parse(root, jerr)) return bad(path, "has an invalid safetensors header: " + jerr);
-    if (root.kind != Json::Object) return bad(path, "header is not a JSON object");
+    if (!JsonParser(header.data(), header.size()).parse(root, jerr)) return bad(path, "header JSON: " + jerr);
+    if (root.kind != Json::Object) return bad(path, std::string("the header is a JSON ") + kind_name(root.kind) + ", not an object");
     for (const auto& kv : root.members) {
-        const std::string& name = kv.first;
-        const Json& e = kv.second;
-        if (name == "__metadata__") continue;
-        if (e.kind != Json::Object) return bad(path, ": tensor '" + name + "' entry is not an object");
-        const Json* dt = member(e, "dtype");
-        if (!dt || dt->kind != Json::String) return bad(path, ": tensor '" + name + "' has no dtype");
+        if (kv.first == "__metadata__") continue;
         TensorInfo t;
-        t.name = name;
-        t.dtype = -1;
-        for (int i = 0; i < 13; i++)
-            if (dt->str == kDtypeNames[i]) t.dtype = i;
-        if (t.dtype < 0) return fail(L0H_ERR_UNSUPPORTED, "Tensor '" + name + "' uses unsupported dtype '" + dt->str + "'");
-        const Json* sh = member(e, "shape");
-        if (!sh || sh->kind != Json::Array) return bad(path, ": tensor '" + name + "' has no shape");
-        for (const Json& d : sh->items) {
-            if (d.kind != Json::Number || !d.integral || d.ival < 0)
-                return bad(path, ": tensor '" + name + "' has an invalid dimension");
-            if (d.ival && t.count > (long long)(INT64_MAX / d.ival)) return bad(path, ": tensor '" + name + "' shape overflows");
-            t.count *= d.ival;
-            t.shape.push_back(d.ival);
-        }
-        const Json* off = member(e, "data_offsets");
-        if (!off || off->kind != Json::Array || off->items.size() != 2 || off->items[0].kind != Json::Number ||
-            off->items[1].kind != Json::Number || !off->items[0].integral || !off->items[1].integral)
-            return bad(path, ": tensor '" + name + "' has invalid data_offsets");
-        const long long b = off->items[0].ival, en = off->items[1].ival;
-        if (b < 0 || en < b || en > data_len)
-            return bad(path, ": tensor '" + name + "' data_offsets [" + std::to_string(b) + ", " + std::to_string(en) +
-                                 "] fall outside the " + std::to_string(data_len) + "-byte data section");
-        const int es = kDtypeSizes[t.dtype];
-        if (t.count > INT64_MAX / es) return bad(path, ": tensor '" + name + "' size overflows");
-        if (en - b != t.count * es)
-            return bad(path, ": tensor '" + name + "' spans " + std::to_string(en - b) + " bytes but its shape needs " +
-                                 std::to_string(t.count * es));
-        t.offset = b;
-        t.bytes = en - b;
-        if (!f->tensors.emplace(name, std::move(t)).second) return bad(path, "lists tensor '" + name + "' more than once");
+        std::string unknown;
+        const std::string problem = check_entry(kv.first, kv.second, data_len, t, &unknown);
+        if (!problem.empty()) return bad(path, "tensor '" + kv.first + "': " + problem);
+        if (!unknown.empty())
+            return fail(L0H_ERR_UNSUPPORTED, "'" + path + "': tensor '" + kv.first + "' has element type '" + unknown +
+                                                 "', which safetensors does not define");
+        if (!f->tensors.emplace(kv.first, std::move(t)).second)
+            return bad(path, "the header declares '" + kv.first + "' twice");
     }
-    // No two tensors with data may overlap (SafetensorsReader.EnsureNoOverlap).
-    std::vector<const TensorInfo*> order;
+    std::vector<const TensorInfo*> by_offset;
     for (const auto& kv : f->tensors)
-        if (kv.second.bytes > 0) order.push_back(&kv.second);
-    std::sort(order.begin(), order.end(), [](const TensorInfo* a, const TensorInfo* b) { return a->offset < b->offset; });
-    for (size_t i = 1; i < order.size(); i++)
-        if (order[i]->offset < order[i - 1]->offset + order[i - 1]->bytes)
-            return bad(path, ": tensors '" + order[i - 1]->name + "' and '" + order[i]->name + "' overlap");
+        if (kv.second.bytes > 0) by_offset.push_back(&kv.second);
+    std::sort(by_offset.begin(), by_offset.end(), [](const TensorInfo* x, const TensorInfo* y) { return x->offset < y->offset; });
+    long long covered = 0;  // end of the extents seen so far
+    const TensorInfo* last = nullptr;
+    for (const TensorInfo* t : by_offset) {
+        if (last && t->offset < covered)
+            return bad(path, "the data of '" + last->name + "' and '" + t->name + "' share bytes");
+        covered = t->offset + t->bytes;
+        last = t;
+    }
     out = std::move(f);
     return L0H_OK;
 }
@@ -425,13 +459,13 @@ int l0h_safetensors_open(const char* path, l0h_safetensors** out) {
             Json root;
             std::string jerr;
             if (!JsonParser(text.data(), text.size()).parse(root, jerr) || root.kind != Json::Object)
-                return fail(L0H_ERR_INVALID_DATA, "'" + index + "' is not valid JSON");
+                return fail(L0H_ERR_INVALID_DATA, "'" + index + "': not a JSON object");
             const Json* wm = member(root, "weight_map");
-            if (!wm || wm->kind != Json::Object) return fail(L0H_ERR_INVALID_DATA, "'" + index + "' has no weight_map object");
+            if (!wm || wm->kind != Json::Object) return fail(L0H_ERR_INVALID_DATA, "'" + index + "': \"weight_map\" is missing or not an object");
             for (const auto& kv : wm->members) {
                 const std::string& f = kv.second.str;
                 if (kv.second.kind != Json::String || f.empty() || f.find('/') != std::string::npos || f == "." || f == "..")
-                    return fail(L0H_ERR_INVALID_DATA, "'" + index + "' maps '" + kv.first + "' to an invalid file name");
+                    return fail(L0H_ERR_INVALID_DATA, "'" + index + "': the shard of '" + kv.first + "' must be a file name in the same directory");
                 weight_map[kv.first] = f;
                 if (std::find(files.begin(), files.end(), f) == files.end()) files.push_back(f);
             }
@@ -439,7 +473,7 @@ int l0h_safetensors_open(const char* path, l0h_safetensors** out) {
         } else if (is_file(p + "/model.safetensors")) {
             files.push_back(p + "/model.safetensors");
         } else {
-            return fail(L0H_ERR_INVALID_ARG, "'" + p + "' holds neither model.safetensors.index.json nor model.safetensors");
+            return fail(L0H_ERR_INVALID_ARG, "'" + p + "': no model.safetensors.index.json and no model.safetensors inside");
         }
     } else {
         files.push_back(p);
@@ -451,14 +485,14 @@ int l0h_safetensors_open(const char* path, l0h_safetensors** out) {
         if (st) return st;
         for (const auto& kv : f->tensors)
             if (!owner.emplace(kv.first, f.get()).second)
-                return fail(L0H_ERR_INVALID_DATA, "tensor '" + kv.first + "' appears in two shards");
+                return fail(L0H_ERR_INVALID_DATA, "'" + kv.first + "' is stored in more than one shard");
         ck->files.push_back(std::move(f));
     }
     // The index and the shards must agree: every mapped tensor is in the shard it names.
     for (const auto& kv : weight_map) {
         auto it = owner.find(kv.first);
         if (it == owner.end() || it->second->path != p + "/" + kv.second)
-            return fail(L0H_ERR_INVALID_DATA, "the index maps '" + kv.first + "' to '" + kv.second + "', which does not hold it");
+            return fail(L0H_ERR_INVALID_DATA, "the index places '" + kv.first + "' in '" + kv.second + "', but that shard does not contain it");
     }
     for (const auto& kv : owner) ck->names.emplace_back(kv.first, kv.second);  // std::map: sorted
     *out = ck.release();
@@ -511,13 +545,13 @@ int l0h_safetensors_read_f32(const l0h_safetensors* st, const char* name, float*
     L0H_CHECK_ARG(st && name && dst, "null argument");
     const File* f = nullptr;
     const TensorInfo* t = st->find(name, &f);
-    if (!t) return fail(L0H_ERR_INVALID_ARG, std::string("Tensor '") + name + "' is not in the checkpoint");
+    if (!t) return fail(L0H_ERR_INVALID_ARG, std::string("no tensor named '") + name + "'");
     if ((long long)count != t->count)
-        return fail(L0H_ERR_INVALID_ARG, "Tensor '" + t->name + "' has " + std::to_string(t->count) +
-                                             " elements but the destination holds " + std::to_string(count));
+        return fail(L0H_ERR_INVALID_ARG, "'" + t->name + "' holds " + std::to_string(t->count) +
+                                             " values; the destination was sized for " + std::to_string(count));
     if (t->dtype != kDtypeF32 && t->dtype != kDtypeF16 && t->dtype != kDtypeBF16 && t->dtype != kDtypeF64)
-        return fail(L0H_ERR_UNSUPPORTED, "Tensor '" + t->name + "' is " + kDtypeNames[t->dtype] +
-                                             "; ReadFloat32 supports F32, F16, BF16 and F64");
+        return fail(L0H_ERR_UNSUPPORTED, "'" + t->name + "' is stored as " + kDtypeNames[t->dtype] +
+                                             ": only F32, F16, BF16 and F64 convert to fp32");
     const int es = kDtypeSizes[t->dtype];
     const size_t per = kChunkBytes / es;
     std::vector<unsigned char> buf(kChunkBytes);
@@ -527,7 +561,7 @@ int l0h_safetensors_read_f32(const l0h_safetensors* st, const char* name, float*
         size_t got = 0;
         while (got < bytes) {
             const ssize_t r = ::pread(f->fd, buf.data() + got, bytes - got, at + (off_t)got);
-            if (r <= 0) return fail(L0H_ERR_INVALID_DATA, "cannot read tensor '" + t->name + "' from '" + f->path + "'");
+            if (r <= 0) return fail(L0H_ERR_INVALID_DATA, "'" + f->path + "': read error in the data of '" + t->name + "'");
             got += (size_t)r;
         }
         float* d = dst + done;

@@ -119,6 +119,9 @@ void orc_quantize_i8pc(const float* w, int N, int K, int8_t* q, uint16_t* s16) {
             if (a > amax) amax = a;
         }
         uint16_t sh = orc_f32_to_f16(amax / 127.0f);
+        /* a non-zero row keeps a finite, non-zero scale: 2^-24 at least, 65504 at most */
+        if ((sh & 0x7fffu) == 0 && amax > 0.0f) sh = 0x0001u;
+        if ((sh & 0x7fffu) >= 0x7c00u) sh = 0x7bffu;
         float s = orc_f16_to_f32(sh);
         s16[n] = sh;
         for (int k = 0; k < K; k++) {
@@ -371,8 +374,10 @@ static void attend_one(const float* q, const void* kc, const void* vc, int dtype
     int group = nh / nkv;
     int kv_dim = nkv * head_dim;
     double scale = 1.0 / sqrt((double)head_dim);
-    double* p = (double*)malloc(sizeof(double) * (size_t)(len > 0 ? len : 1));
+    /* heads are independent: one per thread (the arithmetic of a head does not depend on it) */
+#pragma omp parallel for schedule(static) if (len >= 1024)
     for (int h = 0; h < nh; h++) {
+        double* p = (double*)malloc(sizeof(double) * (size_t)(len > 0 ? len : 1));
         int g = h / group;
         const float* qh = q + (size_t)h * head_dim;
         double mx = -INFINITY;
@@ -394,8 +399,8 @@ static void attend_one(const float* q, const void* kc, const void* vc, int dtype
                 acc += p[t] * (double)cache_at(dtype, vc, (size_t)t * kv_dim + (size_t)g * head_dim + d);
             out[(size_t)h * head_dim + d] = (float)(acc / sum);
         }
+        free(p);
     }
-    free(p);
 }
 
 /* Attention.Execute (LlmDecoderLayer.cs:325-327). */

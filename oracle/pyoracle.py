@@ -310,6 +310,15 @@ class Model:
                          mat("lm_head.weight"), ctypes.cast(layers, ctypes.POINTER(_Layer)), keep(f32(inv_freq)),
                          cache_dtype, max_seq_len, ctypes.cast(kp, ctypes.POINTER(P)), ctypes.cast(vp, ctypes.POINTER(P)))
 
+    def load_cache(self, layer: int, k_bytes: np.ndarray, v_bytes: np.ndarray) -> None:
+        """Seeds layer `layer`'s K and V caches with raw cache bytes ([max_seq_len, kv_dim] of the
+        cache dtype; a shorter prefix fills the first slots)."""
+        for dst, src in ((self.k_caches[layer], k_bytes), (self.v_caches[layer], v_bytes)):
+            b = np.ascontiguousarray(src).view(np.uint8).reshape(-1)
+            if b.size > dst.size:
+                raise ValueError("cache bytes exceed the oracle's cache")
+            dst[: b.size] = b
+
     def step(self, token: int, position: int) -> tuple[int, np.ndarray]:
         logits = np.empty(self.vocab, dtype=np.float32)
         nxt = _lib.orc_model_step(ctypes.byref(self._m), token, position, _p(logits))

@@ -47,6 +47,33 @@ def test_quantizer_matches_oracle_bitwise():
     np.testing.assert_array_equal(s.view(np.uint16), os_)
 
 
+def test_quantizer_scale_stays_finite_and_nonzero():
+    """Rows whose max|w| / 127 rounds to 0 in fp16 keep the smallest subnormal scale 2^-24, rows whose
+    scale would overflow keep 65504, all-zero rows keep 0; library and oracle agree bit for bit, and
+    every non-zero row dequantizes to finite values with |q * s - w| bounded."""
+    rng = np.random.default_rng(21)
+    w = rng.normal(0, 1, (6, 64)).astype(np.float32)
+    w[0] *= 1e-8          # max|w| / 127 below half the smallest subnormal
+    w[1] *= 1e-6          # subnormal scale
+    w[2] *= 1e7           # max|w| / 127 above 65504
+    w[3] = 0.0            # all-zero row
+    w[4, :] = 0.0
+    w[4, 5] = 3e-7        # one tiny value
+    q, s = l0.quantize_i8pc(w)
+    oq, os_ = orc.quantize_i8pc(w)
+    np.testing.assert_array_equal(q, oq)
+    np.testing.assert_array_equal(s.view(np.uint16), os_)
+    bits = s.view(np.uint16)
+    assert bits[0] == 0x0001 and bits[4] == 0x0001  # 2^-24
+    assert bits[2] == 0x7BFF                        # 65504
+    assert bits[3] == 0 and not q[3].any()
+    deq = q.astype(np.float64) * s.astype(np.float64)[:, None]
+    assert np.all(np.isfinite(deq))
+    for r in (1, 5):  # normal and subnormal scales: rounding error at most half a step
+        assert np.max(np.abs(deq[r] - w[r])) <= 0.5 * float(s[r]) * 1.0001
+    assert np.all(np.abs(q) <= 127)
+
+
 def test_rope_frequencies_match_oracle_and_golden():
     import json
     cases = json.loads((GOLDEN / "rope.golden.json").read_text())["cases"]
