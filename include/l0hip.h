@@ -233,6 +233,17 @@ int l0h_attention_decode(l0h_device* dev, const void* q, int q_dtype, const void
                          const void* v_cache, int cache_dtype, void* out, int out_dtype, int batch,
                          int head_dim, int n_heads, int n_kv_heads, int seq_len, int max_seq_len);
 
+/* l0h_attention_decode without any allocation: no counterpart in the reference. For callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving loops, hosts that
+ * forbid hipMalloc). Same arguments, kernels and split count as l0h_attention_decode outside a
+ * recording; the split partials live in a 4 MiB static device array that each GPU holds until the
+ * process ends. L0H_ERR_INVALID_ARG when a shape needs more partials than that (only batch x
+ * n_kv_heads in the hundreds with 8 q heads per kv head come close). Calls that overlap on one GPU
+ * (other streams, other threads) share the array and race. */
+int l0h_attention_decode_noalloc(l0h_device* dev, const void* q, int q_dtype, const void* k_cache,
+                                 const void* v_cache, int cache_dtype, void* out, int out_dtype, int batch,
+                                 int head_dim, int n_heads, int n_kv_heads, int seq_len, int max_seq_len);
+
 /* ======================================================================
  * Host-side helpers (CPU, no device needed)
  * ==================================================================== */

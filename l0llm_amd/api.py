@@ -268,6 +268,13 @@ class LlmKernelSuite:
         """x fp16 [m, k], w int8 [n, k], scales fp16 [n]."""
         check(lib.l0h_gemm_nk_i8pc(self.device.handle, m, n, k, _ptr(x), _ptr(w), _ptr(scales), _ptr(y), y_dtype))
 
+    def attention_decode_noalloc(self, q, q_dtype, k_cache, v_cache, cache_dtype, out, out_dtype, batch, head_dim,
+                                 n_heads, n_kv, seq_len, max_seq_len):
+        """attention_decode with its split partials in the library's static scratch (no allocation)."""
+        check(lib.l0h_attention_decode_noalloc(self.device.handle, _ptr(q), q_dtype, _ptr(k_cache), _ptr(v_cache),
+                                               cache_dtype, _ptr(out), out_dtype, batch, head_dim, n_heads, n_kv,
+                                               seq_len, max_seq_len))
+
     def attention_decode(self, q, q_dtype, k_cache, v_cache, cache_dtype, out, out_dtype, batch, head_dim, n_heads,
                          n_kv, seq_len, max_seq_len):
         check(lib.l0h_attention_decode(self.device.handle, _ptr(q), q_dtype, _ptr(k_cache), _ptr(v_cache),

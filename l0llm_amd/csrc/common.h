@@ -63,6 +63,9 @@ struct l0h_device {
     // q8_rows x q8_cols fp32, grown by l0h_q8_scratch_ensure outside recording.
     float* q8_scratch = nullptr;
     int q8_rows = 0, q8_cols = 0;
+    // This device's address of the static scratch array of l0h_attention_decode_noalloc, looked
+    // up once when the device is opened (host code never uses the array's own name).
+    float* static_scratch = nullptr;
     std::mutex mu;
 };
 
@@ -73,6 +76,9 @@ int use_device(l0h_device* dev);
 // Makes sure the workspace holds `bytes` and `tickets` counters. Fails while recording
 // if growth would be needed.
 int ensure_workspace(l0h_device* dev, size_t bytes, size_t tickets);
+// Looks up this device's address of the allocation-free attention scratch (ops.hip); the device
+// must be current.
+int static_scratch_init(l0h_device* dev);
 // Drops the kept executable graph of the last recording (it may address memory that is about
 // to be freed or moved); l0h_replay_recording refuses until the next recording.
 void drop_recording(l0h_device* dev);

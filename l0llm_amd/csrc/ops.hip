@@ -17,6 +17,21 @@ constexpr int kMaxRows = 8;
 // activation scratch rounds its row width up to it (LlmModel.cs:139-144).
 constexpr int kQ8Group = 32;
 
+// Split partials of l0h_attention_decode_noalloc: a file-scope device array, so that entry point
+// allocates nothing. Every GPU the library runs on holds one copy (4 MiB) until the process ends;
+// host code reaches it only through the address static_scratch_init looks up per device.
+constexpr size_t kStaticScratchBytes = 4u << 20;
+static __device__ __align__(256) float scratch[kStaticScratchBytes / sizeof(float)];
+
+int static_scratch_init(l0h_device* dev) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+        return fail(L0H_ERR_DEVICE, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+    dev->static_scratch = static_cast<float*>(ptr);
+    return L0H_OK;
+}
+
 // Split count for a decode attention call. Inside a recording the workspace cannot grow, so the
 // sequence is split into as many parts as the workspace already holds (l0h_attention_reserve
 // sizes it beforehand for the default count).
@@ -358,6 +373,43 @@ int l0h_gemm_nk_i8pc(l0h_device* dev, int m, int n, int k, const void* x, const 
     }
     return launch_gemm_nk(dev->stream, L0H_I8PC, m, n, k, x, w, y, y_dtype, static_cast<float*>(dev->workspace),
                           dev->workspace_bytes, dev->compute_units, scales);
+}
+
+int l0h_attention_decode_noalloc(l0h_device* dev, const void* q, int q_dtype, const void* k_cache,
+                                 const void* v_cache, int cache_dtype, void* out, int out_dtype, int batch,
+                                 int head_dim, int n_heads, int n_kv_heads, int seq_len, int max_seq_len) {
+    L0H_ENTER(dev);
+    L0H_CHECK_ARG(q && k_cache && v_cache && out, "null buffer");
+    L0H_CHECK_ARG(batch > 0 && seq_len > 0 && seq_len <= max_seq_len, "bad batch or sequence length");
+    L0H_CHECK_ARG(q_dtype == L0H_F32 || q_dtype == L0H_F16, "q is F32 or F16");
+    L0H_CHECK_ARG(n_kv_heads > 0 && n_heads > 0 && head_dim > 0, "head counts and head_dim must be positive");
+    if (!dev->static_scratch) return fail(L0H_ERR_INVALID_OP, "the device has no static attention scratch");
+    AttnParams p;
+    p.q = q;
+    p.q_dtype = q_dtype;
+    p.kc = k_cache;
+    p.vc = v_cache;
+    p.cache_dtype = cache_dtype;
+    p.out = out;
+    p.out_dtype = out_dtype;
+    p.batch = batch;
+    p.head_dim = head_dim;
+    p.nh = n_heads;
+    p.nkv = n_kv_heads;
+    p.seq_len = seq_len;
+    p.max_seq_len = max_seq_len;
+    // The split count l0h_attention_decode takes outside a recording; its partials (every one is
+    // written by the call, none is read before) go to the static array.
+    p.splits = attention_default_splits(batch, n_kv_heads, max_seq_len, dev->compute_units);
+    if (p.splits > 1) {
+        const size_t bytes = attention_partials_bytes(p);
+        if (bytes > kStaticScratchBytes)
+            return fail(L0H_ERR_INVALID_ARG, "this attention needs " + std::to_string(bytes) +
+                                                 " bytes of split partials; the allocation-free entry point holds " +
+                                                 std::to_string(kStaticScratchBytes));
+        p.partials = dev->static_scratch;
+    }
+    return launch_attention_decode(dev->stream, p);
 }
 
 int l0h_attention_decode(l0h_device* dev, const void* q, int q_dtype, const void* k_cache, const void* v_cache,

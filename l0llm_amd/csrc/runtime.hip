@@ -142,6 +142,7 @@ int l0h_device_open(int ordinal, l0h_device** out) {
         return fail(L0H_ERR_DEVICE, "stream creation failed");
     }
     int st = ensure_workspace(d, 1 << 20, 4096);
+    if (!st) st = static_scratch_init(d);  // hipSetDevice(ordinal) above: the device is current
     if (st) {
         l0h_device_close(d);
         return st;
