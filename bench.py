@@ -13,8 +13,9 @@ The JSON line also carries:
                 lm_head launches): algorithmic bytes / HIP-event duration per launch, measured
                 live on the model's stream (back-to-back launches over all layers), against 8 TB/s
   kernels       the same per kernel kind
-  cpu_baseline  the CPU oracle (fp64-accumulating C) running the same model's decode steps on the
-                host cores, for a bounded sample of `--cpu-tokens` tokens
+  cpu_baseline  the CPU restatements (fp32-accumulating vectorised C, and the fp64 check loop)
+                running the same model's decode steps and the int8 GEMV 896 -> 4864 on the host
+                cores, all cores and one core, for a bounded sample
 """
 from __future__ import annotations
 
@@ -227,8 +228,37 @@ def measure_configs(dev) -> dict:
     return out
 
 
+def _median_s(fn, runs: int) -> float:
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return float(np.median(ts))
+
+
 def cpu_baseline(model, cfg, tokens: int, position: int) -> dict:
+    """The CPU restatements timed on this host's cores: the fp64 check loop (the reference's own CPU
+    matmul semantics, LlmMatrixTests.cs:71-80) and an fp32-accumulating, vectorised, OpenMP form of the
+    same operations; all cores and one core. The int8 GEMV 896 -> 4864 is the median of 21 runs per
+    form; the 8B decode step is the median over `tokens` steps (fp32 form, all cores: the `value`),
+    fewer for the slow forms, so the whole leg stays around half a minute."""
     from oracle import pyoracle as orc
+
+    all_cores = orc.num_threads()
+    # int8 GEMV 896 -> 4864: int8 weights uniform in [-127, 127], fp16 scales U[1e-3, 1e-2], x ~ N(0, 1)
+    rng = np.random.default_rng(101)
+    q = rng.integers(-127, 128, (4864, 896), dtype=np.int8)
+    sc = rng.uniform(1e-3, 1e-2, 4864).astype(np.float16).view(np.uint16)
+    x = rng.standard_normal(896).astype(np.float16).astype(np.float32)
+    gemv = {}
+    for label, fn in (("fp64_check_loop", orc.gemv_nk), ("fp32_vectorised", orc.gemv_nk_f32acc)):
+        for cores in (all_cores, 1):
+            orc.set_threads(cores)
+            fn(orc.I8PC, q, x, sc)
+            t = _median_s(lambda: fn(orc.I8PC, q, x, sc), 21)
+            gemv[f"{label}_{cores}_cores"] = dict(us=round(t * 1e6, 1), gbs=round(4379392 / t / 1e9, 2))
+    orc.set_threads(all_cores)
 
     H = cfg.hidden_size
     w = {"model.embed_tokens.weight": model.export_vector("model.embed_tokens.weight", cfg.vocab_size * H),
@@ -244,18 +274,32 @@ def cpu_baseline(model, cfg, tokens: int, position: int) -> dict:
     c = dict(vocab_size=cfg.vocab_size, hidden_size=H, intermediate_size=cfg.intermediate_size,
              num_layers=cfg.num_layers, num_attention_heads=cfg.num_attention_heads,
              num_key_value_heads=cfg.num_key_value_heads, head_dim=cfg.head_dim, rms_norm_eps=cfg.rms_norm_eps)
-    om = orc.Model(c, w, inv, att, orc.F16, position + tokens + 1)
-    tok = 1
-    om.step(tok, position)  # page in the weights once
-    t0 = time.perf_counter()
-    for i in range(tokens):
-        tok, _ = om.step(tok, position + 1 + i)
-    dt = time.perf_counter() - t0
-    return dict(value=round(tokens / dt, 4), unit="tokens/s", cores=orc.num_threads(), kind="port",
-                sample=f"{tokens} decode tokens of the same int8 model (all 32 layers + lm_head + argmax) at "
-                       f"positions {position + 1}..{position + tokens}, fp64-accumulating C oracle, "
-                       f"{orc.num_threads()} OpenMP threads",
-                cpu_model=host_cpu_model(), host_cpus=len(os.sched_getaffinity(0)))
+    om = orc.Model(c, w, inv, att, orc.F16, position + 3 * tokens + 8)
+    pos = [position]
+
+    def step():
+        om.step(1, pos[0])
+        pos[0] += 1
+
+    steps = {}
+    orc.set_fast_projections(True)
+    step()  # pages the weights in
+    for cores, n in ((all_cores, tokens), (1, max(1, tokens // 4))):
+        orc.set_threads(cores)
+        t = _median_s(step, n)
+        steps[f"fp32_vectorised_{cores}_cores"] = dict(tokens_per_s=round(1 / t, 4), tokens=n)
+    orc.set_threads(all_cores)
+    orc.set_fast_projections(False)
+    n = max(1, tokens // 4)
+    t = _median_s(step, n)
+    steps[f"fp64_check_loop_{all_cores}_cores"] = dict(tokens_per_s=round(1 / t, 4), tokens=n)
+    value = steps[f"fp32_vectorised_{all_cores}_cores"]["tokens_per_s"]
+    return dict(value=value, unit="tokens/s", cores=all_cores, kind="port",
+                sample=f"median decode step of the same int8 Llama-3.1-8B-shaped model (32 layers + lm_head + "
+                       f"argmax, positions from {position}) over {tokens} steps: the fp32-accumulating vectorised "
+                       f"C restatement on {all_cores} OpenMP threads; the other forms and core counts below",
+                step=steps, gemv_int8_896x4864=gemv, cpu_model=host_cpu_model(),
+                host_cpus=len(os.sched_getaffinity(0)), nproc=os.cpu_count())
 
 
 def host_cpu_model() -> str:
@@ -277,7 +321,9 @@ def main() -> int:
     ap.add_argument("--ctx", type=int, default=2048, help="prefilled KV-cache length")
     ap.add_argument("--profile-rounds", type=int, default=4,
                     help="passes over all layers when timing each kernel kind for the roofline")
-    ap.add_argument("--cpu-tokens", type=int, default=2, help="tokens in the CPU baseline sample (0: skip)")
+    ap.add_argument("--cpu-tokens", type=int, default=8,
+                    help="decode steps in the CPU baseline's fp32 all-core sample (a quarter of that for the other "
+                         "forms; 0: skip the CPU baseline)")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the per-configuration kernel measurements (GEMV, prefill GEMM, attention)")
     ap.add_argument("--eager-step", action="store_true",
@@ -296,7 +342,11 @@ def main() -> int:
     cfg = llama8b()
     dev = l0.Device(0)
     copy = hbm_copy_probe(dev)
-    log(f"HBM copy probe: {copy['gbs']} GB/s ({copy['bytes_per_launch']} bytes in {copy['avg_us']} us)")
+    read_gbs = dev.read_bandwidth(2 << 30, 10)
+    copy["read_stream_gbs"] = round(read_gbs, 1)
+    copy["read_stream_kernel"] = "read_stream_kernel (16-byte non-temporal loads over 2 GiB, best of 3 launch shapes)"
+    log(f"HBM probes: streaming read {read_gbs:.0f} GB/s; copy {copy['gbs']} GB/s ({copy['bytes_per_launch']} bytes "
+        f"read + written in {copy['avg_us']} us)")
     max_seq = args.ctx + args.steps + args.cpu_tokens + 8
     log(f"device {dev.name}; building the model (max_seq {max_seq})")
     model = l0.LlmModel(dev, cfg, precision=l0.PRECISION_INT8, cache_dtype=l0.F16, max_seq_len=max_seq)
@@ -339,6 +389,8 @@ def main() -> int:
     gemv_bytes = sum(table[k]["bytes_per_launch"] * table[k]["launches_per_step"] for k in GEMV_KINDS)
     launches = sum(table[k]["launches_per_step"] for k in GEMV_KINDS)
     achieved = gemv_bytes / (gemv_us * 1e-6) / 1e9
+    for t in table.values():  # the same rates against the read ceiling measured on this box
+        t["frac_of_read_ceiling"] = round(t["gbs"] / read_gbs, 4) if read_gbs > 0 else None
     step_bytes = sum(t["bytes_per_launch"] * t["launches_per_step"] for t in table.values())
     # HBM bytes per int8 GEMV launch from the rocprofv3 FETCH_SIZE / WRITE_SIZE runs (calibrated
     # against the copy kernel of known size), summarised in profiles/.
@@ -382,11 +434,13 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": "gemv_nk_kernel<I8PC> (q|k|v, O, gate|up, down, lm_head)",
-                     "bytes_per_launch": round(gemv_bytes / launches), "avg_us_per_launch": round(gemv_us / launches, 3)},
+                     "bytes_per_launch": round(gemv_bytes / launches), "avg_us_per_launch": round(gemv_us / launches, 3),
+                     "frac_of_read_ceiling": round(achieved / read_gbs, 4) if read_gbs > 0 else None,
+                     "read_ceiling_gbs": round(read_gbs, 1)},
         "step_roofline": {"bytes_per_step": round(step_bytes), "ideal_tokens_per_s": round(HBM_PEAK_GBS * 1e9 / step_bytes, 1),
                           "frac": round(tps * step_bytes / (HBM_PEAK_GBS * 1e9), 4)},
         "kernels": table,
-        "hbm_copy_probe": copy,
+        "hbm_probe": copy,
         "prefill": prefill,
         "configs": configs,
         "cpu_baseline": cpu,

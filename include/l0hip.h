@@ -101,6 +101,11 @@ int l0h_replay_recording(l0h_device* dev, int count, float* ms_per_replay);
 int l0h_is_recording(l0h_device* dev, int* out);
 /* Wait for every queued operation. */
 int l0h_synchronize(l0h_device* dev);
+/* Measurement aid, no counterpart in the reference: the HBM read rate of this device in GB/s, from a
+ * streaming-read kernel (16-byte non-temporal loads) over a freshly allocated `bytes`-byte buffer
+ * (well above the 256 MB Infinity Cache for a cold figure), best of three launch shapes, `reps`
+ * launches each. It allocates and frees its buffer. */
+int l0h_device_read_bandwidth(l0h_device* dev, size_t bytes, int reps, double* gbs);
 /* Message of the calling thread's last failure ("" if none). */
 const char* l0h_last_error(void);
 

@@ -137,6 +137,12 @@ class Device:
         check(lib.l0h_is_recording(self.handle, ctypes.byref(v)))
         return bool(v.value)
 
+    def read_bandwidth(self, nbytes: int = 2 << 30, reps: int = 10) -> float:
+        """HBM read rate (GB/s) of a streaming-read kernel over a fresh `nbytes` buffer."""
+        g = ctypes.c_double()
+        check(lib.l0h_device_read_bandwidth(self.handle, ctypes.c_size_t(nbytes), reps, ctypes.byref(g)))
+        return g.value
+
     def synchronize(self) -> None:
         check(lib.l0h_synchronize(self.handle))
 

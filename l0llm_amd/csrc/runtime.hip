@@ -9,6 +9,7 @@
 // hipGraphExecUpdate when the next recording has the same topology.
 #include "common.h"
 
+#include <algorithm>
 #include <cstring>
 
 namespace l0h {
@@ -34,6 +35,27 @@ __global__ void zero_words_kernel(uint32_t* p, size_t words) {
 __global__ void zero_bytes_kernel(uint8_t* p, size_t bytes) {
     size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < bytes) p[i] = 0;
+}
+
+// Streaming read of n16 16-byte chunks (non-temporal loads, 8 per thread in flight, grid-stride):
+// the read rate a weight-streaming kernel can reach on this device. The XOR keeps the loads live.
+__global__ __launch_bounds__(256) void read_stream_kernel(const uint4* p, size_t n16, unsigned* sink) {
+    constexpr int U = 8;
+    const size_t nth = (size_t)gridDim.x * blockDim.x;
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    unsigned acc = 0;
+    for (; i + (U - 1) * nth < n16; i += U * nth) {
+        uint4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) v[u] = ld_nt16(p + i + u * nth);
+#pragma unroll
+        for (int u = 0; u < U; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    for (; i < n16; i += nth) {
+        const uint4 v = ld_nt16(p + i);
+        acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    if (acc == 0x9e3779b9u) sink[0] = acc;  // practically never: only so the loads are not removed
 }
 
 // Zero fill by kernel (not hipMemsetAsync), so it is safe inside a captured graph.
@@ -335,6 +357,47 @@ int l0h_abort_recording(l0h_device* dev) {
 int l0h_is_recording(l0h_device* dev, int* out) {
     L0H_CHECK_ARG(dev && out, "null pointer");
     *out = dev->recording ? 1 : 0;
+    return L0H_OK;
+}
+
+int l0h_device_read_bandwidth(l0h_device* dev, size_t bytes, int reps, double* gbs) {
+    int st = use_device(dev);
+    if (st) return st;
+    L0H_CHECK_ARG(gbs && reps > 0 && bytes >= (1u << 20), "need gbs, reps > 0 and at least 1 MiB");
+    if (dev->recording) return fail(L0H_ERR_INVALID_OP, "the device is recording");
+    bytes &= ~(size_t)15;
+    void* buf = nullptr;
+    unsigned* sink = nullptr;
+    L0H_HIP_TRY(hipMalloc(&buf, bytes));
+    hipError_t e = hipMalloc(&sink, 64);
+    hipEvent_t a = nullptr, b = nullptr;
+    if (e == hipSuccess) e = hipEventCreate(&a);
+    if (e == hipSuccess) e = hipEventCreate(&b);
+    if (e == hipSuccess && zero_fill(dev->stream, buf, bytes)) e = hipErrorLaunchFailure;
+    double best = 0.0;
+    const size_t n16 = bytes / 16;
+    // Launch shapes: 2, 4 and 8 blocks of 256 threads per CU; the best rate counts.
+    for (int per_cu = 2; per_cu <= 8 && e == hipSuccess; per_cu *= 2) {
+        const unsigned grid = (unsigned)(per_cu * std::max(1, dev->compute_units));
+        read_stream_kernel<<<grid, 256, 0, dev->stream>>>(static_cast<const uint4*>(buf), n16, sink);  // warm-up
+        e = hipEventRecord(a, dev->stream);
+        for (int r = 0; r < reps && e == hipSuccess; r++) {
+            read_stream_kernel<<<grid, 256, 0, dev->stream>>>(static_cast<const uint4*>(buf), n16, sink);
+            e = hipGetLastError();
+        }
+        if (e == hipSuccess) e = hipEventRecord(b, dev->stream);
+        if (e == hipSuccess) e = hipEventSynchronize(b);
+        float ms = 0.f;
+        if (e == hipSuccess) e = hipEventElapsedTime(&ms, a, b);
+        if (e == hipSuccess && ms > 0.f) best = std::max(best, (double)bytes * reps / (ms * 1e-3) / 1e9);
+    }
+    (void)hipStreamSynchronize(dev->stream);
+    if (a) (void)hipEventDestroy(a);
+    if (b) (void)hipEventDestroy(b);
+    if (sink) (void)hipFree(sink);
+    (void)hipFree(buf);
+    if (e != hipSuccess) return fail(L0H_ERR_DEVICE, std::string("read bandwidth probe: ") + hipGetErrorString(e));
+    *gbs = best;
     return L0H_OK;
 }
 

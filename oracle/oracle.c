@@ -461,8 +461,14 @@ float orc_top2_margin(const float* logits, int n) {
 /* Whole decoder                                                       */
 /* ------------------------------------------------------------------ */
 
+static int g_fast_projections = 0;
+void orc_set_fast_projections(int on) { g_fast_projections = on; }
+
 static void project(const orc_matrix* m, const float* x, float* y) {
-    orc_gemv_nk(m->wdtype, 1, m->N, m->K, x, m->w, m->scales, y);
+    if (g_fast_projections)
+        orc_gemv_nk_f32acc(m->wdtype, 1, m->N, m->K, x, m->w, m->scales, y);
+    else
+        orc_gemv_nk(m->wdtype, 1, m->N, m->K, x, m->w, m->scales, y);
 }
 
 /* LlmDecoderLayer.Forward (LlmDecoderLayer.cs:129-196) with MixFull (:291-334). */

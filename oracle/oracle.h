@@ -186,6 +186,16 @@ int orc_model_step(const orc_model* m, int token, int position, float* logits);
 
 /* Number of OpenMP threads the oracle uses (1 when built without OpenMP). */
 int orc_num_threads(void);
+/* Sets the number of OpenMP threads (the 1-core CPU baseline). */
+void orc_set_threads(int n);
+
+/* The CPU-baseline form of orc_gemv_nk (cpu_fast.c): fp32 accumulation, vectorised, OpenMP over
+ * output rows. Same operation; rounding differs from the fp64 check loop. */
+void orc_gemv_nk_f32acc(int wdtype, int rows, int N, int K, const float* x, const void* W,
+                        const uint16_t* scales, float* y);
+/* 1: orc_model_step / orc_layer_forward project with orc_gemv_nk_f32acc (the timed CPU baseline);
+ * 0 (default): with the fp64 check loop orc_gemv_nk. */
+void orc_set_fast_projections(int on);
 
 #ifdef __cplusplus
 }

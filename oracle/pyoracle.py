@@ -70,6 +70,28 @@ _sig("orc_embedding", [P, P, P, ctypes.c_int, ctypes.c_int])
 _sig("orc_argmax", [P, ctypes.c_int], ctypes.c_int)
 _sig("orc_top2_margin", [P, ctypes.c_int], ctypes.c_float)
 _sig("orc_num_threads", [], ctypes.c_int)
+_sig("orc_set_threads", [ctypes.c_int])
+_sig("orc_set_fast_projections", [ctypes.c_int])
+_sig("orc_gemv_nk_f32acc", [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, P, P, P, P])
+
+
+def gemv_nk_f32acc(wdtype: int, w: np.ndarray, x: np.ndarray, scales: np.ndarray | None = None) -> np.ndarray:
+    """The CPU-baseline form of gemv_nk: fp32 accumulation, vectorised, OpenMP over output rows."""
+    w = np.ascontiguousarray(w)
+    n, k = w.shape
+    xx = f32(x).reshape(-1, k)
+    y = np.empty((xx.shape[0], n), dtype=np.float32)
+    s = None if scales is None else np.ascontiguousarray(scales).view(np.uint16)
+    _lib.orc_gemv_nk_f32acc(wdtype, xx.shape[0], n, k, _p(xx), _p(w), _p(s), _p(y))
+    return y
+
+
+def set_threads(n: int) -> None:
+    _lib.orc_set_threads(int(n))
+
+
+def set_fast_projections(on: bool) -> None:
+    _lib.orc_set_fast_projections(int(bool(on)))
 
 
 def num_threads() -> int:

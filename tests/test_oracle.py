@@ -377,3 +377,20 @@ def test_model_rope_table_follows_config():
     inv, att = rope_table_for(d["cfg"])
     plain, _ = orc.rope_frequencies(16, 500000.0, 256)
     assert att == 1.0 and inv.shape == plain.shape and not np.allclose(inv, plain)
+
+
+@pytest.mark.parametrize("wdtype", [orc.I8PC, orc.F16, orc.BF16, orc.F32])
+def test_fp32_baseline_gemv_matches_fp64_restatement(wdtype):
+    """The CPU-baseline form (fp32 accumulation, vectorised) computes the same GEMV as the fp64 check
+    loop: within fp32 summation error, 1e-5 of the largest output."""
+    from tests.helpers import stored
+    rng = np.random.default_rng(77 + wdtype)
+    w = rng.normal(0, 0.02, (300, 896)).astype(np.float32)
+    dt, ws, s = stored(wdtype, w)
+    x = rng.normal(0, 1, (3, 896)).astype(np.float32)
+    want = orc.gemv_nk(dt, ws, x, s)
+    got = orc.gemv_nk_f32acc(dt, ws, x, s)
+    assert np.max(np.abs(got - want)) <= 1e-5 * np.max(np.abs(want))
+    # a wrong accumulation (one term dropped) would not pass
+    bad = orc.gemv_nk_f32acc(dt, np.ascontiguousarray(ws[:, :-1]), x[:, :-1], s)
+    assert np.max(np.abs(bad - want)) > 1e-5 * np.max(np.abs(want))
