@@ -430,7 +430,7 @@ def main() -> int:
                                f"{args.ctx}-token prefilled KV cache (fp16), {args.steps} generated tokens",
                    "layers": 32, "hidden": 4096, "intermediate": 14336, "heads": 32, "kv_heads": 8,
                    "head_dim": 128, "vocab": 128256, "batch": 1, "ctx": args.ctx,
-                   "step": "eager launches" if args.eager_step else "HIP graph replay"},
+                   "step": {"graph": "HIP graph replay", "eager": "eager launches"}[model.step_path]},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": "gemv_nk_kernel<I8PC> (q|k|v, O, gate|up, down, lm_head)",

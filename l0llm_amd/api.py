@@ -584,6 +584,13 @@ class LlmModel:
         return k.value, v.value
 
     @property
+    def step_path(self) -> str:
+        """'graph', 'eager' or 'persistent': how a decode step runs."""
+        v = ctypes.c_int()
+        check(lib.l0h_model_step_path(self.handle, ctypes.byref(v)))
+        return ("graph", "eager", "persistent")[v.value]
+
+    @property
     def projection_bytes(self) -> int:
         b = ctypes.c_longlong()
         check(lib.l0h_model_projection_bytes(self.handle, ctypes.byref(b)))

@@ -30,6 +30,7 @@
 
 #include <cstdlib>
 
+#include "dpp.h"
 #include "kernels.h"
 
 namespace l0h {
@@ -41,22 +42,6 @@ constexpr int kBlock = 64 * kWaves;
 // 16 values (two blocks per CU still fit the 160 KiB of LDS).
 constexpr size_t kLdsBudget = 72 * 1024;
 constexpr int kMaxRotaryHalf = 128;       // cos/sin table entries per block (rotary_dim <= 256)
-
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ float dpp_src(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, false));
-}
-
-// Sum over the 64 lanes of a wave, returned to every lane (wave-uniform).
-__device__ __forceinline__ float wave_sum(float v) {
-    v += dpp_src<0xB1, 0xf>(v);   // quad_perm [1,0,3,2]
-    v += dpp_src<0x4E, 0xf>(v);   // quad_perm [2,3,0,1]
-    v += dpp_src<0x141, 0xf>(v);  // row_half_mirror
-    v += dpp_src<0x140, 0xf>(v);  // row_mirror
-    v += dpp_src<0x142, 0xa>(v);  // row_bcast15 into rows 1, 3
-    v += dpp_src<0x143, 0xc>(v);  // row_bcast31 into rows 2, 3
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
-}
 
 // Block-wide sum (all threads of a kBlock block must call it). Returns the sum to all.
 __device__ __forceinline__ float block_sum(float v, float* red) {

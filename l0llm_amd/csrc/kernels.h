@@ -139,6 +139,50 @@ int launch_gemm_nk(hipStream_t s, int dtype, int m, int n, int k, const void* x,
                    void* y, int y_dtype, float* ws, size_t ws_bytes, int compute_units,
                    const uint16_t* scales = nullptr, int epilogue = EPI_STORE);
 
+// ---- persistent decode step (step_kernel.hip) ----
+// One weight-streaming phase of the step: a projection with its epilogue.
+enum StepKind : int { STEP_QKV = 0, STEP_O = 1, STEP_GU = 2, STEP_DOWN = 3, STEP_LM = 4 };
+struct StepPhase {
+    const void* w = nullptr;           // [n, k] weights (HuggingFace order, stored rows)
+    const uint16_t* scales = nullptr;  // int8: fp16 per row
+    const float* norm_w = nullptr;     // RMSNorm of the input (QKV, GU, LM)
+    const float* bias = nullptr;       // q|k|v bias in stored row order (or null)
+    void* k_cache = nullptr;           // QKV: this layer's caches
+    void* v_cache = nullptr;
+    int n = 0, k = 0;                  // rows, row length (elements)
+    int kind = STEP_QKV;
+    int layer = 0;
+};
+struct StepParams {
+    const StepPhase* phases = nullptr;  // device array, nphases entries
+    int nphases = 0;
+    int w_dtype = L0H_I8PC;
+    int hidden = 0, inter = 0, q_dim = 0, kv_dim = 0, n_heads = 0, n_kv = 0, head_dim = 0, rotary_dim = 0;
+    int vocab = 0, max_seq = 0, cache_dtype = L0H_F16;
+    float eps = 0.f, rope_scale = 1.f;
+    const float* inv_freq = nullptr;
+    const float* embedding = nullptr;
+    float *hidden_buf = nullptr, *q = nullptr, *attn = nullptr, *act = nullptr, *logits = nullptr;
+    float* attn_partials = nullptr;      // [n_kv, splits, stride] split partials
+    unsigned long long* amax = nullptr;  // [blocks] argmax keys
+    int *token = nullptr, *position = nullptr, *sampled = nullptr, *step = nullptr, *out_list = nullptr;
+    int out_capacity = 0;
+    unsigned* bar = nullptr;  // [0] grid-barrier arrivals, [1] finished blocks (both return to 0)
+    unsigned* err = nullptr;  // set when a grid barrier waited past its spin limit
+    int splits = 1;           // attention splits per kv head
+    int kx_pad = 0;           // LDS activation tile (elements)
+    int rows_max = 0;         // most rows any block owns in a phase
+};
+// Whether the persistent step supports this model shape (weight type, head size, group size, LDS).
+bool step_kernel_supported(int w_dtype, int head_dim, int group, size_t lds_bytes);
+size_t step_kernel_lds_bytes(const StepParams& p);
+int step_kernel_blocks(int compute_units);
+int launch_decode_step(hipStream_t s, const StepParams& p, int blocks);
+// Bytes of the step's attention partials for n_kv heads x splits (group = q heads per kv head).
+size_t step_partials_bytes(int n_kv, int splits, int head_dim, int group);
+// Attention splits per (kv head, group of up to 4 q heads): about one attention wave per block.
+int step_attention_splits(int blocks, int n_kv, int group);
+
 // Random init: w[i] ~ N(0, std^2) from (seed, i); stored as dtype (F32/F16/BF16).
 int launch_init_normal(hipStream_t s, void* dst, int dtype, size_t count, uint64_t seed,
                        float stddev);
