@@ -25,6 +25,7 @@
 // second pass sums in a fixed order (deterministic). Blocks are renumbered so the blocks that
 // read the same weight columns run on the same XCD (blocks are dealt to the 8 XCDs round robin),
 // where they share that XCD's L2.
+#include <cstdlib>
 #include <type_traits>
 #include <utility>
 
@@ -308,6 +309,191 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(1, 2))
     }
 }
 
+// Both operands through LDS, for the tall shapes (M >= 256): block tile BM x BN, K in stages of 64,
+// four waves in a 2 x 2 layout, each computing a (BM / 2) x (BN / 2) wave tile of 32 x 32 MFMA
+// fragments. A block loads every activation and weight byte of its tile once per stage (16-byte
+// chunks, 8 consecutive lanes per 128-byte row segment) and the waves read their fragments from
+// LDS, so the L2 -> CU traffic per flop is that of the block tile, not of each wave's columns. Rows
+// are padded to 144 bytes: the eight lanes of a 16-byte fragment read cover distinct banks. Stages
+// go global -> registers -> LDS through RS register sets and two LDS buffers: with two sets stage
+// t + 2 is requested before stage t is computed (two compute phases cover each load), with one
+// (the larger tiles, whose registers hold more accumulators and whose compute phase is longer)
+// right after; one barrier per stage orders the LDS hand-off. 16-bit weights only.
+template <int WT, int BM, int BN, int WGM, int WGN, int RS>
+__global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(WGM * WGN / 4, WGM * WGN / 4))) void gemm_lds_kernel(
+    int M, int N, int K, int k_per_split, const uint16_t* __restrict__ X, const void* __restrict__ Wv, void* Y,
+    int y_dtype, int epi, float* partial) {
+    static_assert(WT == L0H_BF16 || WT == L0H_F16, "16-bit weights");
+    constexpr int SK = 64;        // K per stage
+    constexpr int LD = SK + 8;    // LDS row stride in elements (144 bytes)
+    constexpr int STAGE = (BM + BN) * LD;
+    constexpr int NT = 64 * WGM * WGN;  // threads
+    constexpr int TM = BM / WGM, TN = BN / WGN;
+    constexpr int FI = TM / 32, FJ = TN / 32;
+    constexpr int ACH = BM * 8 / NT;  // 16-byte activation chunks per thread per stage
+    constexpr int BCH = BN * 8 / NT;  // 16-byte weight chunks per thread per stage
+    constexpr int ROWS = NT / 8;      // rows between a thread's chunks
+    static_assert(FI >= 1 && FJ >= 1 && ACH >= 1 && BCH >= 1, "tile too small");
+    extern __shared__ uint4 gemm_lds_smem[];
+    uint16_t* lds = reinterpret_cast<uint16_t*>(gemm_lds_smem);  // [2][STAGE]
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave % WGM, wn = wave / WGM;
+    // Block order as in gemm_nk_kernel: consecutive ids on one XCD, groups of row blocks first, so
+    // the row blocks that read the same weight columns share an XCD's L2.
+    const int gx = gridDim.x, gy = gridDim.y, gz = gridDim.z;
+    const int total = gx * gy * gz;
+    int lin = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
+    if (total % kXcds == 0) lin = (lin % kXcds) * (total / kXcds) + lin / kXcds;
+    const int G = row_group(gx);
+    const int gr = lin % G, rest = lin / G;
+    const int bz = rest % gy, bn = (rest / gy) % gz, bm = (rest / (gy * gz)) * G + gr;
+    const int m0 = bm * BM, n0 = bn * BN;
+    const int kbeg = bz * k_per_split;
+    const int nsteps = max(0, min(K, kbeg + k_per_split) - kbeg) / SK;
+    const int last = max(nsteps - 1, 0);
+
+    // Chunk c of this thread: activation and weight rows tid / 8 + c NT / 8, 16 bytes at K offset
+    // (tid % 8) * 8.
+    const uint16_t* ap = X + kbeg + (tid & 7) * 8;
+    const uint16_t* bp = static_cast<const uint16_t*>(Wv) + kbeg + (tid & 7) * 8;
+    const int arow = m0 + (tid >> 3), brow = n0 + (tid >> 3);
+
+    uint4 ra[RS][ACH], rb[RS][BCH];
+    auto gload = [&](uint4 (&a)[ACH], uint4 (&b)[BCH], int t) {
+        const int k0 = min(t, last) * SK;  // stages past the end re-read the last one (never stored)
+#pragma unroll
+        for (int c = 0; c < ACH; c++)
+            a[c] = *reinterpret_cast<const uint4*>(ap + (size_t)min(arow + ROWS * c, M - 1) * K + k0);
+#pragma unroll
+        for (int c = 0; c < BCH; c++)  // several row blocks read it: cached
+            b[c] = *reinterpret_cast<const uint4*>(bp + (size_t)min(brow + ROWS * c, N - 1) * K + k0);
+    };
+    auto sstore = [&](const uint4 (&a)[ACH], const uint4 (&b)[BCH], int buf) {
+        uint16_t* sa = lds + buf * STAGE;
+        uint16_t* sb = sa + BM * LD;
+        // As vector values: a struct copy would keep the registers in memory.
+#pragma unroll
+        for (int c = 0; c < ACH; c++)
+            *reinterpret_cast<u32x4_t*>(&sa[((tid >> 3) + ROWS * c) * LD + (tid & 7) * 8]) =
+                u32x4_t{a[c].x, a[c].y, a[c].z, a[c].w};
+#pragma unroll
+        for (int c = 0; c < BCH; c++)
+            *reinterpret_cast<u32x4_t*>(&sb[((tid >> 3) + ROWS * c) * LD + (tid & 7) * 8]) =
+                u32x4_t{b[c].x, b[c].y, b[c].z, b[c].w};
+    };
+
+    acc_t<32> acc[FI][FJ];
+#pragma unroll
+    for (int i = 0; i < FI; i++)
+#pragma unroll
+        for (int j = 0; j < FJ; j++) acc[i][j] = acc_t<32>{};
+    // The fragments of K substep s + 1 are read from LDS before substep s's MFMAs are issued (two
+    // fragment sets), and a scheduling barrier after each substep keeps the compiler from hoisting
+    // every substep's reads to the top, which would need four sets of fragment registers.
+    auto compute = [&](int buf) {
+        const uint16_t* sa = lds + buf * STAGE + (wm * TM + lane % 32) * LD + 8 * (lane / 32);
+        const uint16_t* sb = lds + buf * STAGE + (BM + wn * TN + lane % 32) * LD + 8 * (lane / 32);
+        uint4 a[2][FI], b[2][FJ];
+        auto frags = [&](int f, int s) {
+#pragma unroll
+            for (int i = 0; i < FI; i++) a[f][i] = *reinterpret_cast<const uint4*>(sa + i * 32 * LD + s * 16);
+#pragma unroll
+            for (int j = 0; j < FJ; j++) b[f][j] = *reinterpret_cast<const uint4*>(sb + j * 32 * LD + s * 16);
+        };
+        frags(0, 0);
+#pragma unroll
+        for (int s = 0; s < SK / 16; s++) {
+            if (s + 1 < SK / 16) frags((s + 1) & 1, s + 1);
+#pragma unroll
+            for (int i = 0; i < FI; i++)
+#pragma unroll
+                for (int j = 0; j < FJ; j++) acc[i][j] = mfma<WT, 32>(a[s & 1][i], b[s & 1][j], acc[i][j]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    if (nsteps > 0) {
+        if constexpr (RS == 2) {
+            gload(ra[0], rb[0], 0);
+            gload(ra[1], rb[1], 1);
+            sstore(ra[0], rb[0], 0);
+            lds_barrier();
+            // Stage t: request stage t + 2 into the register set stage t's data left, compute stage t
+            // from LDS buffer t % 2, move stage t + 1 from registers into the other buffer. Unrolled
+            // by two so the register sets are compile-time.
+            for (int t = 0; t < nsteps; t += 2) {
+                gload(ra[0], rb[0], t + 2);
+                compute(0);
+                sstore(ra[1], rb[1], 1);  // past the end: never read
+                lds_barrier();
+                if (t + 1 >= nsteps) break;
+                gload(ra[1], rb[1], t + 3);
+                compute(1);
+                sstore(ra[0], rb[0], 0);
+                lds_barrier();
+            }
+        } else {
+            gload(ra[0], rb[0], 0);
+            sstore(ra[0], rb[0], 0);
+            gload(ra[0], rb[0], 1);
+            lds_barrier();
+            // Stage t: compute stage t from LDS buffer t % 2, move stage t + 1 from the registers into
+            // the other buffer, request stage t + 2.
+            for (int t = 0; t < nsteps; t += 2) {
+                compute(0);
+                sstore(ra[0], rb[0], 1);  // past the end: never read
+                gload(ra[0], rb[0], t + 2);
+                lds_barrier();
+                if (t + 1 >= nsteps) break;
+                compute(1);
+                sstore(ra[0], rb[0], 0);
+                gload(ra[0], rb[0], t + 3);
+                lds_barrier();
+            }
+        }
+    }
+
+    // Accumulator register r of lane l holds D[8 (r / 4) + 4 (l / 32) + r % 4][l % 32].
+    auto each_out = [&](auto&& f) {
+#pragma unroll
+        for (int j = 0; j < FJ; j++) {
+            const int col = n0 + wn * TN + j * 32 + lane % 32;
+#pragma unroll
+            for (int i = 0; i < FI; i++) {
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int row = m0 + wm * TM + i * 32 + (r / 4) * 8 + (lane / 32) * 4 + (r % 4);
+                    f(row, col, acc[i][j][r]);
+                }
+                __builtin_amdgcn_sched_barrier(0);  // one fragment's addresses live at a time
+            }
+        }
+    };
+    if (partial) {
+        each_out([&](int row, int col, float v) {
+            if (row < M && col < N) partial[((size_t)bz * M + row) * N + col] = v;
+        });
+    } else if (epi == EPI_SWIGLU) {
+        // Column pairs (2c, 2c + 1) sit in lanes (2i, 2i + 1): a DPP swap, executed by every lane,
+        // brings the up value to the gate lane.
+        each_out([&](int row, int col, float v) {
+            const float up = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xf, 0xf, false));
+            if (row < M && col < N && (lane & 1) == 0)
+                store_act_sat(Y, y_dtype, (size_t)row * (N / 2) + col / 2, v / (1.0f + __expf(-v)) * up);
+        });
+    } else if (epi == EPI_RESIDUAL) {
+        each_out([&](int row, int col, float v) {
+            if (row < M && col < N) static_cast<float*>(Y)[(size_t)row * N + col] += v;
+        });
+    } else {
+        each_out([&](int row, int col, float v) {
+            if (row < M && col < N) store_act(Y, y_dtype, (size_t)row * N + col, v);
+        });
+    }
+}
+
 // Sum of the K splits' partials in split order, then the epilogue: store, add to fp32 Y, or (one
 // thread per column pair) silu(gate) * up into Y[row][c].
 __global__ void splitk_reduce_kernel(const float* partial, int splits, size_t mn, void* Y, int y_dtype, int epi) {
@@ -444,6 +630,85 @@ int launch_tiles(hipStream_t s, int m, int n, int k, const void* x, const void* 
     return launch_status("gemm splitk reduce");
 }
 
+// Two-operand LDS tiles (gemm_lds_kernel) for M >= 256 and K a multiple of 64, where they measured
+// faster than gemm_nk_kernel on MI355X: N >= 16384 or K >= 8192 (bf16, host clock per launch:
+// 512 x 16384 x 2048 54.1 against 56.8 us, 512 x 2048 x 8192 39.5 against 43.2, 2047 x 28672 x
+// 4096 671 against 694, 2047 x 4096 x 14336 314 against 345; slower at 512 x 3072 x 2048, 25.8
+// against 24.1, and 512 x 2048 x 2048, 21.1 against 15.3). The largest tile that gives about one
+// block per CU (3/4 of the CUs or more) without a K split, else the K split (power of two, at
+// least 8 stages of 64 per split) that gets there with the fewest partials.
+struct LdsPlan {
+    int bm = 0, bn = 0, splits = 1;
+};
+
+bool lds_plan_for(int dtype, int m, int n, int k, int cus, LdsPlan& out) {
+    static const int mode = [] {
+        const char* e = std::getenv("L0H_GEMM_LDS");  // 0: never, 2: every shape it supports (tuning)
+        return e ? std::atoi(e) : 1;
+    }();
+    // int8 weights stay on gemm_nk_kernel: their conversion on the way into LDS made the 8B
+    // prefill slower (0.044 against 0.041 s for 2048 tokens).
+    if (!mode || dtype == L0H_I8PC || m < 256 || k % 64) return false;
+    if (mode != 2 && n < 16384 && k < 8192) return false;  // 2: wherever it applies (tests, tuning)
+    static const int tiles[][2] = {{128, 256}, {256, 128}, {128, 128}};
+    const size_t want = (size_t)std::max(cus, 1) * 3 / 4;
+    auto blocks = [&](int bm, int bn) { return (size_t)ceil_div(m, bm) * ceil_div(n, bn); };
+    for (const auto& t : tiles)
+        if (blocks(t[0], t[1]) >= want) {
+            out = LdsPlan{t[0], t[1], 1};
+            return true;
+        }
+    for (int sp = 2; sp <= kMaxSplits && k / sp >= 8 * 64; sp *= 2)
+        for (const auto& t : tiles)
+            if (blocks(t[0], t[1]) * sp >= want) {
+                out = LdsPlan{t[0], t[1], sp};
+                return true;
+            }
+    out = LdsPlan{128, 128, 1};
+    while (out.splits * 2 <= kMaxSplits && k / (out.splits * 2) >= 8 * 64) out.splits *= 2;
+    return true;
+}
+
+template <int WT, int BM, int BN, int WGM, int WGN>
+int launch_lds(hipStream_t s, int m, int n, int k, const void* x, const void* w, void* y, int y_dtype, int epi,
+               int splits, float* ws) {
+    constexpr size_t lds = (size_t)2 * (BM + BN) * (64 + 8) * sizeof(uint16_t);
+    constexpr int NT = 64 * WGM * WGN;
+    static const int rs_env = [] {
+        const char* e = std::getenv("L0H_GEMM_LDS_RS");  // register stages (tuning): 1 or 2
+        return e ? std::atoi(e) : 0;
+    }();
+    const int rs = rs_env == 1 || rs_env == 2 ? rs_env : 1;
+    auto kern = rs == 2 ? gemm_lds_kernel<WT, BM, BN, WGM, WGN, 2> : gemm_lds_kernel<WT, BM, BN, WGM, WGN, 1>;
+    static const hipError_t attr = [&] {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_lds_kernel<WT, BM, BN, WGM, WGN, 1>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e == hipSuccess)
+            e = hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_lds_kernel<WT, BM, BN, WGM, WGN, 2>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        return e;
+    }();
+    if (attr != hipSuccess) return fail(L0H_ERR_DEVICE, std::string("hipFuncSetAttribute: ") + hipGetErrorString(attr));
+    const int k_per_split = (k / 64 + splits - 1) / splits * 64;
+    dim3 grid(ceil_div(m, BM), splits, ceil_div(n, BN));
+    kern<<<grid, NT, lds, s>>>(m, n, k, k_per_split, static_cast<const uint16_t*>(x), w, y, y_dtype, epi,
+                              splits > 1 ? ws : nullptr);
+    int st = launch_status("gemm_lds");
+    if (st || splits == 1) return st;
+    const size_t mn = (size_t)m * n;
+    const size_t threads = epi == EPI_SWIGLU ? mn / 2 : mn;
+    splitk_reduce_kernel<<<ceil_div(threads, 256), 256, 0, s>>>(ws, splits, mn, y, y_dtype, epi);
+    return launch_status("gemm splitk reduce");
+}
+
+template <int WT>
+int launch_lds_plan(hipStream_t s, const LdsPlan& p, int m, int n, int k, const void* x, const void* w, void* y,
+                    int y_dtype, int epi, float* ws) {
+    if (p.bm == 128 && p.bn == 256) return launch_lds<WT, 128, 256, 2, 4>(s, m, n, k, x, w, y, y_dtype, epi, p.splits, ws);
+    if (p.bm == 256 && p.bn == 128) return launch_lds<WT, 256, 128, 4, 2>(s, m, n, k, x, w, y, y_dtype, epi, p.splits, ws);
+    return launch_lds<WT, 128, 128, 2, 2>(s, m, n, k, x, w, y, y_dtype, epi, p.splits, ws);
+}
+
 template <int WT>
 int launch_plan(hipStream_t s, const Plan& p, int m, int n, int k, const void* x, const void* w,
                 const uint16_t* scales, void* y, int y_dtype, int epi, float* ws) {
@@ -468,8 +733,11 @@ int launch_plan(hipStream_t s, const Plan& p, int m, int n, int k, const void* x
 
 size_t gemm_workspace_bytes(int m, int n, int k, int compute_units) {
     if (k % BK) return 0;
-    const Plan p = plan_for(m, n, k, compute_units);
-    return p.splits > 1 ? (size_t)p.splits * m * n * sizeof(float) : 0;
+    // The larger of the two kernels' split-K partials (the weight type picks the kernel).
+    LdsPlan lp;
+    const int lds_splits = lds_plan_for(L0H_BF16, m, n, k, compute_units, lp) ? lp.splits : 1;
+    const int splits = std::max(lds_splits, plan_for(m, n, k, compute_units).splits);
+    return splits > 1 ? (size_t)splits * m * n * sizeof(float) : 0;
 }
 
 int launch_gemm_nk(hipStream_t s, int dtype, int m, int n, int k, const void* x, const void* w,
@@ -491,6 +759,12 @@ int launch_gemm_nk(hipStream_t s, int dtype, int m, int n, int k, const void* x,
         gemm_nk_generic_kernel<<<ceil_div(mn, 256), 256, 0, s>>>(dtype, m, n, k, static_cast<const uint16_t*>(x),
                                                                  static_cast<const uint16_t*>(w), y, y_dtype);
         return launch_status("gemm_nk_generic");
+    }
+    LdsPlan lp;
+    if (lds_plan_for(dtype, m, n, k, cus, lp)) {
+        while (lp.splits > 1 && (size_t)lp.splits * m * n * sizeof(float) > ws_bytes) lp.splits /= 2;
+        return dtype == L0H_BF16 ? launch_lds_plan<L0H_BF16>(s, lp, m, n, k, x, w, y, y_dtype, epilogue, ws)
+                                 : launch_lds_plan<L0H_F16>(s, lp, m, n, k, x, w, y, y_dtype, epilogue, ws);
     }
     Plan p = plan_for(m, n, k, cus);
     while (p.splits > 1 && (size_t)p.splits * m * n * sizeof(float) > ws_bytes) p.splits /= 2;

@@ -397,12 +397,13 @@ def test_recording_matches_eager_and_replays(device, suite):
 # ---- MFMA prefill GEMM -------------------------------------------------------------------------
 
 # Stages of two K steps (K % 64 == 0), one K step (K % 64 == 32: (96, 300, 160)), the 128 x 64
-# wave tile (512 x 16384), K splits, ragged M / N, the any-shape fallback (K % 32 != 0), and the
-# 256 x 256 eight-wave blocks with a ragged last row block and fewer stages than the ring holds
-# (1030 x 10240 x 256).
+# wave tile (512 x 16384), K splits, ragged M / N, the any-shape fallback (K % 32 != 0), the
+# 256 x 256 eight-wave blocks with a ragged last row block (1030 x 10240 x 256); the two-operand
+# LDS tiles (M >= 256 with N >= 16384 or K >= 8192): ragged rows and an odd stage count
+# (300 x 16384 x 320), a ragged column block with K = 8192 (260 x 640 x 8192).
 @pytest.mark.parametrize("m,n,k", [(64, 256, 512), (128, 3072, 2048), (512, 2048, 2048), (100, 200, 128),
                                    (128, 64, 8192), (33, 40, 70), (96, 300, 160), (512, 1024, 256),
-                                   (1030, 10240, 256)])
+                                   (1030, 10240, 256), (300, 16384, 320), (260, 640, 8192)])
 @pytest.mark.parametrize("dtype", [l0.BF16, l0.F16])
 def test_gemm_nk_matches_oracle(device, suite, m, n, k, dtype):
     rng = np.random.default_rng(m + n + k)
@@ -420,7 +421,8 @@ def test_gemm_nk_matches_oracle(device, suite, m, n, k, dtype):
 
 
 @pytest.mark.parametrize("m,n,k", [(64, 256, 512), (256, 768, 4096), (256, 512, 14336), (100, 200, 128),
-                                   (33, 48, 96), (128, 2048, 1024), (512, 320, 2048), (1030, 10240, 512)])
+                                   (33, 48, 96), (128, 2048, 1024), (512, 320, 2048), (1030, 10240, 512),
+                                   (260, 384, 8192), (520, 16384, 448)])
 def test_gemm_nk_i8pc_matches_oracle(device, suite, m, n, k):
     """int8 weights converted to fp16 in registers (exact), fp16 activations, fp32 accumulation,
     row scale in the epilogue: the oracle's int8 per-channel product on the same fp16 inputs."""
