@@ -179,6 +179,41 @@ def measure_configs(dev) -> dict:
                            ("lm_head", 151936, 896)):
             gemv_case(f"qwen05b_{tag}_{name}", wdt, n, k)
 
+    # The reference-layout fp16 GEMV (Gemv.Execute, W as [K, N], fp32 x and y), which an unchanged
+    # LlmMatrix.Project reaches for fp16 storage: the int8 GEMV's 896 -> 4864 shape and the
+    # Qwen2.5-0.5B linears, next to the [N, K] kernel at the same shapes (vs_nk = kn / nk time).
+    def kn_case(name, n, k):
+        wbytes = n * k * 2
+        reps = max(2, min(512, -(-COLD_BYTES // wbytes)))
+        wblock = (rng.standard_normal(min(n * k, 1 << 22), dtype=np.float32) * 0.02).astype(np.float16)
+        w = _replicated(dev, wblock, wbytes, reps)
+        x = dev.alloc_shared(rng.standard_normal(k).astype(np.float32))
+        y = dev.alloc(n * 4)
+        suite.gemv_execute(n, k, x, w, y)  # sizes the K-slice workspace before recording
+
+        def run(count, cold=True):
+            for i in range(count):
+                suite.gemv_execute(n, k, x, w.ptr + (i % reps if cold else 0) * wbytes, y)
+
+        cold_us = _replay_us(dev, lambda: run(reps), reps)
+        hot_us = _replay_us(dev, lambda: run(64, cold=False), 64)
+        nbytes = wbytes + k * 4 + n * 4
+        for b in (w, x, y):
+            b.free()
+        nk = out.get(f"qwen05b_fp16_{name}") if name != "up_896x4864" else None
+        out[f"fp16_gemv_kn_{name}"] = dict(
+            n=n, k=k, w="fp16 [K,N]", bytes=nbytes, us=round(cold_us, 3), gbs=round(nbytes / cold_us / 1e3, 1),
+            frac=round(nbytes / cold_us / 1e3 / HBM_PEAK_GBS, 4), hot_us=round(hot_us, 3),
+            vs_nk=round(cold_us / nk["us"], 3) if nk else None)
+
+    gemv_case("fp16_gemv_nk_up_896x4864", l0.F16, 4864, 896, x_dt=l0.F32, y_dt=l0.F32)
+    kn_case("up_896x4864", 4864, 896)
+    out["fp16_gemv_kn_up_896x4864"]["vs_nk"] = round(
+        out["fp16_gemv_kn_up_896x4864"]["us"] / out["fp16_gemv_nk_up_896x4864"]["us"], 3)
+    for name, n, k in (("qkv", 1152, 896), ("o", 896, 896), ("gate_up", 9728, 896), ("down", 896, 4864),
+                       ("lm_head", 151936, 896)):
+        kn_case(name, n, k)
+
     # Llama-3.2-1B prefill GEMMs, bf16 operands, fp32 accumulation on MFMA, bf16 out
     for m in (128, 512):
         for name, n, k in (("qkv", 3072, 2048), ("o", 2048, 2048), ("gate_up", 16384, 2048), ("down", 2048, 8192)):

@@ -193,13 +193,114 @@ __global__ __launch_bounds__(kBlock) void gemv_kn_tile_kernel(int N, int K, int 
     }
 }
 
-// y[r, n] = sum over slices s (in order) of part[s, r, n].
+// y[r, n] = sum over slices of part[s, r, n] in a fixed order: four running sums over the slices
+// s = 4 j + q (their loads independent, so four are in flight), added as (s0 + s1) + (s2 + s3).
 __global__ void kn_slice_sum_kernel(const float* part, float* y, int splits, size_t count) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= count) return;
-    float v = part[i];
-    for (int s = 1; s < splits; s++) v += part[(size_t)s * count + i];
-    y[i] = v;
+    float a[4] = {0.f, 0.f, 0.f, 0.f};
+    int s = 0;
+    for (; s + 4 <= splits; s += 4) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) a[q] += part[(size_t)(s + q) * count + i];
+    }
+    for (int q = 0; s + q < splits; q++) a[q] += part[(size_t)(s + q) * count + i];
+    y[i] = (a[0] + a[1]) + (a[2] + a[3]);
+}
+
+// One activation row in narrow column tiles: block (tile t of 8 chunks = 128 bytes of every weight
+// row, K slice s). Lane l reads chunk l % 8 of row l / 8 of each group of 8 rows, so one wave
+// instruction covers 8 whole 128-byte row segments and the block's 4 waves take rows 32 apart.
+// The slice's rows go in batches of kNarrowU per lane, the next batch requested before the current
+// one is computed; x comes from LDS (zero past the slice, where the clamped rows add nothing). The
+// 8 lanes of a chunk are summed over DPP and row swaps, the waves through LDS in a fixed order.
+constexpr int kNarrowU = 8;      // row groups per lane per batch
+constexpr int kNarrowRPS = 32;   // rows per block step (8 per wave instruction, 4 waves)
+constexpr int kNarrowLds = kKnLds - 4096;  // dynamic LDS for x (the wave reduction is static)
+
+template <int WT>
+__global__ __launch_bounds__(kBlock) void gemv_kn_narrow_kernel(int N, int K, int ks, const float* x, const void* w,
+                                                                float* out) {
+    constexpr int EPC = WT == L0H_F16 ? 8 : 4;  // columns per 16-byte chunk
+    constexpr int TC = 8 * EPC;                 // columns per tile
+    extern __shared__ float kn_smem[];
+    float* xs = kn_smem;                         // [steps rounded to batches * kNarrowRPS]
+    __shared__ float red[kWaves][TC];
+    const int CN = N / EPC;
+    const int t = blockIdx.x, sl = blockIdx.y;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = lane >> 3, cj = lane & 7;
+    const int k0 = sl * ks, k1 = min(K, k0 + ks);
+    const int steps = (k1 - k0 + kNarrowRPS - 1) / kNarrowRPS;
+    const int batches = (steps + kNarrowU - 1) / kNarrowU;
+    const int nx = batches * kNarrowU * kNarrowRPS;
+    for (int i = threadIdx.x; i < nx; i += kBlock) xs[i] = k0 + i < k1 ? x[k0 + i] : 0.f;
+    __syncthreads();
+    const uint4* wp = static_cast<const uint4*>(w) + min(t * 8 + cj, CN - 1);
+    float acc[EPC];
+#pragma unroll
+    for (int e = 0; e < EPC; e++) acc[e] = 0.f;
+    auto load = [&](uint4 (&v)[kNarrowU], int b) {
+#pragma unroll
+        for (int u = 0; u < kNarrowU; u++) {
+            const int row = k0 + (b * kNarrowU + u) * kNarrowRPS + wave * 8 + r;
+            v[u] = ld_nt16(wp + (size_t)min(row, K - 1) * CN);
+        }
+    };
+    auto compute = [&](const uint4 (&v)[kNarrowU], int b) {
+#pragma unroll
+        for (int u = 0; u < kNarrowU; u++) {
+            const float xv = xs[(b * kNarrowU + u) * kNarrowRPS + wave * 8 + r];
+            const uint32_t d[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+            if constexpr (WT == L0H_F16) {
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const float2 h = __half22float2(__builtin_bit_cast(__half2, d[q]));
+                    acc[2 * q] = fmaf(xv, h.x, acc[2 * q]);
+                    acc[2 * q + 1] = fmaf(xv, h.y, acc[2 * q + 1]);
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; q++) acc[q] = fmaf(xv, __uint_as_float(d[q]), acc[q]);
+            }
+        }
+    };
+    // Batch b: request batch b + 1, compute batch b (the last one with nothing behind it).
+    uint4 va[kNarrowU], vb[kNarrowU];
+    if (batches > 0) {
+        load(va, 0);
+        int b = 0;
+        for (;;) {
+            if (b + 1 == batches) {
+                compute(va, b);
+                break;
+            }
+            load(vb, b + 1);
+            compute(va, b);
+            if (++b + 1 == batches) {
+                compute(vb, b);
+                break;
+            }
+            load(va, b + 1);
+            compute(vb, b);
+            b++;
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < EPC; e++) acc[e] = slot_reduce<8, false>(acc[e]);  // the 8 row lanes of chunk cj
+    if (r == 0) {
+#pragma unroll
+        for (int e = 0; e < EPC; e++) red[wave][cj * EPC + e] = acc[e];
+    }
+    __syncthreads();
+    if (threadIdx.x < TC) {
+        const int c = t * TC + threadIdx.x;
+        float v = red[0][threadIdx.x];
+#pragma unroll
+        for (int ww = 1; ww < kWaves; ww++) v += red[ww][threadIdx.x];
+        if (c < N) out[(size_t)sl * N + c] = v;
+    }
 }
 
 // Any shape (N not a multiple of the load width, unaligned buffers): each thread owns 4
@@ -264,6 +365,20 @@ int launch_kn_tile(hipStream_t s, int n, int k, int ks, int splits, const float*
 }
 
 template <int WT>
+int launch_kn_narrow(hipStream_t s, int n, int k, int ks, int splits, const float* x, const void* w, float* out) {
+    constexpr int EPC = WT == L0H_F16 ? 8 : 4;
+    const unsigned tiles = ceil_div((size_t)(n / EPC), 8);
+    const int steps = (ks + kNarrowRPS - 1) / kNarrowRPS;
+    const size_t shmem = (size_t)((steps + kNarrowU - 1) / kNarrowU) * kNarrowU * kNarrowRPS * sizeof(float);
+    auto kern = gemv_kn_narrow_kernel<WT>;
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, kNarrowLds);
+    if (attr != hipSuccess) return fail(L0H_ERR_DEVICE, std::string("hipFuncSetAttribute: ") + hipGetErrorString(attr));
+    kern<<<dim3(tiles, splits), kBlock, shmem, s>>>(n, k, ks, x, w, out);
+    return launch_status("gemv_kn_narrow");
+}
+
+template <int WT>
 int launch_kn_rows(hipStream_t s, int mr, int n, int k, int ks, int splits, const float* x, const void* w, float* out) {
     switch (mr) {
     case 1: return launch_kn_tile<WT, 1>(s, n, k, ks, splits, x, w, out);
@@ -276,6 +391,32 @@ int launch_kn_rows(hipStream_t s, int mr, int n, int k, int ks, int splits, cons
 
 KnPlan plan_gemv_kn(int rows, int n, int k, int w_dtype, int compute_units, size_t ws_bytes) {
     const int epc = w_dtype == L0H_F16 ? 8 : 4;
+    if (rows == 1) {
+        // Narrow tiles: no K split from min_tiles tiles up (a K split costs a second launch for the
+        // slice sum); else slices of whole batches (at least 256 rows) up to about one block per CU.
+        KnPlan pl;
+        pl.narrow = true;
+        const int tiles = (int)ceil_div((size_t)(n / epc), 8);
+        const int batch_rows = kNarrowU * kNarrowRPS;
+        const int max_ks = (kNarrowLds / 4) / batch_rows * batch_rows;  // the slice's x fits the LDS
+        static const int min_tiles_env = [] {  // tiles from which no K split is made (tuning)
+            const char* e = std::getenv("L0H_GEMV_KN_TILES");
+            return e ? std::atoi(e) : 0;
+        }();
+        // 16 tiles (1024 fp16 columns) measured best on MI355X: Qwen2.5-0.5B q|k|v (18 tiles) 4.9 us
+        // unsplit against 5.7 us in slices; 896 -> 4864 (76 tiles) 5.4 against 6.6 us.
+        const int min_tiles = min_tiles_env > 0 ? min_tiles_env : 16;
+        int splits = tiles >= min_tiles ? 1 : (int)ceil_div((size_t)std::max(compute_units, 1), (size_t)tiles);
+        splits = std::min(splits, std::max(1, k / batch_rows));
+        splits = std::max(splits, (int)ceil_div((size_t)k, (size_t)max_ks));
+        const size_t per_split = (size_t)n * sizeof(float);
+        if (splits > 1 && (size_t)splits * per_split > ws_bytes)
+            splits = std::max((int)ceil_div((size_t)k, (size_t)max_ks), (int)std::min<size_t>(splits, ws_bytes / per_split));
+        pl.ks = (int)ceil_div((size_t)ceil_div((size_t)k, (size_t)std::max(splits, 1)), (size_t)kNarrowRPS) * kNarrowRPS;
+        pl.ks = std::min(pl.ks, max_ks);
+        pl.splits = (int)ceil_div((size_t)k, (size_t)pl.ks);
+        return pl;
+    }
     const int tiles = (int)ceil_div((size_t)(n / epc), 64);
     constexpr int step = kWaves * kKnUnroll;  // rows of a slice come in whole unrolled steps
     // About two blocks per CU over the column tiles.
@@ -327,7 +468,12 @@ int launch_gemv_kn(hipStream_t s, int rows, int n, int k, const float* x, const 
         const float* xr = x + (size_t)done * k;
         float* yr = y + (size_t)done * n;
         float* out = pl.splits > 1 ? ws : yr;
-        int st = w_dtype == L0H_F16 ? launch_kn_rows<L0H_F16>(s, pl.mr, n, k, pl.ks, pl.splits, xr, w, out)
+        int st;
+        if (pl.narrow)
+            st = w_dtype == L0H_F16 ? launch_kn_narrow<L0H_F16>(s, n, k, pl.ks, pl.splits, xr, w, out)
+                                    : launch_kn_narrow<L0H_F32>(s, n, k, pl.ks, pl.splits, xr, w, out);
+        else
+            st = w_dtype == L0H_F16 ? launch_kn_rows<L0H_F16>(s, pl.mr, n, k, pl.ks, pl.splits, xr, w, out)
                                     : launch_kn_rows<L0H_F32>(s, pl.mr, n, k, pl.ks, pl.splits, xr, w, out);
         if (st) return st;
         if (pl.splits > 1) {

@@ -65,7 +65,8 @@ def test_q8_members_project_like_llm_matrix(device, suite):
 # is no multiple of a slice; the any-shape path (N % 8 != 0).
 KN_CASES = [(4864, 896, 1, l0.F16), (1152, 896, 1, l0.F16), (896, 896, 1, l0.F16), (9728, 896, 1, l0.F16),
             (896, 4864, 1, l0.F16), (151936, 896, 1, l0.F16), (4864, 896, 8, l0.F16), (4864, 896, 5, l0.F32),
-            (1000, 300, 2, l0.F32), (2048, 1000, 3, l0.F16), (4100, 64, 1, l0.F16), (30, 17, 2, l0.F16)]
+            (1000, 300, 2, l0.F32), (2048, 1000, 3, l0.F16), (4100, 64, 1, l0.F16), (30, 17, 2, l0.F16),
+            (4864, 896, 1, l0.F32), (1000, 1000, 1, l0.F16), (896, 14336, 1, l0.F16)]
 
 
 @pytest.mark.parametrize("n,k,rows,wdt", KN_CASES)
