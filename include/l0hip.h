@@ -412,8 +412,8 @@ int l0h_model_projection_bytes(l0h_model* model, long long* bytes);
 /* How a decode step runs (no reference counterpart; the reference records one command list per
  * token, LlmModel.cs:402-444): L0H_STEP_GRAPH, the step's kernels captured once as a HIP graph and
  * replayed; L0H_STEP_EAGER, the same kernels enqueued one by one (L0H_EAGER_STEP=1); or
- * L0H_STEP_PERSISTENT, the whole step as one persistent kernel (L0H_STEP_KERNEL=1 at creation,
- * int8 weights with an fp16 cache). */
+ * L0H_STEP_PERSISTENT, the whole step as one persistent kernel (int8 weights with an fp16 cache;
+ * disabled: model creation with L0H_STEP_KERNEL=1 fails with L0H_ERR_UNSUPPORTED). */
 #define L0H_STEP_GRAPH 0
 #define L0H_STEP_EAGER 1
 #define L0H_STEP_PERSISTENT 2
