@@ -395,23 +395,31 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
     auto compute = [&](int buf) {
         const uint16_t* sa = lds + buf * STAGE + (wm * TM + lane % 32) * LD + 8 * (lane / 32);
         const uint16_t* sb = lds + buf * STAGE + (BM + wn * TN + lane % 32) * LD + 8 * (lane / 32);
-        uint4 a[2][FI], b[2][FJ];
-        auto frags = [&](int f, int s) {
+        uint4 a0[FI], b0[FJ], a1[FI], b1[FJ];
+        auto frags = [&](uint4 (&a)[FI], uint4 (&b)[FJ], int s) {
 #pragma unroll
-            for (int i = 0; i < FI; i++) a[f][i] = *reinterpret_cast<const uint4*>(sa + i * 32 * LD + s * 16);
+            for (int i = 0; i < FI; i++) a[i] = *reinterpret_cast<const uint4*>(sa + i * 32 * LD + s * 16);
 #pragma unroll
-            for (int j = 0; j < FJ; j++) b[f][j] = *reinterpret_cast<const uint4*>(sb + j * 32 * LD + s * 16);
+            for (int j = 0; j < FJ; j++) b[j] = *reinterpret_cast<const uint4*>(sb + j * 32 * LD + s * 16);
         };
-        frags(0, 0);
-#pragma unroll
-        for (int s = 0; s < SK / 16; s++) {
-            if (s + 1 < SK / 16) frags((s + 1) & 1, s + 1);
+        auto mma = [&](const uint4 (&a)[FI], const uint4 (&b)[FJ]) {
 #pragma unroll
             for (int i = 0; i < FI; i++)
 #pragma unroll
-                for (int j = 0; j < FJ; j++) acc[i][j] = mfma<WT, 32>(a[s & 1][i], b[s & 1][j], acc[i][j]);
+                for (int j = 0; j < FJ; j++) acc[i][j] = mfma<WT, 32>(a[i], b[j], acc[i][j]);
+        };
+        frags(a0, b0, 0);
+        for_each_index<SK / 16>([&](auto sc) {  // substep indices are constants: the sets stay registers
+            constexpr int s = decltype(sc)::value;
+            if constexpr (s % 2 == 0) {
+                if constexpr (s + 1 < SK / 16) frags(a1, b1, s + 1);
+                mma(a0, b0);
+            } else {
+                if constexpr (s + 1 < SK / 16) frags(a0, b0, s + 1);
+                mma(a1, b1);
+            }
             __builtin_amdgcn_sched_barrier(0);
-        }
+        });
     };
 
     if (nsteps > 0) {
