@@ -122,13 +122,15 @@ def test_prefill_matches_sequential_decode(device):  # Qwen25PrefillTests.cs:41-
 # query-tiled prefill attention: 300 prompt tokens = a full 256-token chunk + a ragged one + the
 # last token through the decode step. fp32 weights run multi-row GEMVs on fp32 activations (the
 # decode arithmetic); int8 / fp16 / bf16 run the MFMA GEMM on activations rounded to fp16 / fp16 /
-# bf16, hence their looser bounds (relative to max |logit|).
-CHUNKED = [(l0.PRECISION_INT8, 1e-2), (l0.PRECISION_FLOAT32, 2e-3), (l0.PRECISION_FLOAT16, 1e-2),
-           (l0.PRECISION_BFLOAT16, 5e-2)]
+# bf16, hence their looser bounds (relative to max |logit|; measured on MI355X: int8 9.4e-4, fp16
+# 6.6e-4, bf16 2.9e-3, so the bounds hold about 3x margin). The cache keys are bounded by key_tol
+# relative to max(1, max |key|).
+CHUNKED = [(l0.PRECISION_INT8, 3e-3, 4e-2), (l0.PRECISION_FLOAT32, 2e-3, 8e-3), (l0.PRECISION_FLOAT16, 3e-3, 4e-2),
+           (l0.PRECISION_BFLOAT16, 1.5e-2, 2e-1)]
 
 
-@pytest.mark.parametrize("precision,tol", CHUNKED)
-def test_chunked_prefill_matches_sequential_decode(device, precision, tol, monkeypatch):
+@pytest.mark.parametrize("precision,tol,key_tol", CHUNKED)
+def test_chunked_prefill_matches_sequential_decode(device, precision, tol, key_tol, monkeypatch):
     monkeypatch.setenv("L0H_PREFILL_CHUNK", "256")  # read at model creation: 299 rows -> chunks of 256 and 43
     cfg = l0.HfConfig(hidden_size=256, intermediate_size=512, num_layers=3, num_attention_heads=4,
                       num_key_value_heads=2, head_dim=64, vocab_size=512, max_position_embeddings=4096,
@@ -154,7 +156,7 @@ def test_chunked_prefill_matches_sequential_decode(device, precision, tol, monke
         for li in range(3):  # keys of every prompt position (the last one written by the decode step)
             a = k_seq[li].astype(np.float32)
             b = keys(li).astype(np.float32)
-            assert np.max(np.abs(a - b)) <= 4 * tol * max(1.0, np.max(np.abs(a))), li
+            assert np.max(np.abs(a - b)) <= key_tol * max(1.0, np.max(np.abs(a))), li
 
 
 @pytest.mark.parametrize("precision,tol", [(l0.PRECISION_INT8, 1e-2), (l0.PRECISION_FLOAT16, 1e-2)])
@@ -176,12 +178,14 @@ def test_wide_prefill_split_k_epilogues_match_decode(device, precision, tol):
 
 
 @pytest.mark.parametrize("tokens", [600, 2048])
-@pytest.mark.parametrize("precision,tol", [(l0.PRECISION_INT8, 1e-2), (l0.PRECISION_BFLOAT16, 5e-2)])
+@pytest.mark.parametrize("precision,tol", [(l0.PRECISION_INT8, 3e-3), (l0.PRECISION_BFLOAT16, 1.5e-2)])
 def test_tall_prefill_eight_wave_tiles_match_decode(device, precision, tol, tokens):
-    """599 prefill rows at hidden 4096, intermediate 8192: the GEMMs take the eight-wave 128-row
-    tiles (gate|up one-step stages; down, K = 8192, two-step stages with K split in four). 2047
-    rows: q|k|v (N = 6144) and gate|up (N = 16384, SwiGLU epilogue) take the 256 x 256 blocks
-    with a ragged last row block, O and down the 128-row tiles."""
+    """599 prefill rows at hidden 4096, intermediate 8192: the int8 GEMMs take the eight-wave
+    128-row tiles (gate|up one-step stages; down, K = 8192, two-step stages with K split in four).
+    2047 rows: q|k|v (N = 6144) and gate|up (N = 16384, SwiGLU epilogue) take the 256 x 256 blocks
+    with a ragged last row block, O and down the 128-row tiles. For bf16 weights gate|up and down
+    (N = 16384, K = 8192) take the two-operand LDS tiles at both lengths. Measured deviations on
+    MI355X: int8 7.6e-4 / 7.0e-4, bf16 4.3e-3 / 4.9e-3 of max |logit| (600 / 2048 tokens)."""
     cfg = l0.HfConfig(hidden_size=4096, intermediate_size=8192, num_layers=1, num_attention_heads=32,
                       num_key_value_heads=8, head_dim=128, vocab_size=256, max_position_embeddings=4096,
                       rms_norm_eps=1e-5, rope_theta=500000.0)
