@@ -21,6 +21,12 @@
 // used), and the one barrier per stage waits on LDS only, so the in-order memory counter's waits
 // are exact: the wait before stage t + 1's LDS store lets the P - 2 younger stages stay in flight.
 //
+// From 256 rows, 16-bit weights take gemm_dma_kernel instead: both operands pass through a ring of
+// LDS stages that LDS-direct loads (global_load_lds_dwordx4) fill, so two stages of both operands
+// are in flight while one is computed and no registers stage them; block tiles of 128 x 256,
+// 256 x 128 or 128 x 128 with 64 x 64 wave tiles, and an epilogue that goes through LDS so each
+// output row segment is written by consecutive lanes.
+//
 // Shapes with fewer blocks than the GPU has CUs split K across blocks into fp32 partials that a
 // second pass sums in a fixed order (deterministic). Blocks are renumbered so the blocks that
 // read the same weight columns run on the same XCD (blocks are dealt to the 8 XCDs round robin),
@@ -309,33 +315,138 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(1, 2))
     }
 }
 
-// Both operands through LDS, for the tall shapes (M >= 256): block tile BM x BN, K in stages of 64,
-// four waves in a 2 x 2 layout, each computing a (BM / 2) x (BN / 2) wave tile of 32 x 32 MFMA
-// fragments. A block loads every activation and weight byte of its tile once per stage (16-byte
-// chunks, 8 consecutive lanes per 128-byte row segment) and the waves read their fragments from
-// LDS, so the L2 -> CU traffic per flop is that of the block tile, not of each wave's columns. Rows
-// are padded to 144 bytes: the eight lanes of a 16-byte fragment read cover distinct banks. Stages
-// go global -> registers -> LDS through RS register sets and two LDS buffers: with two sets stage
-// t + 2 is requested before stage t is computed (two compute phases cover each load), with one
-// (the larger tiles, whose registers hold more accumulators and whose compute phase is longer)
-// right after; one barrier per stage orders the LDS hand-off. 16-bit weights only.
-template <int WT, int BM, int BN, int WGM, int WGN, int RS>
-__global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(WGM * WGN / 4, WGM * WGN / 4))) void gemm_lds_kernel(
+// ---- two-operand tiles through a ring of LDS stages filled by LDS-direct loads ----------------
+// An LDS row holds 64 16-bit values of one operand row (K step of a stage): 8 chunks of 16 bytes,
+// unpadded, chunk c of tile row r in slot c ^ lds_swz(r). Eight consecutive rows then put a
+// fragment read's 16-byte chunks (same c, rows r .. r + 7) in 8 different slots and alternate
+// 64-byte bank halves, and rows r + 8 .. r + 15 take the other 8 slot orders, so the 16 lanes
+// of a ds_read_b128 pass hit distinct banks.
+__device__ __forceinline__ int lds_swz(int r) { return (r ^ (r >> 3)) & 7; }
+
+// 16 bytes per lane from sbase + voff into LDS bytes lds + 16 * lane (global_load_lds_dwordx4; the
+// LDS address comes from M0). Written as assembly so the compiler, which cannot tell which LDS
+// bytes such a load writes, does not wait for every one in flight before each LDS read: the ring
+// below waits for them itself (vmcnt) before the barrier that hands a stage to the other waves.
+// M0, which the compiler reserves, is restored afterwards.
+__device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t lds) {
+    // Wave-uniform values the compiler may hold in vector registers: the operands need scalar ones.
+    // (readfirstlane returns int: each half goes through uint32_t so the low one is not
+    // sign-extended into the high one.)
+    const uint64_t b = reinterpret_cast<uintptr_t>(base);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+    const uint64_t sbase = (uint64_t)lo | ((uint64_t)hi << 32);
+    lds = __builtin_amdgcn_readfirstlane(lds);
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %3\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, %2\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(voff), "s"(sbase), "s"(lds)
+        : "memory");
+}
+
+// s_waitcnt vmcnt(N) (N < 64), expcnt and lgkmcnt left alone.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+__device__ __forceinline__ uint32_t act_bits16(int dt, float v) {
+    return dt == L0H_F16 ? __half_as_ushort(__float2half_rn(v)) : float_to_bf16_bits(v);
+}
+
+// The epilogue of output columns col .. col + 3 (col % 4 == 0) of row `row`, v their fp32 results:
+// the K split's partial, or the store (Y in y_dtype), the residual add (fp32 Y += v) or SwiGLU
+// (column pairs (gate, up) -> silu(gate) * up into Y of width N / 2). One vector access where the
+// four columns are inside N and the destination is aligned, else element by element.
+__device__ __forceinline__ void store4(int epi, float* partial, int bz, void* Y, int y_dtype, int M, int N, int row,
+                                       int col, float4 v) {
+    if (row >= M || col >= N) return;
+    const float e[4] = {v.x, v.y, v.z, v.w};
+    const bool whole = col + 4 <= N;
+    if (partial) {
+        float* d = partial + ((size_t)bz * M + row) * N + col;
+        if (whole && ((uintptr_t)d & 15) == 0) {
+            *reinterpret_cast<float4*>(d) = v;
+        } else {
+            for (int i = 0; i < 4 && col + i < N; i++) d[i] = e[i];
+        }
+        return;
+    }
+    if (epi == EPI_SWIGLU) {  // N even, col even: pairs (col, col + 1) and (col + 2, col + 3)
+        const float o0 = v.x / (1.0f + __expf(-v.x)) * v.y, o1 = v.z / (1.0f + __expf(-v.z)) * v.w;
+        const size_t idx = (size_t)row * (N / 2) + col / 2;
+        if (whole && y_dtype != L0H_F32 && ((uintptr_t)(static_cast<uint16_t*>(Y) + idx) & 3) == 0) {
+            auto sat = [&](float o) {  // as store_act_sat: fp16 saturates at +-65504, NaN stays NaN
+                return y_dtype == L0H_F16 && fabsf(o) > 65504.f ? copysignf(65504.f, o) : o;
+            };
+            *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(Y) + idx) =
+                act_bits16(y_dtype, sat(o0)) | (act_bits16(y_dtype, sat(o1)) << 16);
+        } else {
+            store_act_sat(Y, y_dtype, idx, o0);
+            if (col + 2 < N) store_act_sat(Y, y_dtype, idx + 1, o1);
+        }
+        return;
+    }
+    const size_t idx = (size_t)row * N + col;
+    if (epi == EPI_RESIDUAL) {
+        float* d = static_cast<float*>(Y) + idx;
+        if (whole && ((uintptr_t)d & 15) == 0) {
+            float4 o = *reinterpret_cast<const float4*>(d);
+            o.x += v.x;
+            o.y += v.y;
+            o.z += v.z;
+            o.w += v.w;
+            *reinterpret_cast<float4*>(d) = o;
+        } else {
+            for (int i = 0; i < 4 && col + i < N; i++) d[i] += e[i];
+        }
+        return;
+    }
+    if (whole && y_dtype == L0H_F32 && ((uintptr_t)(static_cast<float*>(Y) + idx) & 15) == 0) {
+        *reinterpret_cast<float4*>(static_cast<float*>(Y) + idx) = v;
+    } else if (whole && y_dtype != L0H_F32 && ((uintptr_t)(static_cast<uint16_t*>(Y) + idx) & 7) == 0) {
+        *reinterpret_cast<uint2*>(static_cast<uint16_t*>(Y) + idx) =
+            make_uint2(act_bits16(y_dtype, v.x) | (act_bits16(y_dtype, v.y) << 16),
+                       act_bits16(y_dtype, v.z) | (act_bits16(y_dtype, v.w) << 16));
+    } else {
+        for (int i = 0; i < 4 && col + i < N; i++) store_act(Y, y_dtype, idx + i, e[i]);
+    }
+}
+
+// Y[M, N] = X[M, K] W[N, K]^T for 16-bit operands, K a multiple of 64. Block tile BM x BN, waves
+// WGM x WGN with a (BM / WGM) x (BN / WGN) tile each of 32 x 32 x 16 MFMAs. K advances in stages of
+// 64 through NS LDS buffers: at stage t every wave waits for its own loads of stage t, the block
+// meets at one barrier (which also means every wave has finished reading stage t - 1), the waves
+// request stage t + NS - 1 into the buffer stage t - 1 used, and compute stage t. So NS - 1
+// stages of both operands are in flight during each stage's MFMAs, with no register staging.
+// A wave's loads of a stage: rows w, w + NW, ... of the stage's (BM + BN) / 8 groups of 8 rows
+// (A rows first), one 1 KiB load per group; every load is unconditional (rows past M / N and
+// stages past the end re-read valid addresses, never used), so the in-order counter's wait for
+// stage t is exact.
+template <int WT, int BM, int BN, int WGM, int WGN, int NS>
+__global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(WGM * WGN / 4, WGM * WGN / 4))) void gemm_dma_kernel(
     int M, int N, int K, int k_per_split, const uint16_t* __restrict__ X, const void* __restrict__ Wv, void* Y,
     int y_dtype, int epi, float* partial) {
     static_assert(WT == L0H_BF16 || WT == L0H_F16, "16-bit weights");
-    constexpr int SK = 64;        // K per stage
-    constexpr int LD = SK + 8;    // LDS row stride in elements (144 bytes)
-    constexpr int STAGE = (BM + BN) * LD;
-    constexpr int NT = 64 * WGM * WGN;  // threads
+    constexpr int SK = 64;
+    constexpr int ROWB = SK * 2;               // bytes per LDS row
+    constexpr int STAGE = (BM + BN) * ROWB;    // bytes per stage
+    constexpr int NW = WGM * WGN;              // waves
+    constexpr int NT = 64 * NW;                // threads
     constexpr int TM = BM / WGM, TN = BN / WGN;
     constexpr int FI = TM / 32, FJ = TN / 32;
-    constexpr int ACH = BM * 8 / NT;  // 16-byte activation chunks per thread per stage
-    constexpr int BCH = BN * 8 / NT;  // 16-byte weight chunks per thread per stage
-    constexpr int ROWS = NT / 8;      // rows between a thread's chunks
-    static_assert(FI >= 1 && FJ >= 1 && ACH >= 1 && BCH >= 1, "tile too small");
-    extern __shared__ uint4 gemm_lds_smem[];
-    uint16_t* lds = reinterpret_cast<uint16_t*>(gemm_lds_smem);  // [2][STAGE]
+    constexpr int DA = BM / 8 / NW, D = (BM + BN) / 8 / NW;  // loads per wave per stage (A, all)
+    static_assert(FI >= 1 && FJ >= 1 && DA >= 1 && DA * NW * 8 == BM && D * NW * 8 == BM + BN, "tile shape");
+    static_assert(NS >= 2 && (NS - 2) * D < 64, "ring depth");
+    extern __shared__ uint4 gemm_dma_smem[];
+    const char* lds = reinterpret_cast<const char*>(gemm_dma_smem);
+    const uint32_t lds0 = (uint32_t)(uintptr_t)((__attribute__((address_space(3))) char*)gemm_dma_smem);
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -354,34 +465,25 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
     const int nsteps = max(0, min(K, kbeg + k_per_split) - kbeg) / SK;
     const int last = max(nsteps - 1, 0);
 
-    // Chunk c of this thread: activation and weight rows tid / 8 + c NT / 8, 16 bytes at K offset
-    // (tid % 8) * 8.
-    const uint16_t* ap = X + kbeg + (tid & 7) * 8;
-    const uint16_t* bp = static_cast<const uint16_t*>(Wv) + kbeg + (tid & 7) * 8;
-    const int arow = m0 + (tid >> 3), brow = n0 + (tid >> 3);
-
-    uint4 ra[RS][ACH], rb[RS][BCH];
-    auto gload = [&](uint4 (&a)[ACH], uint4 (&b)[BCH], int t) {
-        const int k0 = min(t, last) * SK;  // stages past the end re-read the last one (never stored)
+    // This lane's source offset (bytes from the stage's K column) for each of the wave's loads:
+    // group g = wave + NW d holds tile rows 8 g' .. 8 g' + 7 of A (g' = g) or of B (g' = g - BM / 8);
+    // lane l fills slot l % 8 of row 8 g' + l / 8, which holds chunk (l % 8) ^ lds_swz(row).
+    uint32_t voff[D];
 #pragma unroll
-        for (int c = 0; c < ACH; c++)
-            a[c] = *reinterpret_cast<const uint4*>(ap + (size_t)min(arow + ROWS * c, M - 1) * K + k0);
+    for (int d = 0; d < D; d++) {
+        const int g = wave + NW * d;
+        const int gl = d < DA ? g : g - BM / 8;
+        const int r = 8 * gl + lane / 8;
+        const int row = d < DA ? min(m0 + r, M - 1) : min(n0 + r, N - 1);
+        voff[d] = (uint32_t)row * (uint32_t)K * 2u + (uint32_t)(((lane & 7) ^ lds_swz(r)) * 16);
+    }
+    const uint16_t* xa = X + kbeg;
+    const uint16_t* wb = static_cast<const uint16_t*>(Wv) + kbeg;
+    auto issue = [&](int t, int buf) {
+        const int k0 = min(t, last) * SK;
+        const uint32_t base = lds0 + (uint32_t)(buf * STAGE + wave * 1024);
 #pragma unroll
-        for (int c = 0; c < BCH; c++)  // several row blocks read it: cached
-            b[c] = *reinterpret_cast<const uint4*>(bp + (size_t)min(brow + ROWS * c, N - 1) * K + k0);
-    };
-    auto sstore = [&](const uint4 (&a)[ACH], const uint4 (&b)[BCH], int buf) {
-        uint16_t* sa = lds + buf * STAGE;
-        uint16_t* sb = sa + BM * LD;
-        // As vector values: a struct copy would keep the registers in memory.
-#pragma unroll
-        for (int c = 0; c < ACH; c++)
-            *reinterpret_cast<u32x4_t*>(&sa[((tid >> 3) + ROWS * c) * LD + (tid & 7) * 8]) =
-                u32x4_t{a[c].x, a[c].y, a[c].z, a[c].w};
-#pragma unroll
-        for (int c = 0; c < BCH; c++)
-            *reinterpret_cast<u32x4_t*>(&sb[((tid >> 3) + ROWS * c) * LD + (tid & 7) * 8]) =
-                u32x4_t{b[c].x, b[c].y, b[c].z, b[c].w};
+        for (int d = 0; d < D; d++) dma16(d < DA ? (const void*)(xa + k0) : (const void*)(wb + k0), voff[d], base + d * NW * 1024);
     };
 
     acc_t<32> acc[FI][FJ];
@@ -389,18 +491,27 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
     for (int i = 0; i < FI; i++)
 #pragma unroll
         for (int j = 0; j < FJ; j++) acc[i][j] = acc_t<32>{};
-    // The fragments of K substep s + 1 are read from LDS before substep s's MFMAs are issued (two
-    // fragment sets), and a scheduling barrier after each substep keeps the compiler from hoisting
-    // every substep's reads to the top, which would need four sets of fragment registers.
+    // Fragment rows of this lane (tile rows; B rows after the BM A rows) and their swizzles.
+    int ar[FI], br[FJ];
+#pragma unroll
+    for (int i = 0; i < FI; i++) ar[i] = wm * TM + i * 32 + lane % 32;
+#pragma unroll
+    for (int j = 0; j < FJ; j++) br[j] = wn * TN + j * 32 + lane % 32;
+    const int hi = lane / 32;
+    // K substep s reads chunk 2 s + lane / 32 of each fragment row. The fragments of substep s + 1
+    // are read before substep s's MFMAs are issued (two sets); a scheduling barrier per substep
+    // keeps the compiler from hoisting all four substeps' reads.
     auto compute = [&](int buf) {
-        const uint16_t* sa = lds + buf * STAGE + (wm * TM + lane % 32) * LD + 8 * (lane / 32);
-        const uint16_t* sb = lds + buf * STAGE + (BM + wn * TN + lane % 32) * LD + 8 * (lane / 32);
+        const char* sa = lds + buf * STAGE;
+        const char* sb = sa + BM * ROWB;
         uint4 a0[FI], b0[FJ], a1[FI], b1[FJ];
         auto frags = [&](uint4 (&a)[FI], uint4 (&b)[FJ], int s) {
 #pragma unroll
-            for (int i = 0; i < FI; i++) a[i] = *reinterpret_cast<const uint4*>(sa + i * 32 * LD + s * 16);
+            for (int i = 0; i < FI; i++)
+                a[i] = *reinterpret_cast<const uint4*>(sa + ar[i] * ROWB + (((2 * s + hi) ^ lds_swz(ar[i])) << 4));
 #pragma unroll
-            for (int j = 0; j < FJ; j++) b[j] = *reinterpret_cast<const uint4*>(sb + j * 32 * LD + s * 16);
+            for (int j = 0; j < FJ; j++)
+                b[j] = *reinterpret_cast<const uint4*>(sb + br[j] * ROWB + (((2 * s + hi) ^ lds_swz(br[j])) << 4));
         };
         auto mma = [&](const uint4 (&a)[FI], const uint4 (&b)[FJ]) {
 #pragma unroll
@@ -409,7 +520,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
                 for (int j = 0; j < FJ; j++) acc[i][j] = mfma<WT, 32>(a[i], b[j], acc[i][j]);
         };
         frags(a0, b0, 0);
-        for_each_index<SK / 16>([&](auto sc) {  // substep indices are constants: the sets stay registers
+        for_each_index<SK / 16>([&](auto sc) {
             constexpr int s = decltype(sc)::value;
             if constexpr (s % 2 == 0) {
                 if constexpr (s + 1 < SK / 16) frags(a1, b1, s + 1);
@@ -423,82 +534,45 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
     };
 
     if (nsteps > 0) {
-        if constexpr (RS == 2) {
-            gload(ra[0], rb[0], 0);
-            gload(ra[1], rb[1], 1);
-            sstore(ra[0], rb[0], 0);
-            lds_barrier();
-            // Stage t: request stage t + 2 into the register set stage t's data left, compute stage t
-            // from LDS buffer t % 2, move stage t + 1 from registers into the other buffer. Unrolled
-            // by two so the register sets are compile-time.
-            for (int t = 0; t < nsteps; t += 2) {
-                gload(ra[0], rb[0], t + 2);
-                compute(0);
-                sstore(ra[1], rb[1], 1);  // past the end: never read
-                lds_barrier();
-                if (t + 1 >= nsteps) break;
-                gload(ra[1], rb[1], t + 3);
-                compute(1);
-                sstore(ra[0], rb[0], 0);
-                lds_barrier();
-            }
-        } else {
-            gload(ra[0], rb[0], 0);
-            sstore(ra[0], rb[0], 0);
-            gload(ra[0], rb[0], 1);
-            lds_barrier();
-            // Stage t: compute stage t from LDS buffer t % 2, move stage t + 1 from the registers into
-            // the other buffer, request stage t + 2.
-            for (int t = 0; t < nsteps; t += 2) {
-                compute(0);
-                sstore(ra[0], rb[0], 1);  // past the end: never read
-                gload(ra[0], rb[0], t + 2);
-                lds_barrier();
-                if (t + 1 >= nsteps) break;
-                compute(1);
-                sstore(ra[0], rb[0], 0);
-                gload(ra[0], rb[0], t + 3);
-                lds_barrier();
-            }
+#pragma unroll
+        for (int t = 0; t < NS - 1; t++) issue(t, t);
+        int cur = 0, nxt = NS - 1;  // buffer of stage t, buffer stage t + NS - 1 goes to
+        for (int t = 0; t < nsteps; t++) {
+            wait_vmcnt<(NS - 2) * D>();  // this wave's loads of stage t have landed in LDS
+            lds_barrier();               // everyone's have; everyone is done with stage t - 1
+            issue(t + NS - 1, nxt);
+            compute(cur);
+            nxt = cur;
+            cur = cur + 1 == NS ? 0 : cur + 1;
         }
+        wait_vmcnt<0>();  // the clamped tail loads: none may still write LDS when the block exits
     }
 
-    // Accumulator register r of lane l holds D[8 (r / 4) + 4 (l / 32) + r % 4][l % 32].
-    auto each_out = [&](auto&& f) {
+    // Epilogue through LDS: the fp32 tile (rows padded to BN + 8 floats) is written fragment by
+    // fragment, then read back as 4 consecutive columns per thread, so each output row segment is
+    // stored by consecutive lanes (16 / 8 / 4 contiguous bytes per lane instead of one 2-byte value
+    // per lane spread over two rows).
+    float* tile = reinterpret_cast<float*>(gemm_dma_smem);
+    constexpr int LDT = BN + 8;  // 4 rows apart = 128 bytes mod 256: the two half-waves' rows use distinct banks
+    lds_barrier();               // every wave is done reading the stages
+#pragma unroll
+    for (int i = 0; i < FI; i++)
 #pragma unroll
         for (int j = 0; j < FJ; j++) {
-            const int col = n0 + wn * TN + j * 32 + lane % 32;
+            const int c = wn * TN + j * 32 + lane % 32;
 #pragma unroll
-            for (int i = 0; i < FI; i++) {
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int row = m0 + wm * TM + i * 32 + (r / 4) * 8 + (lane / 32) * 4 + (r % 4);
-                    f(row, col, acc[i][j][r]);
-                }
-                __builtin_amdgcn_sched_barrier(0);  // one fragment's addresses live at a time
-            }
+            for (int r = 0; r < 16; r++)
+                tile[(wm * TM + i * 32 + (r / 4) * 8 + (lane / 32) * 4 + (r % 4)) * LDT + c] = acc[i][j][r];
         }
-    };
-    if (partial) {
-        each_out([&](int row, int col, float v) {
-            if (row < M && col < N) partial[((size_t)bz * M + row) * N + col] = v;
-        });
-    } else if (epi == EPI_SWIGLU) {
-        // Column pairs (2c, 2c + 1) sit in lanes (2i, 2i + 1): a DPP swap, executed by every lane,
-        // brings the up value to the gate lane.
-        each_out([&](int row, int col, float v) {
-            const float up = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xf, 0xf, false));
-            if (row < M && col < N && (lane & 1) == 0)
-                store_act_sat(Y, y_dtype, (size_t)row * (N / 2) + col / 2, v / (1.0f + __expf(-v)) * up);
-        });
-    } else if (epi == EPI_RESIDUAL) {
-        each_out([&](int row, int col, float v) {
-            if (row < M && col < N) static_cast<float*>(Y)[(size_t)row * N + col] += v;
-        });
-    } else {
-        each_out([&](int row, int col, float v) {
-            if (row < M && col < N) store_act(Y, y_dtype, (size_t)row * N + col, v);
-        });
+    lds_barrier();
+    constexpr int C4 = BN / 4, RPP = NT / C4;  // threads per row, rows per pass
+    static_assert(NT % C4 == 0 && BM % RPP == 0, "epilogue pass shape");
+    const int c4 = tid % C4;
+#pragma unroll 4
+    for (int r0 = 0; r0 < BM; r0 += RPP) {
+        const int rl = r0 + tid / C4;
+        const float4 v = *reinterpret_cast<const float4*>(tile + rl * LDT + 4 * c4);
+        store4(epi, partial, bz, Y, y_dtype, M, N, m0 + rl, n0 + 4 * c4, v);
     }
 }
 
@@ -638,13 +712,14 @@ int launch_tiles(hipStream_t s, int m, int n, int k, const void* x, const void* 
     return launch_status("gemm splitk reduce");
 }
 
-// Two-operand LDS tiles (gemm_lds_kernel) for M >= 256 and K a multiple of 64, where they measured
-// faster than gemm_nk_kernel on MI355X: N >= 16384 or K >= 8192 (bf16, host clock per launch:
-// 512 x 16384 x 2048 54.1 against 56.8 us, 512 x 2048 x 8192 39.5 against 43.2, 2047 x 28672 x
-// 4096 671 against 694, 2047 x 4096 x 14336 314 against 345; slower at 512 x 3072 x 2048, 25.8
-// against 24.1, and 512 x 2048 x 2048, 21.1 against 15.3). The largest tile that gives about one
-// block per CU (3/4 of the CUs or more) without a K split, else the K split (power of two, at
-// least 8 stages of 64 per split) that gets there with the fewest partials.
+// Two-operand LDS tiles (gemm_dma_kernel) for M >= 256 and K a multiple of 64. The largest tile
+// that gives about one block per CU (3/4 of the CUs or more) without a K split, else the K split
+// (power of two, at least 8 stages of 64 per split) that gets there with the fewest partials; used
+// unless that split leaves less than 1024 of K per block, where gemm_nk_kernel without a split is
+// faster. Measured on MI355X (bf16, host clock per launch, against gemm_nk_kernel): 512 x 16384 x
+// 2048 46.8 against 56.5 us, 512 x 2048 x 8192 (split 4) 33.2 against 43.1, 512 x 3072 x 2048
+// (split 2) 22.4 against 23.8, 2047 x 28672 x 4096 600 against 694, 2047 x 4096 x 14336 283 against
+// 344, 2047 x 4096 x 4096 83 against 107; 512 x 2048 x 2048 (split 4) 18.4 against 15.2.
 struct LdsPlan {
     int bm = 0, bn = 0, splits = 1;
 };
@@ -657,7 +732,7 @@ bool lds_plan_for(int dtype, int m, int n, int k, int cus, LdsPlan& out) {
     // int8 weights stay on gemm_nk_kernel: their conversion on the way into LDS made the 8B
     // prefill slower (0.044 against 0.041 s for 2048 tokens).
     if (!mode || dtype == L0H_I8PC || m < 256 || k % 64) return false;
-    if (mode != 2 && n < 16384 && k < 8192) return false;  // 2: wherever it applies (tests, tuning)
+    if ((size_t)std::max(m, n) * k * 2 >= (1ull << 32)) return false;  // the LDS-direct loads take 32-bit offsets
     static const int tiles[][2] = {{128, 256}, {256, 128}, {128, 128}};
     const size_t want = (size_t)std::max(cus, 1) * 3 / 4;
     auto blocks = [&](int bm, int bn) { return (size_t)ceil_div(m, bm) * ceil_div(n, bn); };
@@ -670,38 +745,45 @@ bool lds_plan_for(int dtype, int m, int n, int k, int cus, LdsPlan& out) {
         for (const auto& t : tiles)
             if (blocks(t[0], t[1]) * sp >= want) {
                 out = LdsPlan{t[0], t[1], sp};
-                return true;
+                return mode == 2 || k / sp >= 1024;  // 2: wherever it applies (tests, tuning)
             }
     out = LdsPlan{128, 128, 1};
     while (out.splits * 2 <= kMaxSplits && k / (out.splits * 2) >= 8 * 64) out.splits *= 2;
-    return true;
+    return mode == 2 || k / out.splits >= 1024;
 }
+
+// LDS bytes of the epilogue's fp32 output tile (rows padded by 8 floats).
+constexpr size_t dma_tile_bytes(int bm, int bn) { return (size_t)bm * (bn + 8) * sizeof(float); }
 
 template <int WT, int BM, int BN, int WGM, int WGN>
 int launch_lds(hipStream_t s, int m, int n, int k, const void* x, const void* w, void* y, int y_dtype, int epi,
                int splits, float* ws) {
-    constexpr size_t lds = (size_t)2 * (BM + BN) * (64 + 8) * sizeof(uint16_t);
     constexpr int NT = 64 * WGM * WGN;
-    static const int rs_env = [] {
-        const char* e = std::getenv("L0H_GEMM_LDS_RS");  // register stages (tuning): 1 or 2
-        return e ? std::atoi(e) : 0;
+    constexpr size_t stage = (size_t)(BM + BN) * 128;
+    constexpr int kMaxNs = 160 * 1024 / stage >= 4 ? 4 : 3;
+    static const int ns_env = [] {
+        const char* e = std::getenv("L0H_GEMM_LDS_STAGES");  // tuning: LDS ring depth, 2 .. 4
+        return e ? std::atoi(e) : 3;
     }();
-    const int rs = rs_env == 1 || rs_env == 2 ? rs_env : 1;
-    auto kern = rs == 2 ? gemm_lds_kernel<WT, BM, BN, WGM, WGN, 2> : gemm_lds_kernel<WT, BM, BN, WGM, WGN, 1>;
-    static const hipError_t attr = [&] {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_lds_kernel<WT, BM, BN, WGM, WGN, 1>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e == hipSuccess)
-            e = hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_lds_kernel<WT, BM, BN, WGM, WGN, 2>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        return e;
-    }();
-    if (attr != hipSuccess) return fail(L0H_ERR_DEVICE, std::string("hipFuncSetAttribute: ") + hipGetErrorString(attr));
+    const int ns = std::max(2, std::min(ns_env, kMaxNs));
     const int k_per_split = (k / 64 + splits - 1) / splits * 64;
     dim3 grid(ceil_div(m, BM), splits, ceil_div(n, BN));
-    kern<<<grid, NT, lds, s>>>(m, n, k, k_per_split, static_cast<const uint16_t*>(x), w, y, y_dtype, epi,
-                              splits > 1 ? ws : nullptr);
-    int st = launch_status("gemm_lds");
+    auto launch = [&](auto nsc) {
+        constexpr int NS = decltype(nsc)::value;
+        constexpr size_t bytes = std::max((size_t)NS * stage, dma_tile_bytes(BM, BN));
+        static_assert(bytes <= 160 * 1024, "LDS budget");
+        static const hipError_t attr =
+            hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_dma_kernel<WT, BM, BN, WGM, WGN, NS>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+        if (attr != hipSuccess) return fail(L0H_ERR_DEVICE, std::string("hipFuncSetAttribute: ") + hipGetErrorString(attr));
+        gemm_dma_kernel<WT, BM, BN, WGM, WGN, NS><<<grid, NT, bytes, s>>>(
+            m, n, k, k_per_split, static_cast<const uint16_t*>(x), w, y, y_dtype, epi, splits > 1 ? ws : nullptr);
+        return L0H_OK;
+    };
+    int st = ns == 2   ? launch(std::integral_constant<int, 2>{})
+             : ns == 3 ? launch(std::integral_constant<int, 3>{})
+                       : launch(std::integral_constant<int, kMaxNs>{});
+    if (!st) st = launch_status("gemm_lds");
     if (st || splits == 1) return st;
     const size_t mn = (size_t)m * n;
     const size_t threads = epi == EPI_SWIGLU ? mn / 2 : mn;
