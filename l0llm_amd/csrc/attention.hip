@@ -129,8 +129,9 @@ __global__ __launch_bounds__(kBlock) void attn_split_kernel(const AttnParams p, 
     constexpr int NG = kWaves * PPW;  // position slots per block
     constexpr int U = kUnroll;
     using T = typename CacheRow<CT>::T;
-    __shared__ float s_m[kWaves][G], s_l[kWaves][G];
-    __shared__ float s_acc[kWaves][G][HD];
+    constexpr int NSL = NG;  // position slots of the block (kWaves * PPW)
+    __shared__ float s_m[NSL][G], s_l[NSL][G], s_c[NSL][G], s_M[G];
+    __shared__ float s_acc[NSL][G][HD];
 
     const int split = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
     const int gsize = p.nh / p.nkv;
@@ -337,40 +338,43 @@ __global__ __launch_bounds__(kBlock) void attn_split_kernel(const AttnParams p, 
         }
     }
 
-    // Combine the PPW slots of a wave (lanes lane % LPP == lg).
+    // Combine the block's slots through LDS, in a fixed order: every slot's LPP lanes write their 8
+    // dims of every head and its first lane the running maxima and sums; then each (slot, head)
+    // gets its weight 2^(m - M) against the head's block maximum M; then each output (head, dim)
+    // sums its slots' weighted accumulators and sums.
 #pragma unroll
     for (int h = 0; h < G; h++) {
-        const float M = slot_reduce<LPP, true>(m[h]);
-        const float c = M == -INFINITY ? 0.f : exp2_hw(m[h] - M);
-        const float lw = slot_reduce<LPP, false>(l[h] * c);
-#pragma unroll
-        for (int d = 0; d < 8; d++) acc[h][d] = slot_reduce<LPP, false>(acc[h][d] * c);
-        if (lane < LPP) {
-#pragma unroll
-            for (int d = 0; d < 8; d++) s_acc[wave][h][lg * 8 + d] = acc[h][d];
-            if (lane == 0) {
-                s_m[wave][h] = M;
-                s_l[wave][h] = lw;
-            }
+        float4* dst = reinterpret_cast<float4*>(&s_acc[slot][h][lg * 8]);
+        dst[0] = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
+        dst[1] = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
+        if (lg == 0) {
+            s_m[slot][h] = m[h];
+            s_l[slot][h] = l[h];
         }
     }
     __syncthreads();
+    for (int t = tid; t < NSL * G; t += kBlock) {
+        const int h = t / NSL, sl = t - h * NSL;
+        float M = -INFINITY;
+#pragma unroll 8
+        for (int i = 0; i < NSL; i++) M = fmaxf(M, s_m[i][h]);
+        s_c[sl][h] = M == -INFINITY ? 0.f : exp2_hw(s_m[sl][h] - M);
+        if (sl == 0) s_M[h] = M;
+    }
+    __syncthreads();
 
-    // Combine the waves (fixed order): the output directly when the sequence is not split, else
-    // this split's partial.
+    // The output directly when the sequence is not split, else this split's partial.
     constexpr int PS = partial_stride(G, HD);
     float* part = p.splits > 1 ? p.partials + (((size_t)b * p.nkv + g) * p.splits + split) * PS : nullptr;
     for (int idx = tid; idx < G * HD; idx += kBlock) {
         const int h = idx / HD, d = idx - h * HD;
-        float M = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < kWaves; w++) M = fmaxf(M, s_m[w][h]);
+        const float M = s_M[h];
         float num = 0.f, den = 0.f;
-#pragma unroll
-        for (int w = 0; w < kWaves; w++) {
-            const float c = M == -INFINITY ? 0.f : exp2_hw(s_m[w][h] - M);
-            num = fmaf(c, s_acc[w][h][d], num);
-            den = fmaf(c, s_l[w][h], den);
+#pragma unroll 8
+        for (int i = 0; i < NSL; i++) {
+            const float c = s_c[i][h];
+            num = fmaf(c, s_acc[i][h][d], num);
+            den = fmaf(c, s_l[i][h], den);
         }
         if (p.splits == 1) {
             if (h < gsize)

@@ -31,6 +31,7 @@
 // second pass sums in a fixed order (deterministic). Blocks are renumbered so the blocks that
 // read the same weight columns run on the same XCD (blocks are dealt to the 8 XCDs round robin),
 // where they share that XCD's L2.
+#include <cstdio>
 #include <cstdlib>
 #include <type_traits>
 #include <utility>
@@ -640,6 +641,12 @@ Plan plan_for(int m, int n, int k, int cus) {
     struct Tile {
         int bm, nw, waves;
     };
+    static const Plan forced = [] {  // L0H_GEMM_PLAN=bm,nw,splits,waves (tuning; an unknown tile fails)
+        Plan f{0, 0, 0, 0};
+        if (const char* e = std::getenv("L0H_GEMM_PLAN")) std::sscanf(e, "%d,%d,%d,%d", &f.bm, &f.nw, &f.splits, &f.waves);
+        return f;
+    }();
+    if (forced.bm > 0 && forced.splits >= 1 && forced.splits <= kMaxSplits) return forced;
     static const Tile tiles[] = {{128, 64, 4}, {128, 32, 4}, {128, 16, 4}, {64, 64, 4}, {64, 32, 4}, {64, 16, 4}};
     static const Tile tiles_tall[] = {{256, 32, 8}, {128, 32, 8}, {128, 32, 4}, {128, 64, 4},
                                       {128, 16, 4}, {64, 64, 4},  {64, 32, 4},  {64, 16, 4}};

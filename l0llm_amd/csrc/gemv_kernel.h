@@ -16,11 +16,12 @@
 // counter waits for exactly the item being computed (a conditional load, or a use of a load
 // issued after the prefetch, would make that wait cover the prefetched item too).
 //
-// Activations are staged once per block in LDS as fp32, with the RMSNorm prologue applied there
-// when fused. Every wave issues its activation loads, then the block meets at a barrier before
-// the first weight item is requested: a CU's memory pipeline returns data in order, so the
-// activations come back ahead of the weight stream and are staged while it is in flight; the
-// staging barriers wait on LDS only, never on the weight loads. Dequantisation
+// Activations are staged once per block in LDS as fp32, times the RMSNorm weights when the norm is
+// fused (its scale, one scalar per row, multiplies the row sums in the epilogue). Every wave
+// issues its activation loads, then the block meets at a barrier before the first weight item is
+// requested: a CU's memory pipeline returns data in order, so the activations come back ahead of
+// the weight stream and are staged while it is in flight; the staging barrier waits on LDS only,
+// never on the weight loads. Dequantisation
 // happens in registers (int8: bytes biased by +128 and converted with v_cvt_f32_ubyteN; the bias
 // is removed chunk by chunk: the dot product of every 16-byte chunk starts from -128 times the
 // sum of its 16 activations, staged in LDS next to them, so the accumulator only ever holds
@@ -63,27 +64,6 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-}
-
-// Block-wide sums of two values in one exchange (all threads of a kBlock block must call it);
-// LDS-only barriers (see lds_barrier).
-__device__ __forceinline__ float2 block_sum2(float a, float b, float* red) {
-    a = wave_sum(a);
-    b = wave_sum(b);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    lds_barrier();
-    if (lane == 0) {
-        red[wave] = a;
-        red[kWaves + wave] = b;
-    }
-    lds_barrier();
-    float2 t = make_float2(0.f, 0.f);
-#pragma unroll
-    for (int i = 0; i < kWaves; i++) {
-        t.x += red[i];
-        t.y += red[kWaves + i];
-    }
-    return t;
 }
 
 template <int WT>
@@ -357,10 +337,12 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p, int
     load_w(wa, g, 0);
 
     // ---- stage the one activation row (and RMSNorm) in LDS ----
+    // RMSNorm: x * w goes to LDS at once; the row's scale 1 / rms(x), one scalar, multiplies the
+    // row sums in the epilogue. Each wave leaves the sum of squares of its chunks (x is fp32 here:
+    // 4 values per chunk, matching the 4 norm weights) in `red`, and the barrier that publishes the
+    // staged row publishes those too, so no block reduction waits before the stream starts.
+    float norm_scale = 1.f;
     if constexpr (MR == 1) {
-        // RMSNorm: the sum of squares of the row (x is fp32 here: 4 values per chunk, matching
-        // the 4 norm weights); then x * scale * w goes to LDS.
-        float scale = 1.f;
         if constexpr (NORM) {
             float ss = 0.f;
 #pragma unroll
@@ -372,8 +354,8 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p, int
                     for (int e = 0; e < 4; e++) ss += f[e] * f[e];
                 }
             }
-            // LDS-only barriers inside: the first weight item stays in flight.
-            scale = rsqrtf(block_sum2(ss, 0.f, red).x / (float)K + p.eps);
+            ss = wave_sum(ss);
+            if (lane == 0) red[wave] = ss;
         }
 #pragma unroll
         for (int i = 0; i < KX; i++) {
@@ -381,10 +363,10 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p, int
             float f[8];
             const int n = chunk_to_float(xr[i], xdt, f);
             if constexpr (NORM) {
-                f[0] *= scale * __uint_as_float(nr[i].x);
-                f[1] *= scale * __uint_as_float(nr[i].y);
-                f[2] *= scale * __uint_as_float(nr[i].z);
-                f[3] *= scale * __uint_as_float(nr[i].w);
+                f[0] *= __uint_as_float(nr[i].x);
+                f[1] *= __uint_as_float(nr[i].y);
+                f[2] *= __uint_as_float(nr[i].z);
+                f[3] *= __uint_as_float(nr[i].w);
             }
             if (idx < nxc) {
 #pragma unroll
@@ -423,6 +405,12 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p, int
         }
     }
     lds_barrier();
+    if constexpr (NORM && MR == 1) {  // the waves' sums of squares in a fixed order
+        float t = 0.f;
+#pragma unroll
+        for (int i = 0; i < kWaves; i++) t += red[i];
+        norm_scale = rsqrtf(t / (float)K + p.eps);
+    }
 
     // ---- stream: no barrier below this point, waves run independently ----
     float acc[MR][R];
@@ -472,6 +460,7 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p, int
 #pragma unroll
             for (int r = 0; r < R; r++) {
                 sums[mr][r] = wave_sum(acc[mr][r]);
+                if constexpr (NORM) sums[mr][r] *= norm_scale;
                 acc[mr][r] = 0.f;
             }
         if constexpr (EPI == EPI_STORE) {
