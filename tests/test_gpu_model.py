@@ -183,9 +183,12 @@ def test_tall_prefill_eight_wave_tiles_match_decode(device, precision, tol, toke
     """599 prefill rows at hidden 4096, intermediate 8192: the int8 GEMMs take the eight-wave
     128-row tiles (gate|up one-step stages; down, K = 8192, two-step stages with K split in four).
     2047 rows: q|k|v (N = 6144) and gate|up (N = 16384, SwiGLU epilogue) take the 256 x 256 blocks
-    with a ragged last row block, O and down the 128-row tiles. For bf16 weights gate|up and down
-    (N = 16384, K = 8192) take the two-operand LDS tiles at both lengths. Measured deviations on
-    MI355X: int8 7.6e-4 / 7.0e-4, bf16 4.3e-3 / 4.9e-3 of max |logit| (600 / 2048 tokens)."""
+    with a ragged last row block, O and down the 128-row tiles. For bf16 weights all four GEMMs
+    take the two-operand LDS-ring tiles: at 599 rows O and down with K split in two (the split-K
+    sum carries the residual), at 2047 rows without a split, so the kernel's own LDS-staged
+    epilogue stores q|k|v, adds O and down to the residual and applies SwiGLU to gate|up. Measured
+    deviations on MI355X: int8 7.6e-4 / 7.0e-4, bf16 4.3e-3 / 4.9e-3 of max |logit| (600 / 2048
+    tokens)."""
     cfg = l0.HfConfig(hidden_size=4096, intermediate_size=8192, num_layers=1, num_attention_heads=32,
                       num_key_value_heads=8, head_dim=128, vocab_size=256, max_position_embeddings=4096,
                       rms_norm_eps=1e-5, rope_theta=500000.0)
