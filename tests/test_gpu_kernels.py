@@ -396,14 +396,17 @@ def test_recording_matches_eager_and_replays(device, suite):
 
 # ---- MFMA prefill GEMM -------------------------------------------------------------------------
 
-# Stages of two K steps (K % 64 == 0), one K step (K % 64 == 32: (96, 300, 160)), the 128 x 64
-# wave tile (512 x 16384), K splits, ragged M / N, the any-shape fallback (K % 32 != 0), the
-# 256 x 256 eight-wave blocks with a ragged last row block (1030 x 10240 x 256); the two-operand
-# LDS tiles (M >= 256 with N >= 16384 or K >= 8192): ragged rows and an odd stage count
-# (300 x 16384 x 320), a ragged column block with K = 8192 (260 x 640 x 8192).
+# gemm_nk_kernel: stages of two K steps (K % 64 == 0), one K step (K % 64 == 32: (96, 300, 160)),
+# K splits, ragged M / N, the any-shape fallback (K % 32 != 0), and from 256 rows the shapes whose
+# LDS-ring plan would leave less than 1024 of K per split (512 x 2048 x 2048, 512 x 1024 x 256,
+# 260 x 640 x 8192); its eight-wave and 256 x 256 tiles run in the int8 test below. The two-operand
+# LDS-ring tiles (M >= 256, K a multiple of 64): 128 x 256 blocks with ragged rows and an odd stage
+# count (300 x 16384 x 320) and with a ragged last row block (1030 x 10240 x 256), and 256 x 128
+# blocks with a ragged last column block whose width (16102) leaves rows that are not 16-byte
+# aligned, so the epilogue stores element by element there (300 x 16102 x 512).
 @pytest.mark.parametrize("m,n,k", [(64, 256, 512), (128, 3072, 2048), (512, 2048, 2048), (100, 200, 128),
                                    (128, 64, 8192), (33, 40, 70), (96, 300, 160), (512, 1024, 256),
-                                   (1030, 10240, 256), (300, 16384, 320), (260, 640, 8192)])
+                                   (1030, 10240, 256), (300, 16384, 320), (300, 16102, 512), (260, 640, 8192)])
 @pytest.mark.parametrize("dtype", [l0.BF16, l0.F16])
 def test_gemm_nk_matches_oracle(device, suite, m, n, k, dtype):
     rng = np.random.default_rng(m + n + k)
