@@ -105,9 +105,13 @@ __global__ void kv_store_kernel(const float* k, const float* v, void* kc, void* 
     }
 }
 
-__global__ void embedding_kernel(const int* ids, const float* table, float* out, int h, size_t n) {
+// Also clears `clear[0 .. nclear)` (the decode step's per-layer range flags: the embedding is the
+// step's first kernel).
+__global__ void embedding_kernel(const int* ids, const float* table, float* out, int h, size_t n, unsigned* clear,
+                                 int nclear) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) out[i] = table[(size_t)ids[i / h] * h + i % h];
+    if (i < (size_t)nclear) clear[i] = 0u;
 }
 
 __global__ void copy_kernel(const float* src, float* dst, size_t n) {
@@ -301,9 +305,11 @@ int launch_kv_store(hipStream_t s, const float* k, const float* v, void* kc, voi
     return launch_status("kv_store");
 }
 
-int launch_embedding(hipStream_t s, const int* ids, const float* table, float* out, int h, size_t n) {
-    if (n == 0) return L0H_OK;
-    embedding_kernel<<<ceil_div(n, kBlock), kBlock, 0, s>>>(ids, table, out, h, n);
+int launch_embedding(hipStream_t s, const int* ids, const float* table, float* out, int h, size_t n, unsigned* clear,
+                     int nclear) {
+    if (n == 0 && nclear <= 0) return L0H_OK;
+    const size_t threads = std::max(n, (size_t)std::max(nclear, 0));
+    embedding_kernel<<<ceil_div(threads, kBlock), kBlock, 0, s>>>(ids, table, out, h, n, clear, clear ? nclear : 0);
     return launch_status("embedding");
 }
 

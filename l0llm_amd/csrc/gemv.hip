@@ -65,6 +65,20 @@ int launch_gemv_nk(hipStream_t s, const GemvParams& p0) {
     // Per activation row: the fp32 tile, plus one int8 bias term per 16 values.
     const size_t row_tile = (k_pad_max + (p0.w_dtype == L0H_I8PC ? k_pad_max / 16 : 0)) * sizeof(float);
     const bool fits = row_tile <= kLdsBudget;
+    if (p0.y16 && (!p0.range_flag || p0.epilogue != EPI_SWIGLU))
+        return fail(L0H_ERR_INVALID_ARG, "a 16-bit copy of the output is written by the SwiGLU epilogue, with its range flag");
+    if (p0.x_wide) {  // a 16-bit row with an fp32 twin: the fast kernel chooses between them
+        if (!p0.range_flag || p0.norm_w || fused || p0.m != 1 || p0.x_dtype == L0H_F32)
+            return fail(L0H_ERR_INVALID_ARG, "an fp32 twin row needs its range flag, one 16-bit row and no fused epilogue");
+        if (!aligned || !fits || p0.k % 16 || ((uintptr_t)p0.x_wide & 15)) {  // other kernels read the twin itself
+            GemvParams p = p0;
+            p.x = p0.x_wide;
+            p.x_dtype = L0H_F32;
+            p.x_wide = nullptr;
+            p.range_flag = nullptr;
+            return launch_gemv_nk(s, p);
+        }
+    }
     if (fused) {
         if (!aligned || !fits || p0.m != 1 || p0.x_dtype != L0H_F32 || (p0.epilogue != EPI_STORE && !p0.norm_w) ||
             (p0.epilogue == EPI_QKV && (p0.rotary_dim > 2 * kMaxRotaryHalf || p0.rotary_dim < 2)))

@@ -306,6 +306,10 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p, int
     }
 
     // ---- one activation row: prologue loads first (x, norm weights, RoPE frequencies) ----
+    // A 16-bit row with an fp32 twin (p.x_wide) whose writer flagged a value beyond the 16-bit
+    // range is staged from the twin instead; the flag is read alongside the row's loads, so the
+    // common case waits for nothing more.
+    const unsigned wide = (MR == 1 && p.x_wide) ? *p.range_flag : 0u;
     uint4 xr[KX], nr[NORM ? KX : 1];
     const int xdt = p.x_dtype;
     const int nxc = (int)((size_t)K * dtype_size(xdt) / 16);  // 16-byte chunks of x
@@ -357,36 +361,51 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p, int
             ss = wave_sum(ss);
             if (lane == 0) red[wave] = ss;
         }
-#pragma unroll
-        for (int i = 0; i < KX; i++) {
-            const int idx = i * kBlock + tid;
-            float f[8];
-            const int n = chunk_to_float(xr[i], xdt, f);
-            if constexpr (NORM) {
-                f[0] *= __uint_as_float(nr[i].x);
-                f[1] *= __uint_as_float(nr[i].y);
-                f[2] *= __uint_as_float(nr[i].z);
-                f[3] *= __uint_as_float(nr[i].w);
-            }
-            if (idx < nxc) {
-#pragma unroll
-                for (int e = 0; e < 8; e++)
-                    if (e < n) xs[idx * n + e] = f[e];
-            }
-            if constexpr (WT == L0H_I8PC) {
-                // A weight chunk covers 16 activations: 4 fp32 or 2 16-bit activation chunks, held
-                // by that many adjacent lanes (every lane takes part in the DPP sum).
+        if (wide) {
+            // the fp32 twin, in groups of 16 values (K % 16 == 0 where a twin is given)
+            const float4* xw = reinterpret_cast<const float4*>(p.x_wide);
+            for (int g16 = tid; g16 < K / 16; g16 += kBlock) {
                 float cs = 0.f;
 #pragma unroll
-                for (int e = 0; e < 8; e++)
-                    if (e < n) cs += f[e];
-                cs = idx < nxc ? cs : 0.f;
-                if (xdt == L0H_F32) {
-                    cs = lane_group_sum<4>(cs);
-                    if (idx < nxc && (idx & 3) == 0) xc[idx >> 2] = -128.0f * cs;
-                } else {
-                    cs = lane_group_sum<2>(cs);
-                    if (idx < nxc && (idx & 1) == 0) xc[idx >> 1] = -128.0f * cs;
+                for (int q = 0; q < 4; q++) {
+                    const float4 v = xw[g16 * 4 + q];
+                    *reinterpret_cast<float4*>(xs + g16 * 16 + 4 * q) = v;
+                    cs += (v.x + v.y) + (v.z + v.w);
+                }
+                if constexpr (WT == L0H_I8PC) xc[g16] = -128.0f * cs;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < KX; i++) {
+                const int idx = i * kBlock + tid;
+                float f[8];
+                const int n = chunk_to_float(xr[i], xdt, f);
+                if constexpr (NORM) {
+                    f[0] *= __uint_as_float(nr[i].x);
+                    f[1] *= __uint_as_float(nr[i].y);
+                    f[2] *= __uint_as_float(nr[i].z);
+                    f[3] *= __uint_as_float(nr[i].w);
+                }
+                if (idx < nxc) {
+#pragma unroll
+                    for (int e = 0; e < 8; e++)
+                        if (e < n) xs[idx * n + e] = f[e];
+                }
+                if constexpr (WT == L0H_I8PC) {
+                    // A weight chunk covers 16 activations: 4 fp32 or 2 16-bit activation chunks, held
+                    // by that many adjacent lanes (every lane takes part in the DPP sum).
+                    float cs = 0.f;
+#pragma unroll
+                    for (int e = 0; e < 8; e++)
+                        if (e < n) cs += f[e];
+                    cs = idx < nxc ? cs : 0.f;
+                    if (xdt == L0H_F32) {
+                        cs = lane_group_sum<4>(cs);
+                        if (idx < nxc && (idx & 3) == 0) xc[idx >> 2] = -128.0f * cs;
+                    } else {
+                        cs = lane_group_sum<2>(cs);
+                        if (idx < nxc && (idx & 1) == 0) xc[idx >> 1] = -128.0f * cs;
+                    }
                 }
             }
         }
@@ -491,9 +510,14 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p, int
                     }
                     v0 += sd.b0;
                     v1 += sd.b1;
-                    if constexpr (EPI == EPI_SWIGLU)
-                        store_act(p.y, p.y_dtype, (size_t)(row >> 1), silu(v0) * v1);
-                    else
+                    if constexpr (EPI == EPI_SWIGLU) {
+                        const float o = silu(v0) * v1;
+                        store_act(p.y, p.y_dtype, (size_t)(row >> 1), o);
+                        if (p.y16) {  // the 16-bit copy; a value it cannot hold flags the row
+                            store_act_sat(p.y16, L0H_F16, (size_t)(row >> 1), o);
+                            if (!(fabsf(o) <= 65504.f)) *p.range_flag = 1u;
+                        }
+                    } else
                         qkv_pair(p, row, v0, v1, pos, rope_cs, rope_sn);
                 }
             }

@@ -31,6 +31,12 @@ struct GemvParams {
     const float* bias = nullptr;  // [N] in stored row order
     void* y = nullptr;            // STORE / SWIGLU output
     int y_dtype = L0H_F32;
+    // SWIGLU: also write y as fp16 into y16 (saturated), and set *range_flag when a value leaves
+    // fp16's range (or is NaN). A reader of that row (x = the fp16 copy, x_wide = the fp32 row,
+    // no RMSNorm) stages x_wide instead when *range_flag is set.
+    void* y16 = nullptr;
+    unsigned* range_flag = nullptr;
+    const float* x_wide = nullptr;
     float* resid = nullptr;       // RESIDUAL
     // QKV epilogue: rows [0, q_dim) are q, [q_dim, q_dim+kv_dim) k, then v. Within every q and k
     // head the rows are stored RoPE-paired: row 2i <-> dim i, row 2i+1 <-> dim i + rot/2
@@ -86,8 +92,9 @@ int launch_rope(hipStream_t s, float* q, float* k, const int* positions, const f
                 int rotary_dim);
 int launch_kv_store(hipStream_t s, const float* k, const float* v, void* kc, void* vc,
                     int cache_dtype, const int* pos_device, int pos0, int kv_dim, int tokens);
+// Gathers the rows of `ids` (n = rows * h values); also zeroes clear[0 .. nclear).
 int launch_embedding(hipStream_t s, const int* ids, const float* table, float* out, int h,
-                     size_t n);
+                     size_t n, unsigned* clear = nullptr, int nclear = 0);
 int launch_copy(hipStream_t s, const float* src, float* dst, size_t n);
 // Greedy argmax (first maximal index). `partials` holds 2*blocks words; `ticket` one counter.
 // When feed_token/feed_pos/out_list are set, the chosen id is also written to *feed_token,

@@ -150,6 +150,11 @@ struct l0h_model {
     float* inv_freq = nullptr;
     // activations
     float *hidden = nullptr, *q = nullptr, *attn = nullptr, *act = nullptr, *logits = nullptr;
+    // The SwiGLU output's fp16 copy, which down stages unless its layer's flag says a value of the
+    // row is beyond fp16's range (then down stages `act`); the flags are cleared by the step's
+    // first kernel. Not used for fp32 storage or an intermediate size that is not a multiple of 16.
+    uint16_t* act16 = nullptr;
+    unsigned* range_flags = nullptr;
     int *token = nullptr, *position = nullptr, *sampled = nullptr, *step = nullptr, *out_list = nullptr;
     int out_capacity = 0;
     // workspaces
@@ -369,10 +374,12 @@ double op_bytes(const l0h_model* m, int kind, int position) {
     case L0H_KERNEL_QKV: return gemv_bytes(m, m->qd + 2 * m->kvd, c.hidden_size, 8.0 * H + 4.0 * qd + 2.0 * kvd * ci);
     case L0H_KERNEL_ATTENTION: return 2.0 * (position + 1) * kvd * ci + (4.0 + dtype_size(m->attn_dtype)) * qd;
     case L0H_KERNEL_O_PROJ: return gemv_bytes(m, c.hidden_size, m->qd, dtype_size(m->attn_dtype) * qd + 8.0 * H);
-    case L0H_KERNEL_GATE_UP:
-        return gemv_bytes(m, 2 * c.intermediate_size, c.hidden_size, 8.0 * H + dtype_size(m->act_dtype) * I);
-    case L0H_KERNEL_DOWN:
-        return gemv_bytes(m, c.hidden_size, c.intermediate_size, dtype_size(m->act_dtype) * I + 8.0 * H);
+    case L0H_KERNEL_GATE_UP:  // + the fp16 copy of the output
+        return gemv_bytes(m, 2 * c.intermediate_size, c.hidden_size,
+                          8.0 * H + (dtype_size(m->act_dtype) + (m->act16 ? 2 : 0)) * (double)I);
+    case L0H_KERNEL_DOWN:  // reads the fp16 copy (the fp32 row only after a flagged step)
+        return gemv_bytes(m, c.hidden_size, c.intermediate_size,
+                          (m->act16 ? 2.0 : (double)dtype_size(m->act_dtype)) * I + 8.0 * H);
     case L0H_KERNEL_LM_HEAD: return gemv_bytes(m, c.vocab_size, c.hidden_size, 8.0 * H + 4.0 * c.vocab_size);
     default: return 4.0 * c.vocab_size;  // argmax reads the logits
     }
@@ -390,7 +397,8 @@ int launch_op(l0h_model* m, hipStream_t s, int kind, int li) {
     g.compute_units = m->dev->compute_units;
     switch (kind) {
     case L0H_KERNEL_EMBEDDING:  // LlmModel.cs:424
-        return launch_embedding(s, m->token, m->embedding, m->hidden, H, (size_t)H);
+        return launch_embedding(s, m->token, m->embedding, m->hidden, H, (size_t)H, m->range_flags,
+                                m->range_flags ? c.num_layers : 0);
     case L0H_KERNEL_QKV: {  // LlmDecoderLayer.cs:167, :296-322
         Layer& L = m->layers[li];
         g.w = L.qkv.w;
@@ -460,6 +468,10 @@ int launch_op(l0h_model* m, hipStream_t s, int kind, int li) {
         g.epilogue = EPI_SWIGLU;
         g.y = m->act;
         g.y_dtype = m->act_dtype;
+        if (m->act16) {
+            g.y16 = m->act16;
+            g.range_flag = m->range_flags + li;
+        }
         return launch_gemv_nk(s, g);
     }
     case L0H_KERNEL_DOWN: {  // LlmDecoderLayer.cs:190-194
@@ -470,6 +482,12 @@ int launch_op(l0h_model* m, hipStream_t s, int kind, int li) {
         g.k = c.intermediate_size;
         g.x = m->act;
         g.x_dtype = m->act_dtype;
+        if (m->act16) {  // the fp16 copy, or `act` where the flag is set
+            g.x = m->act16;
+            g.x_dtype = L0H_F16;
+            g.x_wide = m->act;
+            g.range_flag = m->range_flags + li;
+        }
         g.epilogue = EPI_RESIDUAL;
         g.resid = m->hidden;
         return launch_gemv_nk(s, g);
@@ -935,6 +953,11 @@ int l0h_model_create(l0h_device* dev, const l0h_model_config* cfg, int precision
     if ((st = alloc_t(m, (size_t)m->qd, &m->q))) return bail(st);
     if ((st = alloc_t(m, (size_t)m->qd, &m->attn))) return bail(st);
     if ((st = alloc_t(m, (size_t)I, &m->act))) return bail(st);
+    if (storage != L0H_F32 && I % 16 == 0) {
+        if ((st = alloc_t(m, (size_t)I, &m->act16))) return bail(st);
+        if ((st = alloc_t(m, (size_t)c.num_layers, &m->range_flags))) return bail(st);
+        if ((st = l0h_fill_zero(dev, m->range_flags, (size_t)c.num_layers * sizeof(unsigned)))) return bail(st);
+    }
     if ((st = alloc_t(m, (size_t)c.vocab_size, &m->logits))) return bail(st);
     if ((st = alloc_t(m, 4, &m->token))) return bail(st);
     m->position = m->token + 1;
