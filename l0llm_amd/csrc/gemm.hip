@@ -324,6 +324,26 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(1, 2))
 // of a ds_read_b128 pass hit distinct banks.
 __device__ __forceinline__ int lds_swz(int r) { return (r ^ (r >> 3)) & 7; }
 
+// int8 weight rows in LDS: 64 bytes (4 chunks of 16) per row; chunk c of tile row r sits in slot
+// c ^ lds_swz8(r). A fragment read takes 8 bytes of one chunk from 32 consecutive rows; over any 16
+// consecutive rows the (row mod 4, slot) pairs are distinct, so 16 lanes' 8-byte reads hit distinct
+// banks.
+__device__ __forceinline__ int lds_swz8(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+
+// 8 int8 values (bytes of lo, then hi) -> 8 exact fp16 in the same order: byte u = q + 128 (sign bit
+// flipped) placed under the fp16 exponent of 1024 (v_perm_b32) reads as 1024 + u, and a packed add
+// of -1152 leaves q.
+__device__ __forceinline__ uint4 i8x8_to_f16_ordered(uint32_t lo, uint32_t hi) {
+    lo ^= 0x80808080u;
+    hi ^= 0x80808080u;
+    const __half2 off = __builtin_bit_cast(__half2, 0xE480E480u);  // (-1152, -1152)
+    auto cv = [&](uint32_t src, uint32_t sel) {
+        const uint32_t w = __builtin_amdgcn_perm(0x64646464u, src, sel);
+        return __builtin_bit_cast(uint32_t, __hadd2(__builtin_bit_cast(__half2, w), off));
+    };
+    return make_uint4(cv(lo, 0x04010400u), cv(lo, 0x04030402u), cv(hi, 0x04010400u), cv(hi, 0x04030402u));
+}
+
 // 16 bytes per lane from sbase + voff into LDS bytes lds + 16 * lane (global_load_lds_dwordx4; the
 // LDS address comes from M0). Written as assembly so the compiler, which cannot tell which LDS
 // bytes such a load writes, does not wait for every one in flight before each LDS read: the ring
@@ -432,18 +452,23 @@ __device__ __forceinline__ void store4(int epi, float* partial, int bz, void* Y,
 // stage t is exact.
 template <int WT, int BM, int BN, int WGM, int WGN, int NS>
 __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(WGM * WGN / 4, WGM * WGN / 4))) void gemm_dma_kernel(
-    int M, int N, int K, int k_per_split, const uint16_t* __restrict__ X, const void* __restrict__ Wv, void* Y,
-    int y_dtype, int epi, float* partial) {
-    static_assert(WT == L0H_BF16 || WT == L0H_F16, "16-bit weights");
+    int M, int N, int K, int k_per_split, const uint16_t* __restrict__ X, const void* __restrict__ Wv,
+    const uint16_t* __restrict__ scales, void* Y, int y_dtype, int epi, float* partial) {
+    constexpr bool I8 = WT == L0H_I8PC;
+    static_assert(WT == L0H_BF16 || WT == L0H_F16 || I8, "16-bit or int8 weights");
+    constexpr int DT = I8 ? L0H_F16 : WT;     // MFMA operand type (int8 weights: fp16 activations)
     constexpr int SK = 64;
-    constexpr int ROWB = SK * 2;               // bytes per LDS row
-    constexpr int STAGE = (BM + BN) * ROWB;    // bytes per stage
+    constexpr int ROWA = SK * 2;               // bytes per LDS row of A
+    constexpr int ROWB = I8 ? SK : SK * 2;     // bytes per LDS row of B
+    constexpr int RPB = 1024 / ROWB;           // B rows per 1 KiB load (8, or 16 for int8)
+    constexpr int STAGE = BM * ROWA + BN * ROWB;  // bytes per stage
     constexpr int NW = WGM * WGN;              // waves
     constexpr int NT = 64 * NW;                // threads
     constexpr int TM = BM / WGM, TN = BN / WGN;
     constexpr int FI = TM / 32, FJ = TN / 32;
-    constexpr int DA = BM / 8 / NW, D = (BM + BN) / 8 / NW;  // loads per wave per stage (A, all)
-    static_assert(FI >= 1 && FJ >= 1 && DA >= 1 && DA * NW * 8 == BM && D * NW * 8 == BM + BN, "tile shape");
+    constexpr int GA = BM / 8, GB = BN / RPB;  // 1 KiB loads per stage of A and B
+    constexpr int DA = GA / NW, D = (GA + GB) / NW;  // loads per wave per stage (A, all)
+    static_assert(FI >= 1 && FJ >= 1 && DA >= 1 && DA * NW == GA && D * NW == GA + GB, "tile shape");
     static_assert(NS >= 2 && (NS - 2) * D < 64, "ring depth");
     extern __shared__ uint4 gemm_dma_smem[];
     const char* lds = reinterpret_cast<const char*>(gemm_dma_smem);
@@ -467,24 +492,34 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
     const int last = max(nsteps - 1, 0);
 
     // This lane's source offset (bytes from the stage's K column) for each of the wave's loads:
-    // group g = wave + NW d holds tile rows 8 g' .. 8 g' + 7 of A (g' = g) or of B (g' = g - BM / 8);
-    // lane l fills slot l % 8 of row 8 g' + l / 8, which holds chunk (l % 8) ^ lds_swz(row).
+    // load g = wave + NW d fills the g-th KiB of the stage. A: tile rows 8 g .. 8 g + 7, lane l
+    // fills slot l % 8 of row 8 g + l / 8, which holds chunk (l % 8) ^ lds_swz(row). B (g' = g - GA):
+    // 16-bit rows as A; int8 rows 16 g' .. 16 g' + 15, lane l fills slot l % 4 of row 16 g' + l / 4,
+    // which holds chunk (l % 4) ^ lds_swz8(row).
+    constexpr uint32_t WB = I8 ? 1 : 2;  // bytes per weight
     uint32_t voff[D];
 #pragma unroll
     for (int d = 0; d < D; d++) {
         const int g = wave + NW * d;
-        const int gl = d < DA ? g : g - BM / 8;
-        const int r = 8 * gl + lane / 8;
-        const int row = d < DA ? min(m0 + r, M - 1) : min(n0 + r, N - 1);
-        voff[d] = (uint32_t)row * (uint32_t)K * 2u + (uint32_t)(((lane & 7) ^ lds_swz(r)) * 16);
+        if (d < DA) {
+            const int r = 8 * g + lane / 8;
+            voff[d] = (uint32_t)min(m0 + r, M - 1) * (uint32_t)K * 2u + (uint32_t)(((lane & 7) ^ lds_swz(r)) * 16);
+        } else if constexpr (I8) {
+            const int r = 16 * (g - GA) + lane / 4;
+            voff[d] = (uint32_t)min(n0 + r, N - 1) * (uint32_t)K + (uint32_t)(((lane & 3) ^ lds_swz8(r)) * 16);
+        } else {
+            const int r = 8 * (g - GA) + lane / 8;
+            voff[d] = (uint32_t)min(n0 + r, N - 1) * (uint32_t)K * 2u + (uint32_t)(((lane & 7) ^ lds_swz(r)) * 16);
+        }
     }
-    const uint16_t* xa = X + kbeg;
-    const uint16_t* wb = static_cast<const uint16_t*>(Wv) + kbeg;
+    const char* xa = reinterpret_cast<const char*>(X + kbeg);
+    const char* wb = static_cast<const char*>(Wv) + (size_t)kbeg * WB;
     auto issue = [&](int t, int buf) {
         const int k0 = min(t, last) * SK;
         const uint32_t base = lds0 + (uint32_t)(buf * STAGE + wave * 1024);
 #pragma unroll
-        for (int d = 0; d < D; d++) dma16(d < DA ? (const void*)(xa + k0) : (const void*)(wb + k0), voff[d], base + d * NW * 1024);
+        for (int d = 0; d < D; d++)
+            dma16(d < DA ? (const void*)(xa + 2 * k0) : (const void*)(wb + WB * k0), voff[d], base + d * NW * 1024);
     };
 
     acc_t<32> acc[FI][FJ];
@@ -504,21 +539,27 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
     // keeps the compiler from hoisting all four substeps' reads.
     auto compute = [&](int buf) {
         const char* sa = lds + buf * STAGE;
-        const char* sb = sa + BM * ROWB;
+        const char* sb = sa + BM * ROWA;
         uint4 a0[FI], b0[FJ], a1[FI], b1[FJ];
         auto frags = [&](uint4 (&a)[FI], uint4 (&b)[FJ], int s) {
 #pragma unroll
             for (int i = 0; i < FI; i++)
-                a[i] = *reinterpret_cast<const uint4*>(sa + ar[i] * ROWB + (((2 * s + hi) ^ lds_swz(ar[i])) << 4));
+                a[i] = *reinterpret_cast<const uint4*>(sa + ar[i] * ROWA + (((2 * s + hi) ^ lds_swz(ar[i])) << 4));
 #pragma unroll
-            for (int j = 0; j < FJ; j++)
-                b[j] = *reinterpret_cast<const uint4*>(sb + br[j] * ROWB + (((2 * s + hi) ^ lds_swz(br[j])) << 4));
+            for (int j = 0; j < FJ; j++) {
+                if constexpr (I8) {  // K values 16 s + 8 hi .. + 7: half hi of chunk s
+                    const uint2 q = *reinterpret_cast<const uint2*>(sb + br[j] * ROWB + ((s ^ lds_swz8(br[j])) << 4) + 8 * hi);
+                    b[j] = i8x8_to_f16_ordered(q.x, q.y);
+                } else {
+                    b[j] = *reinterpret_cast<const uint4*>(sb + br[j] * ROWB + (((2 * s + hi) ^ lds_swz(br[j])) << 4));
+                }
+            }
         };
         auto mma = [&](const uint4 (&a)[FI], const uint4 (&b)[FJ]) {
 #pragma unroll
             for (int i = 0; i < FI; i++)
 #pragma unroll
-                for (int j = 0; j < FJ; j++) acc[i][j] = mfma<WT, 32>(a[i], b[j], acc[i][j]);
+                for (int j = 0; j < FJ; j++) acc[i][j] = mfma<DT, 32>(a[i], b[j], acc[i][j]);
         };
         frags(a0, b0, 0);
         for_each_index<SK / 16>([&](auto sc) {
@@ -557,14 +598,16 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
     constexpr int LDT = BN + 8;  // 4 rows apart = 128 bytes mod 256: the two half-waves' rows use distinct banks
     lds_barrier();               // every wave is done reading the stages
 #pragma unroll
-    for (int i = 0; i < FI; i++)
+    for (int j = 0; j < FJ; j++) {
+        const int c = wn * TN + j * 32 + lane % 32;
+        // int8: the weight row's scale (output column c)
+        const float sc = I8 ? __half2float(__ushort_as_half(scales[min(n0 + c, N - 1)])) : 1.f;
 #pragma unroll
-        for (int j = 0; j < FJ; j++) {
-            const int c = wn * TN + j * 32 + lane % 32;
+        for (int i = 0; i < FI; i++)
 #pragma unroll
             for (int r = 0; r < 16; r++)
-                tile[(wm * TM + i * 32 + (r / 4) * 8 + (lane / 32) * 4 + (r % 4)) * LDT + c] = acc[i][j][r];
-        }
+                tile[(wm * TM + i * 32 + (r / 4) * 8 + (lane / 32) * 4 + (r % 4)) * LDT + c] = I8 ? acc[i][j][r] * sc : acc[i][j][r];
+    }
     lds_barrier();
     constexpr int C4 = BN / 4, RPP = NT / C4;  // threads per row, rows per pass
     static_assert(NT % C4 == 0 && BM % RPP == 0, "epilogue pass shape");
@@ -736,9 +779,11 @@ bool lds_plan_for(int dtype, int m, int n, int k, int cus, LdsPlan& out) {
         const char* e = std::getenv("L0H_GEMM_LDS");  // 0: never, 2: every shape it supports (tuning)
         return e ? std::atoi(e) : 1;
     }();
-    // int8 weights stay on gemm_nk_kernel: their conversion on the way into LDS made the 8B
-    // prefill slower (0.044 against 0.041 s for 2048 tokens).
-    if (!mode || dtype == L0H_I8PC || m < 256 || k % 64) return false;
+    static const int i8_mode = [] {  // tuning: 0 keeps int8 weights on gemm_nk_kernel
+        const char* e = std::getenv("L0H_GEMM_LDS_I8");
+        return e ? std::atoi(e) : 1;
+    }();
+    if (!mode || (dtype == L0H_I8PC && !i8_mode) || m < 256 || k % 64) return false;
     if ((size_t)std::max(m, n) * k * 2 >= (1ull << 32)) return false;  // the LDS-direct loads take 32-bit offsets
     static const int tiles[][2] = {{128, 256}, {256, 128}, {128, 128}};
     const size_t want = (size_t)std::max(cus, 1) * 3 / 4;
@@ -763,10 +808,10 @@ bool lds_plan_for(int dtype, int m, int n, int k, int cus, LdsPlan& out) {
 constexpr size_t dma_tile_bytes(int bm, int bn) { return (size_t)bm * (bn + 8) * sizeof(float); }
 
 template <int WT, int BM, int BN, int WGM, int WGN>
-int launch_lds(hipStream_t s, int m, int n, int k, const void* x, const void* w, void* y, int y_dtype, int epi,
-               int splits, float* ws) {
+int launch_lds(hipStream_t s, int m, int n, int k, const void* x, const void* w, const uint16_t* scales, void* y,
+               int y_dtype, int epi, int splits, float* ws) {
     constexpr int NT = 64 * WGM * WGN;
-    constexpr size_t stage = (size_t)(BM + BN) * 128;
+    constexpr size_t stage = (size_t)BM * 128 + (size_t)BN * (WT == L0H_I8PC ? 64 : 128);
     constexpr int kMaxNs = 160 * 1024 / stage >= 4 ? 4 : 3;
     static const int ns_env = [] {
         const char* e = std::getenv("L0H_GEMM_LDS_STAGES");  // tuning: LDS ring depth, 2 .. 4
@@ -784,7 +829,7 @@ int launch_lds(hipStream_t s, int m, int n, int k, const void* x, const void* w,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
         if (attr != hipSuccess) return fail(L0H_ERR_DEVICE, std::string("hipFuncSetAttribute: ") + hipGetErrorString(attr));
         gemm_dma_kernel<WT, BM, BN, WGM, WGN, NS><<<grid, NT, bytes, s>>>(
-            m, n, k, k_per_split, static_cast<const uint16_t*>(x), w, y, y_dtype, epi, splits > 1 ? ws : nullptr);
+            m, n, k, k_per_split, static_cast<const uint16_t*>(x), w, scales, y, y_dtype, epi, splits > 1 ? ws : nullptr);
         return L0H_OK;
     };
     int st = ns == 2   ? launch(std::integral_constant<int, 2>{})
@@ -799,11 +844,13 @@ int launch_lds(hipStream_t s, int m, int n, int k, const void* x, const void* w,
 }
 
 template <int WT>
-int launch_lds_plan(hipStream_t s, const LdsPlan& p, int m, int n, int k, const void* x, const void* w, void* y,
-                    int y_dtype, int epi, float* ws) {
-    if (p.bm == 128 && p.bn == 256) return launch_lds<WT, 128, 256, 2, 4>(s, m, n, k, x, w, y, y_dtype, epi, p.splits, ws);
-    if (p.bm == 256 && p.bn == 128) return launch_lds<WT, 256, 128, 4, 2>(s, m, n, k, x, w, y, y_dtype, epi, p.splits, ws);
-    return launch_lds<WT, 128, 128, 2, 2>(s, m, n, k, x, w, y, y_dtype, epi, p.splits, ws);
+int launch_lds_plan(hipStream_t s, const LdsPlan& p, int m, int n, int k, const void* x, const void* w,
+                    const uint16_t* scales, void* y, int y_dtype, int epi, float* ws) {
+    if (p.bm == 128 && p.bn == 256)
+        return launch_lds<WT, 128, 256, 2, 4>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws);
+    if (p.bm == 256 && p.bn == 128)
+        return launch_lds<WT, 256, 128, 4, 2>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws);
+    return launch_lds<WT, 128, 128, 2, 2>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws);
 }
 
 template <int WT>
@@ -860,8 +907,11 @@ int launch_gemm_nk(hipStream_t s, int dtype, int m, int n, int k, const void* x,
     LdsPlan lp;
     if (lds_plan_for(dtype, m, n, k, cus, lp)) {
         while (lp.splits > 1 && (size_t)lp.splits * m * n * sizeof(float) > ws_bytes) lp.splits /= 2;
-        return dtype == L0H_BF16 ? launch_lds_plan<L0H_BF16>(s, lp, m, n, k, x, w, y, y_dtype, epilogue, ws)
-                                 : launch_lds_plan<L0H_F16>(s, lp, m, n, k, x, w, y, y_dtype, epilogue, ws);
+        switch (dtype) {
+        case L0H_BF16: return launch_lds_plan<L0H_BF16>(s, lp, m, n, k, x, w, nullptr, y, y_dtype, epilogue, ws);
+        case L0H_F16: return launch_lds_plan<L0H_F16>(s, lp, m, n, k, x, w, nullptr, y, y_dtype, epilogue, ws);
+        default: return launch_lds_plan<L0H_I8PC>(s, lp, m, n, k, x, w, scales, y, y_dtype, epilogue, ws);
+        }
     }
     Plan p = plan_for(m, n, k, cus);
     while (p.splits > 1 && (size_t)p.splits * m * n * sizeof(float) > ws_bytes) p.splits /= 2;

@@ -423,9 +423,12 @@ def test_gemm_nk_matches_oracle(device, suite, m, n, k, dtype):
     assert rel_err(yb.read().reshape(m, n), want) < 2e-5
 
 
+# gemm_nk_kernel (K splits, small and ragged shapes; with K = 32 mod 64, which the LDS ring does not
+# take, its 256 x 256 tile at 1030 x 10240 x 480 and its eight-wave 128-row tile at 520 x 16384 x
+# 480) and the LDS-ring kernel with int8 rows (1030 x 10240 x 512, 520 x 16384 x 448).
 @pytest.mark.parametrize("m,n,k", [(64, 256, 512), (256, 768, 4096), (256, 512, 14336), (100, 200, 128),
                                    (33, 48, 96), (128, 2048, 1024), (512, 320, 2048), (1030, 10240, 512),
-                                   (260, 384, 8192), (520, 16384, 448)])
+                                   (1030, 10240, 480), (260, 384, 8192), (520, 16384, 448), (520, 16384, 480)])
 def test_gemm_nk_i8pc_matches_oracle(device, suite, m, n, k):
     """int8 weights converted to fp16 in registers (exact), fp16 activations, fp32 accumulation,
     row scale in the epilogue: the oracle's int8 per-channel product on the same fp16 inputs."""
