@@ -1,7 +1,7 @@
 // GQA decode attention over the KV cache for gfx950 (Attention.Execute / ExecutePrefill,
 // LlmDecoderLayer.cs:325-327, :369-371).
 //
-// Split-K over the sequence ("flash decoding"): block (split, kv head, batch) reads its slice of
+// Split-K over the sequence ("flash decoding"): block (kv head, split, batch) reads its slice of
 // the K and V rows of one kv head once and serves all the q heads of that group from it.
 // Layout: cache [batch, max_seq, n_kv * head_dim] (LlmKvCache.cs:5-8). A lane owns 8 dims of a
 // row (one 16-byte fp16 load, two for fp32), head_dim / 8 lanes cover a row, so a wave
@@ -108,8 +108,9 @@ __host__ __device__ constexpr int partial_stride(int G, int HD) { return G * HD 
 // Sequence length of batch entry b, and this split's slice [lo, lo + n) of it. Slices are whole
 // steps (NG * kUnroll positions) so a block's slots stay in step.
 template <int NG>
-__device__ __forceinline__ void split_range(const AttnParams& p, int seq_len_step, int b, int split, int& lo, int& n) {
-    int len = (p.seq_len_device ? *p.seq_len_device + p.seq_len_add : p.seq_len) + b * seq_len_step;
+__device__ __forceinline__ void split_range(const AttnParams& p, int seq_len_step, int b, int split, int& lo, int& n,
+                                            int& len) {
+    len = (p.seq_len_device ? *p.seq_len_device + p.seq_len_add : p.seq_len) + b * seq_len_step;
     len = max(0, min(len, p.max_seq_len));
     constexpr int kStep = NG * kUnroll;
     int chunk = (len + p.splits - 1) / p.splits;
@@ -120,8 +121,9 @@ __device__ __forceinline__ void split_range(const AttnParams& p, int seq_len_ste
 
 // QT: q dtype, G: q heads per kv head rounded up to a power of two (heads >= p.nh / p.nkv are
 // computed on clamped inputs and not written). SC: the reduce-scattered softmax where the shape
-// allows it (head_dim 128, four heads per kv head).
-template <int HD, int CT, int QT, int G, bool SC = false>
+// allows it (head_dim 128, four heads per kv head). SHORT: every slice is at most two steps long
+// (the launch checks max_seq_len against the split count).
+template <int HD, int CT, int QT, int G, bool SC = false, bool SHORT = false>
 __global__ __launch_bounds__(kBlock) void attn_split_kernel(const AttnParams p, int seq_len_step,
                                                             size_t cache_batch_stride) {
     constexpr int LPP = HD / 8;     // lanes per position
@@ -133,15 +135,15 @@ __global__ __launch_bounds__(kBlock) void attn_split_kernel(const AttnParams p, 
     __shared__ float s_m[NSL][G], s_l[NSL][G], s_c[NSL][G], s_M[G];
     __shared__ float s_acc[NSL][G][HD];
 
-    const int split = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+    const int g = blockIdx.x, split = blockIdx.y, b = blockIdx.z;
     const int gsize = p.nh / p.nkv;
     const int kv_dim = p.nkv * HD;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lg = lane % LPP;
     const int slot = wave * PPW + lane / LPP;
-    int lo, n;
-    split_range<NG>(p, seq_len_step, b, split, lo, n);
+    int lo, n, len;
+    split_range<NG>(p, seq_len_step, b, split, lo, n, len);
 
     // q: this lane's 8 dims of every head of the group, scaled by log2(e) / sqrt(HD).
     float qr[G][8];
@@ -150,12 +152,19 @@ __global__ __launch_bounds__(kBlock) void attn_split_kernel(const AttnParams p, 
     for (int h = 0; h < G; h++) {
         const int hh = min(h, gsize - 1);
         load8<QT>(p.q, (size_t)b * p.nh * HD + (size_t)(g * gsize + hh) * HD + lg * 8, qr[h]);
-#pragma unroll
-        for (int d = 0; d < 8; d++) qr[h][d] *= qscale;
     }
+    auto scale_q = [&] {
+#pragma unroll
+        for (int h = 0; h < G; h++)
+#pragma unroll
+            for (int d = 0; d < 8; d++) qr[h][d] *= qscale;
+    };
+    if constexpr (!SHORT) scale_q();
     const T* kbase = static_cast<const T*>(p.kc) + (size_t)b * cache_batch_stride + (size_t)g * HD + lg * 8;
     const T* vbase = static_cast<const T*>(p.vc) + (size_t)b * cache_batch_stride + (size_t)g * HD + lg * 8;
-    const int last = p.max_seq_len - 1;
+    // Positions past the slice read the last written row (masked in the softmax, weight exactly 0),
+    // never a row of the cache that may not have been written (its bits could be Inf or NaN).
+    const int last = max(len - 1, 0);
 
     CacheRow<CT> ka[U], va[U], kb[U], vb[U];
     auto load = [&](CacheRow<CT> (&k)[U], CacheRow<CT> (&v)[U], int step) {
@@ -305,9 +314,25 @@ __global__ __launch_bounds__(kBlock) void attn_split_kernel(const AttnParams p, 
     };
 
     // Steps of NG * U positions; the next step's rows are requested before the current one is
-    // computed, and the last step is computed with nothing issued behind it.
+    // computed, and the last step is computed with nothing issued behind it. SHORT (slices of at
+    // most two steps, chosen by the launch): straight-line code that requests both steps, with q,
+    // before computing either. The loop below would take two memory round trips in a row there:
+    // the compiler's copy of the first step's rows into the loop registers waits for all of them
+    // before the second step is requested. A second step past the slice is fully masked (every
+    // weight is exactly 0, no running maximum moves), so computing it changes no bit.
     const int steps = (n + NG * U - 1) / (NG * U);  // block-uniform
-    if (steps > 0) {
+    if constexpr (SHORT) {
+        load(ka, va, 0);
+        load(kb, vb, 1);
+        // Nothing moves above this point: left alone, the scheduler scales q (waiting for it) before
+        // requesting most of the rows.
+        __builtin_amdgcn_sched_barrier(0);
+        scale_q();
+        if (steps > 0) {
+            compute(ka, va, 0);
+            compute(kb, vb, 1);
+        }
+    } else if (steps > 0) {
         load(ka, va, 0);
         int s = 0;
         for (;;) {
@@ -390,7 +415,7 @@ __global__ __launch_bounds__(kBlock) void attn_split_kernel(const AttnParams p, 
     }
 }
 
-// Log-sum-exp merge of the splits' partials. Block (column group, kv head, batch): thread
+// Log-sum-exp merge of the splits' partials. Block (kv head, column group, batch): thread
 // (column c of 4 dims, lane j of J) loads the max, sum and 4 accumulators of splits j, j + J, ...
 // in one round (eight splits in flight), folds them with an online max, and the J lanes of a
 // column are combined in a fixed order.
@@ -402,9 +427,9 @@ __global__ __launch_bounds__(kBlock) void attn_merge_kernel(const AttnParams p) 
     constexpr int PS = partial_stride(G, HD);
     __shared__ float s_mx[J][CB], s_den[J][CB];
     __shared__ float4 s_num[J][CB];
-    const int g = blockIdx.y, b = blockIdx.z;
+    const int g = blockIdx.x, b = blockIdx.z;
     const int tid = threadIdx.x, cl = tid % CB, j = tid / CB;
-    const int c = blockIdx.x * CB + cl;
+    const int c = blockIdx.y * CB + cl;
     const int cc = min(c, NC - 1);
     const int h = cc * 4 / HD;
     const int gsize = p.nh / p.nkv;
@@ -480,27 +505,39 @@ __global__ __launch_bounds__(kBlock) void attn_merge_kernel(const AttnParams p) 
 
 template <int HD, int CT, int QT, int G>
 int launch_g(hipStream_t s, const AttnParams& p, int seq_len_step, size_t cache_batch_stride) {
-    dim3 grid(p.splits, p.nkv, p.batch);
+    // The kv head is the fastest-varying block index in both kernels: workgroups are dealt to the
+    // XCDs round robin by linear id, so with 8 kv heads every split of head g and the merge blocks
+    // that read its partials run on XCD g, and the merge finds the partials in that XCD's L2.
+    dim3 grid(p.nkv, p.splits, p.batch);
     // The reduce-scattered softmax has fewer VALU operations but longer dependent chains per step.
     // Measured on the 8B shapes: faster for short splits (decode at 2048 positions: 10.4 against
     // 10.9 us per layer; up to 256 positions per split) and for long ones at two blocks per CU
     // (batch 8 x 32768: 183 against 192 us), 3-4 % slower at one block per CU with 512-1024
     // positions per split (batch 1 x 32768, batch 8 x 4096), where one wave per SIMD cannot hide
     // those chains.
-    if constexpr (HD == 128 && G == 4) {
+    // Slices of at most two steps (at any sequence length up to max_seq_len) take the straight-line
+    // kernel; fp16 caches only (two steps of fp32 rows spill with eight heads). Measured on the 8B
+    // shapes: 512 positions 8.9 -> 7.9 us at batch 1 and 10.5 -> 9.5 us at batch 8, 4096 positions
+    // at batch 1 10.5 -> 9.5-9.8 us.
+    constexpr int kStep = (kWaves * 64 / (HD / 8)) * kUnroll;  // positions per step
+    constexpr bool SC = HD == 128 && G == 4;
+    bool short_slices = false;
+    if constexpr (CT == L0H_F16) {
+        short_slices = (int)ceil_div(p.max_seq_len, std::max(p.splits, 1)) <= 2 * kStep;
+        if (short_slices)
+            attn_split_kernel<HD, CT, QT, G, SC, true><<<grid, kBlock, 0, s>>>(p, seq_len_step, cache_batch_stride);
+    }
+    if (!short_slices) {
         const int per_split = p.max_seq_len / std::max(p.splits, 1);
-        if (per_split <= 256 || per_split >= 2048) {
-            attn_split_kernel<HD, CT, QT, G, true><<<grid, kBlock, 0, s>>>(p, seq_len_step, cache_batch_stride);
-        } else {
+        if (SC && (per_split <= 256 || per_split >= 2048))
+            attn_split_kernel<HD, CT, QT, G, SC><<<grid, kBlock, 0, s>>>(p, seq_len_step, cache_batch_stride);
+        else
             attn_split_kernel<HD, CT, QT, G, false><<<grid, kBlock, 0, s>>>(p, seq_len_step, cache_batch_stride);
-        }
-    } else {
-        attn_split_kernel<HD, CT, QT, G><<<grid, kBlock, 0, s>>>(p, seq_len_step, cache_batch_stride);
     }
     int st = launch_status("attention");
     if (st || p.splits == 1) return st;
     constexpr int NC = G * HD / 4, CB = NC < 32 ? NC : 32;
-    attn_merge_kernel<HD, G><<<dim3(NC / CB, p.nkv, p.batch), kBlock, 0, s>>>(p);
+    attn_merge_kernel<HD, G><<<dim3(p.nkv, NC / CB, p.batch), kBlock, 0, s>>>(p);
     return launch_status("attention merge");
 }
 

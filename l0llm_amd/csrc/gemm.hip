@@ -783,8 +783,20 @@ bool lds_plan_for(int dtype, int m, int n, int k, int cus, LdsPlan& out) {
         const char* e = std::getenv("L0H_GEMM_LDS_I8");
         return e ? std::atoi(e) : 1;
     }();
-    if (!mode || (dtype == L0H_I8PC && !i8_mode) || m < 256 || k % 64) return false;
+    static const LdsPlan forced = [] {  // tuning: "bm,bn,splits" for every shape the kernel takes
+        LdsPlan f{0, 0, 1};
+        if (const char* e = std::getenv("L0H_GEMM_LDS_PLAN")) std::sscanf(e, "%d,%d,%d", &f.bm, &f.bn, &f.splits);
+        const bool tile = (f.bm == 128 && (f.bn == 128 || f.bn == 256)) || (f.bm == 256 && f.bn == 128);
+        if (!tile || f.splits < 1 || f.splits > kMaxSplits || (f.splits & (f.splits - 1))) f.bm = 0;
+        return f;
+    }();
+    if (!mode || (dtype == L0H_I8PC && !i8_mode) || k % 64) return false;
     if ((size_t)std::max(m, n) * k * 2 >= (1ull << 32)) return false;  // the LDS-direct loads take 32-bit offsets
+    if (forced.bm && k / forced.splits >= 8 * 64) {
+        out = forced;
+        return true;
+    }
+    if (m < 256) return false;
     static const int tiles[][2] = {{128, 256}, {256, 128}, {128, 128}};
     const size_t want = (size_t)std::max(cus, 1) * 3 / 4;
     auto blocks = [&](int bm, int bn) { return (size_t)ceil_div(m, bm) * ceil_div(n, bn); };

@@ -14,6 +14,9 @@
 // and replayed (the reference records one command list per token); the argmax can feed the
 // chosen token and the next position back on the device for back-to-back greedy decode.
 #include <algorithm>
+#include <array>
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -387,13 +390,33 @@ double op_bytes(const l0h_model* m, int kind, int position) {
 
 bool per_layer_kind(int kind) { return kind >= L0H_KERNEL_QKV && kind <= L0H_KERNEL_DOWN; }
 
+// GEMV blocks per CU of a decode-step kind (2 unless L0H_GEMV_BPC_KINDS = "qkv,o,gate_up,down,lm_head"
+// sets them, for tuning sweeps; L0H_GEMV_BLOCKS_PER_CU still overrides every launch).
+int step_blocks_per_cu(int kind) {
+    static const std::array<int, 8> per = [] {
+        std::array<int, 8> a;
+        a.fill(2);
+        if (const char* e = std::getenv("L0H_GEMV_BPC_KINDS")) {
+            int v[5];
+            if (std::sscanf(e, "%d,%d,%d,%d,%d", &v[0], &v[1], &v[2], &v[3], &v[4]) == 5) {
+                const int kinds[5] = {L0H_KERNEL_QKV, L0H_KERNEL_O_PROJ, L0H_KERNEL_GATE_UP, L0H_KERNEL_DOWN,
+                                      L0H_KERNEL_LM_HEAD};
+                for (int i = 0; i < 5; i++)
+                    if (v[i] >= 1 && v[i] <= 8) a[kinds[i]] = v[i];
+            }
+        }
+        return a;
+    }();
+    return kind >= 0 && kind < 8 ? per[kind] : 2;
+}
+
 // Enqueues one kernel of the decode step (layer li for the per-layer kinds).
 int launch_op(l0h_model* m, hipStream_t s, int kind, int li) {
     const auto& c = m->cfg;
     const int H = c.hidden_size;
     GemvParams g;
     g.w_dtype = m->storage;
-    g.max_blocks = gemv_max_blocks(m->dev->compute_units);
+    g.max_blocks = gemv_max_blocks(m->dev->compute_units, step_blocks_per_cu(kind));
     g.compute_units = m->dev->compute_units;
     switch (kind) {
     case L0H_KERNEL_EMBEDDING:  // LlmModel.cs:424

@@ -295,6 +295,33 @@ def test_attention_decode_matches_oracle(device, suite, hd, nh, nkv, seq, cache)
     np.testing.assert_array_equal(ob.read(), out)
 
 
+# Sequences far shorter than max_seq_len: most splits get an empty slice and the last non-empty one
+# a partial step. Cache rows at and past seq_len hold NaN: a kernel that read any of them (even with
+# a softmax weight of 0) would return NaN. Head dim 128 / 64 and 64 / 32 positions per step, fp16
+# caches on the straight-line kernel for slices of at most two steps (max_seq 2078 and 1000: 17 and
+# 8 splits), fp32 and long slices on the looped one.
+SHORT_ATTN = [(128, 32, 8, 70, 2078, l0.F16), (128, 32, 8, 1, 2078, l0.F16), (128, 32, 8, 2049, 2078, l0.F16),
+              (64, 16, 2, 300, 1000, l0.F16), (128, 32, 8, 70, 2078, l0.F32), (128, 32, 8, 5000, 40000, l0.F16)]
+
+
+@pytest.mark.parametrize("hd,nh,nkv,seq,max_seq,cache", SHORT_ATTN)
+def test_attention_decode_reads_only_written_rows(device, suite, hd, nh, nkv, seq, max_seq, cache):
+    rng = np.random.default_rng(seq + max_seq)
+    kf = rng.normal(0, 1, (max_seq, nkv * hd)).astype(np.float32)
+    vf = rng.normal(0, 1, (max_seq, nkv * hd)).astype(np.float32)
+    kf[seq:] = np.nan
+    vf[seq:] = np.nan
+    q = rng.normal(0, 1, nh * hd).astype(np.float32)
+    kc, vc = (kf, vf) if cache == l0.F32 else (kf.astype(np.float16).view(np.uint16), vf.astype(np.float16).view(np.uint16))
+    want = orc.attention_decode(q, kc, vc, cache, hd, nh, nkv, seq, max_seq)
+    assert np.all(np.isfinite(want))
+    ob = device.alloc(nh * hd * 4)
+    suite.attention_execute(up(device, q), up(device, kc), up(device, vc), ob, hd, nh, nkv, seq, max_seq, cache_dtype=cache)
+    out = ob.read()
+    assert np.all(np.isfinite(out))
+    assert rel_err(out, want) < 1e-4, rel_err(out, want)
+
+
 @pytest.mark.parametrize("batch,seq", [(8, 512), (1, 32768), (8, 8192)])
 def test_attention_decode_batched_fp16(device, suite, batch, seq):
     """GQA 32q/8kv/128, fp16 q/K/V, fp16 out, fp32 softmax. Splits of 128 (8 x 512) and 2048
