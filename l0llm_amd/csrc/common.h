@@ -142,4 +142,16 @@ __device__ __forceinline__ uint4 ld_nt16(const void* p) {
 
 inline unsigned ceil_div(size_t a, size_t b) { return (unsigned)((a + b - 1) / b); }
 
+// Greedy argmax key of logit v at index idx: unsigned order = larger value first, then the smaller
+// index (the first maximum, LlmAbstractions.cs:83-90).
+__device__ __forceinline__ unsigned long long greedy_key(float v, int idx) {
+    uint32_t b = __float_as_uint(v);
+    b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((unsigned long long)b << 32) | (0xffffffffu - (uint32_t)idx);
+}
+
+__device__ __forceinline__ unsigned long long greedy_max(unsigned long long a, unsigned long long b) {
+    return a > b ? a : b;
+}
+
 }  // namespace l0h

@@ -145,30 +145,35 @@ __global__ void fill_kernel(float* dst, float value, size_t n) {
 }
 
 // ---- greedy argmax --------------------------------------------------------------------------
-// Key order: larger value first, then smaller index (first maximum, LlmAbstractions.cs:83-90).
-__device__ __forceinline__ unsigned long long argmax_key(float v, int idx) {
-    uint32_t b = __float_as_uint(v);
-    b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-    return ((unsigned long long)b << 32) | (0xffffffffu - (uint32_t)idx);
-}
-
-__device__ __forceinline__ unsigned long long max_u64(unsigned long long a, unsigned long long b) {
-    return a > b ? a : b;
-}
+// Keys: greedy_key (larger value first, then the smaller index).
 
 __device__ unsigned long long block_max_key(unsigned long long key, unsigned long long* red) {
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) key = max_u64(key, __shfl_xor(key, off, 64));
+    for (int off = 32; off > 0; off >>= 1) key = greedy_max(key, __shfl_xor(key, off, 64));
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     __syncthreads();
     if (lane == 0) red[wave] = key;
     __syncthreads();
     unsigned long long t = red[0];
-    for (int i = 1; i < (int)(blockDim.x >> 6); i++) t = max_u64(t, red[i]);
+    for (int i = 1; i < (int)(blockDim.x >> 6); i++) t = greedy_max(t, red[i]);
     return t;
 }
 
 constexpr int kArgmaxPerBlock = 4096;
+
+// The sampled index of key `best`, and the device-side feedback of a greedy loop: next token,
+// recorded ids, position + 1.
+__device__ void write_sample(unsigned long long best, int* sampled, const ArgmaxFeed& feed) {
+    const int idx = (int)(0xffffffffu - (uint32_t)(best & 0xffffffffull));
+    *sampled = idx;
+    if (feed.token) *feed.token = idx;
+    if (feed.out_list) {
+        const int s = *feed.step;
+        if (s >= 0 && s < feed.capacity) feed.out_list[s] = idx;
+        *feed.step = s + 1;
+    }
+    if (feed.position) *feed.position += 1;
+}
 
 __global__ __launch_bounds__(kBlock) void argmax_kernel(const float* logits, int vocab, int* sampled,
                                                         unsigned long long* partials,
@@ -178,7 +183,7 @@ __global__ __launch_bounds__(kBlock) void argmax_kernel(const float* logits, int
     const int begin = blockIdx.x * kArgmaxPerBlock;
     const int end = min(vocab, begin + kArgmaxPerBlock);
     unsigned long long key = 0ull;
-    for (int i = begin + threadIdx.x; i < end; i += kBlock) key = max_u64(key, argmax_key(logits[i], i));
+    for (int i = begin + threadIdx.x; i < end; i += kBlock) key = greedy_max(key, greedy_key(logits[i], i));
     key = block_max_key(key, red);
     if (threadIdx.x == 0) {
         __hip_atomic_store(&partials[blockIdx.x], key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -191,20 +196,23 @@ __global__ __launch_bounds__(kBlock) void argmax_kernel(const float* logits, int
     __threadfence();
     unsigned long long best = 0ull;
     for (int b = threadIdx.x; b < (int)gridDim.x; b += kBlock)
-        best = max_u64(best, __hip_atomic_load(&partials[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        best = greedy_max(best, __hip_atomic_load(&partials[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
     best = block_max_key(best, red);
     if (threadIdx.x == 0) {
-        const int idx = (int)(0xffffffffu - (uint32_t)(best & 0xffffffffull));
-        *sampled = idx;
-        if (feed.token) *feed.token = idx;
-        if (feed.out_list) {
-            const int s = *feed.step;
-            if (s >= 0 && s < feed.capacity) feed.out_list[s] = idx;
-            *feed.step = s + 1;
-        }
-        if (feed.position) *feed.position += 1;
+        write_sample(best, sampled, feed);
         *ticket = 0u;  // ready for the next launch (graph replay)
     }
+}
+
+// The argmax over per-wave keys that the lm_head GEMV wrote (one block): the largest key, then the
+// same outputs and device-side feedback as argmax_kernel.
+__global__ __launch_bounds__(kBlock) void argmax_keys_kernel(const unsigned long long* keys, int count, int* sampled,
+                                                             ArgmaxFeed feed) {
+    __shared__ unsigned long long red[kBlock / 64];
+    unsigned long long best = 0ull;
+    for (int i = threadIdx.x; i < count; i += kBlock) best = greedy_max(best, keys[i]);
+    best = block_max_key(best, red);
+    if (threadIdx.x == 0) write_sample(best, sampled, feed);
 }
 
 // ---- random initialisation (synthetic weights) ---------------------------------------------
@@ -340,6 +348,12 @@ int launch_argmax(hipStream_t s, const float* logits, int vocab, int* sampled,
     if (vocab <= 0) return fail(L0H_ERR_INVALID_ARG, "vocab must be positive");
     argmax_kernel<<<argmax_blocks(vocab), kBlock, 0, s>>>(logits, vocab, sampled, partials, ticket, feed);
     return launch_status("argmax");
+}
+
+int launch_argmax_keys(hipStream_t s, const unsigned long long* keys, int count, int* sampled, const ArgmaxFeed& feed) {
+    if (count <= 0) return fail(L0H_ERR_INVALID_ARG, "argmax key count must be positive");
+    argmax_keys_kernel<<<1, kBlock, 0, s>>>(keys, count, sampled, feed);
+    return launch_status("argmax keys");
 }
 
 int launch_init_normal(hipStream_t s, void* dst, int dtype, size_t count, uint64_t seed, float stddev) {

@@ -86,8 +86,10 @@ int launch_gemv_nk(hipStream_t s, const GemvParams& p0) {
                         "fused GEMV needs one fp32 activation row with the RMSNorm prologue, K a multiple of the "
                         "load width and a zero-padded row that fits the LDS tile (16384 values)");
     }
+    if (p0.argmax_keys && (p0.m != 1 || p0.epilogue != EPI_STORE))
+        return fail(L0H_ERR_INVALID_ARG, "per-wave argmax keys need one activation row and the store epilogue");
     if (!aligned || !fits) {
-        if (fused) return fail(L0H_ERR_UNSUPPORTED, "fused GEMV shape not supported");
+        if (fused || p0.argmax_keys) return fail(L0H_ERR_UNSUPPORTED, "fused GEMV shape not supported");
         GemvParams p = p0;
         const size_t tasks = (size_t)p.m * p.n;
         gemv_nk_generic_kernel<<<ceil_div(tasks, kWaves), kBlock, 0, s>>>(p);

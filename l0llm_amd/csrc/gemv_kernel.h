@@ -470,6 +470,8 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p, int
         }
     };
 
+    // Largest greedy key of the values this lane stored (argmax_keys, one activation row).
+    unsigned long long best = 0ull;
     // Wave reduction and epilogue of row group `group`; resets the accumulators. No loads.
     auto finish = [&](int group, const Side& sd) {
         const int r0 = group * R;
@@ -492,10 +494,13 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p, int
                         float v = sums[mr][r];
                         if constexpr (WT == L0H_I8PC) v *= half_bits(sd.s0);
                         v += sd.b0;
-                        if (p.epilogue == EPI_STORE)
+                        if (p.epilogue == EPI_STORE) {
                             store_act(p.y, p.y_dtype, (size_t)mr * N + row, v);
-                        else
+                            if constexpr (MR == 1)
+                                if (p.argmax_keys) best = greedy_max(best, greedy_key(v, row));
+                        } else {
                             p.resid[(size_t)mr * N + row] = sd.res + v;
+                        }
                     }
                 }
         } else {
@@ -574,6 +579,13 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p, int
             }
         }
     }
+    if constexpr (MR == 1 && EPI == EPI_STORE) {
+        if (p.argmax_keys) {  // every wave of the grid writes its key (0 when it stored nothing)
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) best = greedy_max(best, __shfl_xor(best, off, 64));
+            if (lane == 0) p.argmax_keys[(size_t)blockIdx.x * kWaves + wave] = best;
+        }
+    }
 }
 
 // Zero-padded activation tile of the fast kernel: K rounded up to whole batches.
@@ -618,6 +630,7 @@ int launch_fast(hipStream_t s, const GemvParams& p) {
         const unsigned cap = std::min<unsigned>((unsigned)p.max_blocks, (unsigned)(occ_blocks * std::max(1, p.compute_units)));
         grid = std::min(grid, cap);
     }
+    if (p.launched_waves) *p.launched_waves = (int)(grid * kWaves);
     kern<<<grid, kBlock, shmem, s>>>(p, k_pad);
     return launch_status("gemv_nk");
 }

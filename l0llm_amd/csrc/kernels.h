@@ -53,6 +53,11 @@ struct GemvParams {
     // loop over the row groups (activations staged once per block).
     int max_blocks = 0;
     int compute_units = 0;  // with max_blocks: caps the grid at the blocks resident in one round
+    // EPI_STORE with one activation row: every wave also writes the greedy key (greedy_key) of the
+    // largest value it stored to argmax_keys[wave of the grid], so an argmax needs only those keys;
+    // launched_waves (host memory) receives the launch's wave count.
+    unsigned long long* argmax_keys = nullptr;
+    int* launched_waves = nullptr;
 };
 
 // Persistent-grid size for weight-streaming kernels on a device with `compute_units` CUs:
@@ -107,6 +112,8 @@ struct ArgmaxFeed {
     int capacity = 0;  // entries of out_list; later steps are not recorded
 };
 int argmax_blocks(int vocab);
+// Argmax over `count` per-wave keys written by a GEMV with argmax_keys set (one block).
+int launch_argmax_keys(hipStream_t s, const unsigned long long* keys, int count, int* sampled, const ArgmaxFeed& feed);
 int launch_argmax(hipStream_t s, const float* logits, int vocab, int* sampled,
                   unsigned long long* partials, unsigned* ticket, const ArgmaxFeed& feed);
 

@@ -9,7 +9,8 @@
 //   4. gate|up GEMV (rows interleaved) with the post-attention RMSNorm in its prologue and
 //      SwiGLU in its epilogue                            (:183-189)
 //   5. down GEMV, epilogue hidden += y                   (:190-194)
-// then the final RMSNorm fused into the lm_head GEMV and a one-launch greedy argmax. The
+// then the final RMSNorm fused into the lm_head GEMV, whose epilogue also keeps each wave's
+// greedy key (largest logit, first index), and a one-block argmax over those keys. The
 // token and position live in device memory, so the whole step is captured once as a HIP graph
 // and replayed (the reference records one command list per token); the argmax can feed the
 // chosen token and the next position back on the device for back-to-back greedy decode.
@@ -164,6 +165,10 @@ struct l0h_model {
     float* attn_partials = nullptr;
     unsigned long long* argmax_partials = nullptr;
     unsigned* argmax_ticket = nullptr;
+    // Greedy keys the lm_head GEMV writes, one per wave of its grid (lm_waves, set when the lm_head
+    // launch is enqueued; 0 before), so the argmax reads those keys instead of the logits.
+    unsigned long long* lm_keys = nullptr;
+    int lm_waves = 0;
     int attn_splits = 1;
     // chunked prefill (allocated on first use): rows of up to pf_cap tokens
     int prefill_chunk = 0;  // tokens per chunk: 2048, or L0H_PREFILL_CHUNK (tuning, tests)
@@ -384,7 +389,7 @@ double op_bytes(const l0h_model* m, int kind, int position) {
         return gemv_bytes(m, c.hidden_size, c.intermediate_size,
                           (m->act16 ? 2.0 : (double)dtype_size(m->act_dtype)) * I + 8.0 * H);
     case L0H_KERNEL_LM_HEAD: return gemv_bytes(m, c.vocab_size, c.hidden_size, 8.0 * H + 4.0 * c.vocab_size);
-    default: return 4.0 * c.vocab_size;  // argmax reads the logits
+    default: return m->lm_waves > 0 ? 8.0 * m->lm_waves : 4.0 * c.vocab_size;  // argmax: keys or logits
     }
 }
 
@@ -526,6 +531,8 @@ int launch_op(l0h_model* m, hipStream_t s, int kind, int li) {
         g.epilogue = EPI_STORE;
         g.y = m->logits;
         g.y_dtype = L0H_F32;
+        g.argmax_keys = m->lm_keys;
+        g.launched_waves = &m->lm_waves;
         return launch_gemv_nk(s, g);
     default: {  // LlmModel.cs:398, plus device-side feedback for back-to-back decode
         ArgmaxFeed feed;
@@ -534,6 +541,9 @@ int launch_op(l0h_model* m, hipStream_t s, int kind, int li) {
         feed.step = m->step;
         feed.out_list = m->out_list;
         feed.capacity = m->out_capacity;
+        // The lm_head launch before this one left one greedy key per wave: reduce those (one block)
+        // rather than re-read the logits.
+        if (m->lm_waves > 0) return launch_argmax_keys(s, m->lm_keys, m->lm_waves, m->sampled, feed);
         return launch_argmax(s, m->logits, c.vocab_size, m->sampled, m->argmax_partials, m->argmax_ticket, feed);
     }
     }
@@ -997,6 +1007,8 @@ int l0h_model_create(l0h_device* dev, const l0h_model_config* cfg, int precision
     a.splits = m->attn_splits;
     if ((st = alloc_owned(m, attention_partials_bytes(a), reinterpret_cast<void**>(&m->attn_partials)))) return bail(st);
     if ((st = alloc_t(m, (size_t)argmax_blocks(c.vocab_size), &m->argmax_partials))) return bail(st);
+    // at most one wave per row group of two rows (the GEMV's smallest), plus a block's spare waves
+    if ((st = alloc_t(m, (size_t)c.vocab_size / 2 + 8, &m->lm_keys))) return bail(st);
     if ((st = alloc_t(m, 1, &m->argmax_ticket))) return bail(st);
     if ((st = l0h_fill_zero(dev, m->argmax_ticket, sizeof(unsigned)))) return bail(st);
     const int zeros[4] = {0, 0, 0, 0};
