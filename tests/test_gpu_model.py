@@ -344,6 +344,41 @@ def test_random_int8_model_matches_oracle(device, hf, steps):
             tok = onext
 
 
+# hidden 256 (16 int8 chunks a row: 8-row groups), vocabulary 5003: the lm_head GEMV spreads the
+# rows over ~600 waves, each keeping the greedy key of its own rows.
+TIES = l0.HfConfig(hidden_size=256, intermediate_size=512, num_layers=1, num_attention_heads=4,
+                   num_key_value_heads=2, head_dim=64, vocab_size=5003, max_position_embeddings=4096,
+                   rms_norm_eps=1e-6, rope_theta=10000.0)
+
+
+@pytest.mark.parametrize("negated", [0, 1700])
+def test_greedy_ties_take_the_first_index(device, negated):
+    """Exact ties across the waves of the lm_head GEMV: every lm_head row is the same vector (the
+    first `negated` rows its negation), so thousands of logits are bit-for-bit equal. The device's
+    greedy pick (per-wave keys reduced by one block) is the first index of the largest logit, as
+    the reference's argmax (LlmAbstractions.cs:83-90) and numpy's."""
+    rng = np.random.default_rng(7)
+    row = rng.normal(0, 0.05, TIES.hidden_size).astype(np.float32)
+    w = np.tile(row, (TIES.vocab_size, 1))
+    w[:negated] = -row
+    prompt = [5, 17, 300]
+    with _random_model(device, TIES, 32, seed=3) as m:
+        m.set_tensor("lm_head.weight", w)
+        logits = m.prefill(prompt)
+        first = int(np.argmax(logits))
+        assert np.count_nonzero(logits == logits[first]) > 1000  # a tie over many waves
+        assert first in (0, negated)
+        assert m.generate_greedy(prompt, 1) == [first]
+        m.prefill(prompt)
+        dev = m.decode_greedy_device(first, 4).tolist()
+        m.prefill(prompt)
+        loop, tok = [], first
+        for _ in range(4):
+            tok = int(np.argmax(m.decode(tok)))
+            loop.append(tok)
+        assert dev == loop
+
+
 def test_odd_shapes_chunked_prefill_matches_decode(device, monkeypatch):
     """The odd-shaped model in 64-token chunks (the MFMA GEMM at its smallest M, with the K = 320
     and 960 rows and the 448-row q|k|v, then a 21-token chunk on the multi-row GEMV)."""
