@@ -440,6 +440,13 @@ __device__ __forceinline__ void store4(int epi, float* partial, int bz, void* Y,
     }
 }
 
+// The LDS ring's epilogue stages the fp32 output tile (rows padded by 8 floats) in LDS: in one pass,
+// or in two passes of BM / 2 rows where the whole tile does not fit the 160 KiB (256 x 256 blocks).
+constexpr int dma_epi_passes(int bm, int bn) { return (size_t)bm * (bn + 8) * sizeof(float) > 160 * 1024 ? 2 : 1; }
+constexpr size_t dma_tile_bytes(int bm, int bn) {
+    return (size_t)(bm / dma_epi_passes(bm, bn)) * (bn + 8) * sizeof(float);
+}
+
 // Y[M, N] = X[M, K] W[N, K]^T for 16-bit operands, K a multiple of 64. Block tile BM x BN, waves
 // WGM x WGN with a (BM / WGM) x (BN / WGN) tile each of 32 x 32 x 16 MFMAs. K advances in stages of
 // 64 through NS LDS buffers: at stage t every wave waits for its own loads of stage t, the block
@@ -596,27 +603,35 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
     // per lane spread over two rows).
     float* tile = reinterpret_cast<float*>(gemm_dma_smem);
     constexpr int LDT = BN + 8;  // 4 rows apart = 128 bytes mod 256: the two half-waves' rows use distinct banks
-    lds_barrier();               // every wave is done reading the stages
-#pragma unroll
-    for (int j = 0; j < FJ; j++) {
-        const int c = wn * TN + j * 32 + lane % 32;
-        // int8: the weight row's scale (output column c)
-        const float sc = I8 ? __half2float(__ushort_as_half(scales[min(n0 + c, N - 1)])) : 1.f;
-#pragma unroll
-        for (int i = 0; i < FI; i++)
-#pragma unroll
-            for (int r = 0; r < 16; r++)
-                tile[(wm * TM + i * 32 + (r / 4) * 8 + (lane / 32) * 4 + (r % 4)) * LDT + c] = I8 ? acc[i][j][r] * sc : acc[i][j][r];
-    }
-    lds_barrier();
-    constexpr int C4 = BN / 4, RPP = NT / C4;  // threads per row, rows per pass
-    static_assert(NT % C4 == 0 && BM % RPP == 0, "epilogue pass shape");
+    constexpr int EP = dma_epi_passes(BM, BN), BMP = BM / EP;  // passes, tile rows per pass
+    static_assert(BMP % TM == 0, "a wave's rows fall in one epilogue pass");
+    constexpr int C4 = BN / 4, RPP = NT / C4;  // threads per row, rows per store round
+    static_assert(NT % C4 == 0 && BMP % RPP == 0, "epilogue pass shape");
     const int c4 = tid % C4;
+#pragma unroll
+    for (int pass = 0; pass < EP; pass++) {
+        lds_barrier();  // the stages (first pass) or the previous pass's rows are no longer read
+        if (wm * TM / BMP == pass) {
+#pragma unroll
+            for (int j = 0; j < FJ; j++) {
+                const int c = wn * TN + j * 32 + lane % 32;
+                // int8: the weight row's scale (output column c)
+                const float sc = I8 ? __half2float(__ushort_as_half(scales[min(n0 + c, N - 1)])) : 1.f;
+#pragma unroll
+                for (int i = 0; i < FI; i++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++)
+                        tile[(wm * TM - pass * BMP + i * 32 + (r / 4) * 8 + (lane / 32) * 4 + (r % 4)) * LDT + c] =
+                            I8 ? acc[i][j][r] * sc : acc[i][j][r];
+            }
+        }
+        lds_barrier();
 #pragma unroll 4
-    for (int r0 = 0; r0 < BM; r0 += RPP) {
-        const int rl = r0 + tid / C4;
-        const float4 v = *reinterpret_cast<const float4*>(tile + rl * LDT + 4 * c4);
-        store4(epi, partial, bz, Y, y_dtype, M, N, m0 + rl, n0 + 4 * c4, v);
+        for (int r0 = 0; r0 < BMP; r0 += RPP) {
+            const int rl = r0 + tid / C4;
+            const float4 v = *reinterpret_cast<const float4*>(tile + rl * LDT + 4 * c4);
+            store4(epi, partial, bz, Y, y_dtype, M, N, m0 + pass * BMP + rl, n0 + 4 * c4, v);
+        }
     }
 }
 
@@ -786,7 +801,7 @@ bool lds_plan_for(int dtype, int m, int n, int k, int cus, LdsPlan& out) {
     static const LdsPlan forced = [] {  // tuning: "bm,bn,splits" for every shape the kernel takes
         LdsPlan f{0, 0, 1};
         if (const char* e = std::getenv("L0H_GEMM_LDS_PLAN")) std::sscanf(e, "%d,%d,%d", &f.bm, &f.bn, &f.splits);
-        const bool tile = (f.bm == 128 && (f.bn == 128 || f.bn == 256)) || (f.bm == 256 && f.bn == 128);
+        const bool tile = (f.bm == 128 && (f.bn == 128 || f.bn == 256)) || (f.bm == 256 && (f.bn == 128 || f.bn == 256));
         if (!tile || f.splits < 1 || f.splits > kMaxSplits || (f.splits & (f.splits - 1))) f.bm = 0;
         return f;
     }();
@@ -800,6 +815,16 @@ bool lds_plan_for(int dtype, int m, int n, int k, int cus, LdsPlan& out) {
     static const int tiles[][2] = {{128, 256}, {256, 128}, {128, 128}};
     const size_t want = (size_t)std::max(cus, 1) * 3 / 4;
     auto blocks = [&](int bm, int bn) { return (size_t)ceil_div(m, bm) * ceil_div(n, bn); };
+    static const bool big = [] {  // tuning: L0H_GEMM_LDS_256=0 keeps tall shapes on 128 x 256
+        const char* e = std::getenv("L0H_GEMM_LDS_256");
+        return !e || std::atoi(e) != 0;
+    }();
+    // From 1024 rows: 256 x 256 blocks (eight 128 x 64 wave tiles) where they still make 3/4 of a
+    // block per CU without a K split.
+    if (big && m >= 1024 && blocks(256, 256) >= want) {
+        out = LdsPlan{256, 256, 1};
+        return true;
+    }
     for (const auto& t : tiles)
         if (blocks(t[0], t[1]) >= want) {
             out = LdsPlan{t[0], t[1], 1};
@@ -816,15 +841,15 @@ bool lds_plan_for(int dtype, int m, int n, int k, int cus, LdsPlan& out) {
     return mode == 2 || k / out.splits >= 1024;
 }
 
-// LDS bytes of the epilogue's fp32 output tile (rows padded by 8 floats).
-constexpr size_t dma_tile_bytes(int bm, int bn) { return (size_t)bm * (bn + 8) * sizeof(float); }
 
 template <int WT, int BM, int BN, int WGM, int WGN>
 int launch_lds(hipStream_t s, int m, int n, int k, const void* x, const void* w, const uint16_t* scales, void* y,
                int y_dtype, int epi, int splits, float* ws) {
     constexpr int NT = 64 * WGM * WGN;
     constexpr size_t stage = (size_t)BM * 128 + (size_t)BN * (WT == L0H_I8PC ? 64 : 128);
-    constexpr int kMaxNs = 160 * 1024 / stage >= 4 ? 4 : 3;
+    constexpr int kFit = (int)(160 * 1024 / stage);  // ring stages that fit the LDS
+    static_assert(kFit >= 2, "two ring stages must fit");
+    constexpr int kMaxNs = kFit >= 4 ? 4 : kFit;
     static const int ns_env = [] {
         const char* e = std::getenv("L0H_GEMM_LDS_STAGES");  // tuning: LDS ring depth, 2 .. 4
         return e ? std::atoi(e) : 3;
@@ -844,9 +869,14 @@ int launch_lds(hipStream_t s, int m, int n, int k, const void* x, const void* w,
             m, n, k, k_per_split, static_cast<const uint16_t*>(x), w, scales, y, y_dtype, epi, splits > 1 ? ws : nullptr);
         return L0H_OK;
     };
-    int st = ns == 2   ? launch(std::integral_constant<int, 2>{})
+    int st;
+    if constexpr (kMaxNs == 2) {
+        st = launch(std::integral_constant<int, 2>{});
+    } else {
+        st = ns == 2   ? launch(std::integral_constant<int, 2>{})
              : ns == 3 ? launch(std::integral_constant<int, 3>{})
                        : launch(std::integral_constant<int, kMaxNs>{});
+    }
     if (!st) st = launch_status("gemm_lds");
     if (st || splits == 1) return st;
     const size_t mn = (size_t)m * n;
@@ -858,6 +888,8 @@ int launch_lds(hipStream_t s, int m, int n, int k, const void* x, const void* w,
 template <int WT>
 int launch_lds_plan(hipStream_t s, const LdsPlan& p, int m, int n, int k, const void* x, const void* w,
                     const uint16_t* scales, void* y, int y_dtype, int epi, float* ws) {
+    if (p.bm == 256 && p.bn == 256)
+        return launch_lds<WT, 256, 256, 2, 4>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws);
     if (p.bm == 128 && p.bn == 256)
         return launch_lds<WT, 128, 256, 2, 4>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws);
     if (p.bm == 256 && p.bn == 128)

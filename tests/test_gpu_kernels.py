@@ -428,12 +428,15 @@ def test_recording_matches_eager_and_replays(device, suite):
 # LDS-ring plan would leave less than 1024 of K per split (512 x 2048 x 2048, 512 x 1024 x 256,
 # 260 x 640 x 8192); its eight-wave and 256 x 256 tiles run in the int8 test below. The two-operand
 # LDS-ring tiles (M >= 256, K a multiple of 64): 128 x 256 blocks with ragged rows and an odd stage
-# count (300 x 16384 x 320) and with a ragged last row block (1030 x 10240 x 256), and 256 x 128
-# blocks with a ragged last column block whose width (16102) leaves rows that are not 16-byte
-# aligned, so the epilogue stores element by element there (300 x 16102 x 512).
+# count (300 x 16384 x 320) and with a ragged last row block (1030 x 8192 x 256), 256 x 256 blocks
+# (eight 128 x 64 wave tiles, the epilogue in two passes of 128 rows) with a ragged last row block
+# (1030 x 10240 x 256), and 256 x 128 blocks with a ragged last column block whose width (16102)
+# leaves rows that are not 16-byte aligned, so the epilogue stores element by element there
+# (300 x 16102 x 512).
 @pytest.mark.parametrize("m,n,k", [(64, 256, 512), (128, 3072, 2048), (512, 2048, 2048), (100, 200, 128),
                                    (128, 64, 8192), (33, 40, 70), (96, 300, 160), (512, 1024, 256),
-                                   (1030, 10240, 256), (300, 16384, 320), (300, 16102, 512), (260, 640, 8192)])
+                                   (1030, 10240, 256), (1030, 8192, 256), (300, 16384, 320), (300, 16102, 512),
+                                   (260, 640, 8192)])
 @pytest.mark.parametrize("dtype", [l0.BF16, l0.F16])
 def test_gemm_nk_matches_oracle(device, suite, m, n, k, dtype):
     rng = np.random.default_rng(m + n + k)
@@ -452,7 +455,8 @@ def test_gemm_nk_matches_oracle(device, suite, m, n, k, dtype):
 
 # gemm_nk_kernel (K splits, small and ragged shapes; with K = 32 mod 64, which the LDS ring does not
 # take, its 256 x 256 tile at 1030 x 10240 x 480 and its eight-wave 128-row tile at 520 x 16384 x
-# 480) and the LDS-ring kernel with int8 rows (1030 x 10240 x 512, 520 x 16384 x 448).
+# 480) and the LDS-ring kernel with int8 rows (256 x 256 blocks at 1030 x 10240 x 512, 128 x 256 at
+# 520 x 16384 x 448).
 @pytest.mark.parametrize("m,n,k", [(64, 256, 512), (256, 768, 4096), (256, 512, 14336), (100, 200, 128),
                                    (33, 48, 96), (128, 2048, 1024), (512, 320, 2048), (1030, 10240, 512),
                                    (1030, 10240, 480), (260, 384, 8192), (520, 16384, 448), (520, 16384, 480)])
