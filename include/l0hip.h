@@ -460,6 +460,21 @@ typedef struct {
  * entries to host_out and the number of launches to count. */
 int l0h_model_profile_step(l0h_model* model, int token, int position, l0h_kernel_timing* host_out,
                            int capacity, int* count);
+/* Stage callback of l0h_model_probe_step: `count` fp32 values of stage `stage` of decoder layer
+ * `layer`, in host memory that is valid during the call (copy what you keep). */
+typedef void (*l0h_probe_fn)(void* user, int layer, const char* stage, const float* values, int count);
+/* LlmDecoderLayer.Probe (LlmDecoderLayer.cs:113-119): one decode step of `token` at `position`
+ * run eagerly (a probe turns recording off, LlmModel.cs:415-417), calling `probe` after each stage
+ * of every layer with the stage's values: "input_norm", "q", "k", "v" (after the bias, before
+ * RoPE, in head order), "attn_out" (the output projection), "post_norm", "mlp_out" (the down
+ * projection) and "output" (the layer's residual stream), as the reference emits them
+ * (LlmDecoderLayer.cs:168-195, :315-317). The step itself runs the fused kernels of the graph step,
+ * so the cache rows and the logits (host_logits, may be null) are those of l0h_model_compute_logits;
+ * the stages the fused kernels never hold in memory (the norms, q/k/v before RoPE, the two
+ * projections before their residual adds) are recomputed from the same inputs by the RMSNorm
+ * kernel and by the same GEMVs with a plain store. `probe` may be null. */
+int l0h_model_probe_step(l0h_model* model, int token, int position, l0h_probe_fn probe, void* user,
+                         float* host_logits);
 /* Average duration of one kernel kind of the decode step at `position`: `rounds` passes, each
  * launching the kind for every layer (per-layer kinds) or once, back to back between one HIP
  * event pair, so the event cost is amortised and every layer's weights come from HBM. Reports the

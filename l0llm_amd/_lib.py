@@ -102,8 +102,13 @@ _SCALARS = {
     "double": ctypes.c_double,
     "size_t": ctypes.c_size_t,
     "uint64_t": ctypes.c_uint64,
+    "l0h_probe_fn": ctypes.c_void_p,
     "void": None,
 }
+
+# void (*)(void* user, int layer, const char* stage, const float* values, int count)
+PROBE_FN = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.c_int, ctypes.c_char_p, ctypes.POINTER(ctypes.c_float),
+                            ctypes.c_int)
 
 _DECL = re.compile(r"^(int|const char\*)\s+(l0h_\w+)\(([^;]*)\);", re.M | re.S)
 

@@ -644,6 +644,19 @@ class LlmModel:
         return [dict(kind=KERNEL_KINDS[e.kind], layer=e.layer, us=e.microseconds, bytes=e.bytes)
                 for e in buf[: n.value]]
 
+    def probe_step(self, token: int, position: int) -> tuple[np.ndarray, dict[tuple[int, str], np.ndarray]]:
+        """LlmDecoderLayer.Probe over every layer of one eager decode step: the logits and a copy of
+        each stage's values, keyed (layer, stage) with the reference's stage names."""
+        stages: dict[tuple[int, str], np.ndarray] = {}
+
+        def on_stage(_user, layer, stage, values, count):
+            stages[(layer, stage.decode())] = np.ctypeslib.as_array(values, shape=(count,)).copy()
+
+        cb = _lib.PROBE_FN(on_stage)
+        out, p = self._logits_out()
+        check(lib.l0h_model_probe_step(self.handle, token, position, ctypes.cast(cb, ctypes.c_void_p), None, p))
+        return out, stages
+
     def profile_kernel(self, kind: str, position: int, rounds: int = 4) -> dict:
         """Back-to-back launches of one kernel kind (every layer per round): avg us, bytes, launches/step."""
         us, b, n = ctypes.c_float(), ctypes.c_double(), ctypes.c_int()

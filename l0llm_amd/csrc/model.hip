@@ -169,6 +169,7 @@ struct l0h_model {
     // launch is enqueued; 0 before), so the argmax reads those keys instead of the logits.
     unsigned long long* lm_keys = nullptr;
     int lm_waves = 0;
+    float* probe_buf = nullptr;  // a probe's stage values, allocated by the first probe step
     int attn_splits = 1;
     // chunked prefill (allocated on first use): rows of up to pf_cap tokens
     int prefill_chunk = 0;  // tokens per chunk: 2048, or L0H_PREFILL_CHUNK (tuning, tests)
@@ -415,8 +416,10 @@ int step_blocks_per_cu(int kind) {
     return kind >= 0 && kind < 8 ? per[kind] : 2;
 }
 
-// Enqueues one kernel of the decode step (layer li for the per-layer kinds).
-int launch_op(l0h_model* m, hipStream_t s, int kind, int li) {
+// Enqueues one kernel of the decode step (layer li for the per-layer kinds). store_to (q|k|v, O,
+// down): the same GEMV with a plain fp32 store into store_to instead of its RoPE / cache or
+// residual epilogue (the probe's stage values; the step's state is left alone).
+int launch_op(l0h_model* m, hipStream_t s, int kind, int li, float* store_to = nullptr) {
     const auto& c = m->cfg;
     const int H = c.hidden_size;
     GemvParams g;
@@ -449,6 +452,12 @@ int launch_op(l0h_model* m, hipStream_t s, int kind, int li) {
         g.kv_dim = m->kvd;
         g.head_dim = c.head_dim;
         g.rotary_dim = m->rot;
+        if (store_to) {
+            g.epilogue = EPI_STORE;
+            g.y = store_to;
+            g.y_dtype = L0H_F32;
+            g.resid = nullptr;
+        }
         return launch_gemv_nk(s, g);
     }
     case L0H_KERNEL_ATTENTION: {  // LlmDecoderLayer.cs:325-327
@@ -482,6 +491,12 @@ int launch_op(l0h_model* m, hipStream_t s, int kind, int li) {
         g.x_dtype = m->attn_dtype;
         g.epilogue = EPI_RESIDUAL;
         g.resid = m->hidden;
+        if (store_to) {
+            g.epilogue = EPI_STORE;
+            g.y = store_to;
+            g.y_dtype = L0H_F32;
+            g.resid = nullptr;
+        }
         return launch_gemv_nk(s, g);
     }
     case L0H_KERNEL_GATE_UP: {  // LlmDecoderLayer.cs:183-189
@@ -518,6 +533,12 @@ int launch_op(l0h_model* m, hipStream_t s, int kind, int li) {
         }
         g.epilogue = EPI_RESIDUAL;
         g.resid = m->hidden;
+        if (store_to) {
+            g.epilogue = EPI_STORE;
+            g.y = store_to;
+            g.y_dtype = L0H_F32;
+            g.resid = nullptr;
+        }
         return launch_gemv_nk(s, g);
     }
     case L0H_KERNEL_LM_HEAD:  // AppendHead: LlmModel.cs:394-395
@@ -1354,6 +1375,72 @@ int l0h_model_profile_step(l0h_model* m, int token, int position, l0h_kernel_tim
     *count = (int)t.entries.size();
     for (int i = 0; i < std::min(capacity, *count); i++) out[i] = t.entries[i];
     return L0H_OK;
+}
+
+int l0h_model_probe_step(l0h_model* m, int token, int position, l0h_probe_fn probe, void* user, float* host_logits) {
+    int st = check_ready(m);
+    if (st) return st;
+    if ((unsigned)token >= (unsigned)m->cfg.vocab_size) return fail(L0H_ERR_INVALID_ARG, "token id outside the vocabulary");
+    if (position < 0 || position >= m->max_seq) return fail(L0H_ERR_INVALID_ARG, "position outside the cache");
+    const auto& c = m->cfg;
+    const int H = c.hidden_size, QKV = m->qd + 2 * m->kvd;
+    if (!m->probe_buf && (st = alloc_t(m, (size_t)std::max(H, QKV), &m->probe_buf))) return st;
+    const int vals[4] = {token, position, 0, 0};
+    if ((st = l0h_write(m->dev, m->token, 0, vals, sizeof(vals)))) return st;
+    hipStream_t s = m->dev->stream;
+    std::vector<float> host((size_t)std::max(H, QKV)), nat((size_t)QKV);
+    auto fetch = [&](const float* src, int n) -> int {
+        L0H_HIP_TRY(hipMemcpyAsync(host.data(), src, (size_t)n * sizeof(float), hipMemcpyDeviceToHost, s));
+        L0H_HIP_TRY(hipStreamSynchronize(s));
+        return L0H_OK;
+    };
+    auto emit = [&](int li, const char* stage, const float* src, int n) -> int {
+        if (!probe) return L0H_OK;
+        int r = fetch(src, n);
+        if (!r) probe(user, li, stage, host.data(), n);
+        return r;
+    };
+    const int hd = c.head_dim;
+    if ((st = launch_op(m, s, L0H_KERNEL_EMBEDDING, -1))) return st;
+    for (int li = 0; li < c.num_layers && !st; li++) {
+        Layer& L = m->layers[li];
+        // LlmDecoderLayer.cs:167-168: the input RMSNorm
+        if ((st = launch_rmsnorm(s, m->hidden, nullptr, L.input_norm, m->probe_buf, c.rms_norm_eps, H, 1, 0)) ||
+            (st = emit(li, "input_norm", m->probe_buf, H)))
+            break;
+        // :296-317: q, k, v after the bias, before RoPE (the fused matrix stores q and k rows
+        // RoPE-paired; they are put back in head order here)
+        if (probe) {
+            if ((st = launch_op(m, s, L0H_KERNEL_QKV, li, m->probe_buf)) || (st = fetch(m->probe_buf, QKV))) break;
+            for (int r = 0; r < m->qd; r++) nat[r] = host[paired_row(r, hd, m->rot)];
+            for (int r = 0; r < m->kvd; r++) nat[m->qd + r] = host[m->qd + paired_row(r, hd, m->rot)];
+            for (int r = 0; r < m->kvd; r++) nat[m->qd + m->kvd + r] = host[m->qd + m->kvd + r];
+            probe(user, li, "q", nat.data(), m->qd);
+            probe(user, li, "k", nat.data() + m->qd, m->kvd);
+            probe(user, li, "v", nat.data() + m->qd + m->kvd, m->kvd);
+        }
+        if ((st = launch_op(m, s, L0H_KERNEL_QKV, li)) || (st = launch_op(m, s, L0H_KERNEL_ATTENTION, li))) break;
+        // :180: the mixer's output projection
+        if (probe && ((st = launch_op(m, s, L0H_KERNEL_O_PROJ, li, m->probe_buf)) ||
+                      (st = emit(li, "attn_out", m->probe_buf, H))))
+            break;
+        if ((st = launch_op(m, s, L0H_KERNEL_O_PROJ, li))) break;
+        // :183-185: the post-attention RMSNorm of the updated residual stream
+        if ((st = launch_rmsnorm(s, m->hidden, nullptr, L.post_norm, m->probe_buf, c.rms_norm_eps, H, 1, 0)) ||
+            (st = emit(li, "post_norm", m->probe_buf, H)))
+            break;
+        if ((st = launch_op(m, s, L0H_KERNEL_GATE_UP, li))) break;
+        // :190-191: the MLP's down projection
+        if (probe && ((st = launch_op(m, s, L0H_KERNEL_DOWN, li, m->probe_buf)) ||
+                      (st = emit(li, "mlp_out", m->probe_buf, H))))
+            break;
+        if ((st = launch_op(m, s, L0H_KERNEL_DOWN, li)) || (st = emit(li, "output", m->hidden, H))) break;
+    }
+    if (!st) st = launch_op(m, s, L0H_KERNEL_LM_HEAD, -1);
+    if (!st) st = launch_op(m, s, L0H_KERNEL_ARGMAX, -1);
+    if (!st && host_logits) st = l0h_read(m->dev, m->logits, 0, host_logits, (size_t)c.vocab_size * 4);
+    if (!st) st = l0h_synchronize(m->dev);
+    return st;
 }
 
 int l0h_model_profile_kernel(l0h_model* m, int kind, int position, int rounds, float* avg_us, double* bytes,

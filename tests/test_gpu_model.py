@@ -270,6 +270,53 @@ def test_model_load_rejects_missing_or_misshapen_tensors(device, tmp_path):
             m.load_safetensors(tmp_path / "transposed.safetensors")
 
 
+@pytest.mark.parametrize("name", ["llama", "qwen2"])
+def test_probe_stages_match_oracle(device, name):
+    """LlmDecoderLayer.Probe (LlmDecoderLayer.cs:113-119, :168-195, :315-317): every stage of every
+    layer of one eager step, checked against the oracle's operators on the weights the device holds.
+    At position 0 the attention over the one cached row returns that row's V, so attn_out is the
+    output projection of the fp16-cached V of each q head's kv head. The step's own logits are the
+    graph step's, bit for bit."""
+    d = load_hf(name)
+    cfg = d["cfg"]
+    H, eps = cfg["hidden_size"], cfg["rms_norm_eps"]
+    nh, nkv, hd = cfg["num_attention_heads"], cfg["num_key_value_heads"], cfg["head_dim"]
+    with load_model(device, d, l0.PRECISION_INT8, l0.F16) as m:
+        tok = int(d["prompt"][0])
+        logits, st = m.probe_step(tok, 0)
+        np.testing.assert_array_equal(logits, m.compute_logits(tok, 0))
+        assert len(st) == 8 * cfg["num_layers"]
+
+        def proj(name_, x):
+            wst, w, sc = m.export_matrix(name_)
+            return orc.gemv_nk(wst, w, np.asarray(x, np.float32), sc)
+
+        x = m.export_vector("model.embed_tokens.weight", cfg["vocab_size"] * H).reshape(-1, H)[tok]
+        for li in range(cfg["num_layers"]):
+            p = f"model.layers.{li}."
+            _, want = orc.rmsnorm(x, m.export_vector(p + "input_layernorm.weight", H), eps)
+            assert rel_err(st[(li, "input_norm")], want) < 1e-5, li
+            for n, width in (("q", nh * hd), ("k", nkv * hd), ("v", nkv * hd)):
+                want = proj(p + f"self_attn.{n}_proj.weight", st[(li, "input_norm")])
+                if cfg.get("attention_bias"):
+                    want = want + m.export_vector(p + f"self_attn.{n}_proj.bias", width)
+                assert rel_err(st[(li, n)], want) < 1e-4, (li, n)
+            v16 = st[(li, "v")].astype(np.float16).astype(np.float32).reshape(nkv, hd)
+            attn = np.concatenate([v16[h // (nh // nkv)] for h in range(nh)])
+            want = proj(p + "self_attn.o_proj.weight", attn.astype(np.float16).astype(np.float32))
+            assert rel_err(st[(li, "attn_out")], want) < 1e-4, li
+            resid = x + st[(li, "attn_out")]
+            _, want = orc.rmsnorm(resid, m.export_vector(p + "post_attention_layernorm.weight", H), eps)
+            assert rel_err(st[(li, "post_norm")], want) < 1e-4, li
+            act = orc.swiglu(proj(p + "mlp.gate_proj.weight", st[(li, "post_norm")]),
+                             proj(p + "mlp.up_proj.weight", st[(li, "post_norm")]))
+            want = proj(p + "mlp.down_proj.weight", act)
+            assert rel_err(st[(li, "mlp_out")], want) < 3e-3, li  # down reads the SwiGLU row in fp16
+            np.testing.assert_allclose(st[(li, "output")], resid + st[(li, "mlp_out")], rtol=1e-5,
+                                       atol=1e-5 * np.abs(st[(li, "output")]).max())
+            x = st[(li, "output")]
+
+
 def test_generate_greedy_matches_step_loop_and_stops(device):
     d = load_hf("llama")
     with load_model(device, d, l0.PRECISION_INT8, l0.F16) as m:
