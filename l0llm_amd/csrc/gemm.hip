@@ -325,9 +325,9 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(1, 2))
 __device__ __forceinline__ int lds_swz(int r) { return (r ^ (r >> 3)) & 7; }
 
 // int8 weight rows in LDS: 64 bytes (4 chunks of 16) per row; chunk c of tile row r sits in slot
-// c ^ lds_swz8(r). A fragment read takes 8 bytes of one chunk from 32 consecutive rows; over any 16
-// consecutive rows the (row mod 4, slot) pairs are distinct, so 16 lanes' 8-byte reads hit distinct
-// banks.
+// c ^ lds_swz8(r). A fragment read takes a whole chunk from each of 32 consecutive rows; over any 16
+// consecutive rows the (row mod 4, slot) pairs are distinct, so each 16-lane group of a 16-byte read
+// hits all 64 banks once.
 __device__ __forceinline__ int lds_swz8(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
 
 // 8 int8 values (bytes of lo, then hi) -> 8 exact fp16 in the same order: byte u = q + 128 (sign bit
@@ -541,22 +541,33 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
     for (int j = 0; j < FJ; j++) br[j] = wn * TN + j * 32 + lane % 32;
     const int hi = lane / 32;
-    // K substep s reads chunk 2 s + lane / 32 of each fragment row. The fragments of substep s + 1
-    // are read before substep s's MFMAs are issued (two sets); a scheduling barrier per substep
-    // keeps the compiler from hoisting all four substeps' reads.
+    // K substep s reads chunk 2 s + lane / 32 of each 16-bit fragment row. int8 weights: substeps
+    // 2P and 2P + 1 take the two halves of one 16-byte weight chunk, 2P + hi (K 32 P + 16 hi + 8 t
+    // .. + 7 for substep 2P + t), read whole in substep 2P (an 8-byte read per substep would leave
+    // half of every 16-byte slot unread by each 32-lane group: a two-way bank conflict), so the
+    // activation chunk of substep 2P + t is 4 P + 2 hi + t: both operands carry the same K values.
+    // The fragments of substep s + 1 are read before substep s's MFMAs are issued (two sets); a
+    // scheduling barrier per substep keeps the compiler from hoisting all four substeps' reads.
     auto compute = [&](int buf) {
         const char* sa = lds + buf * STAGE;
         const char* sb = sa + BM * ROWA;
         uint4 a0[FI], b0[FJ], a1[FI], b1[FJ];
+        uint2 rest[FJ];  // int8: the second half of the chunk read in the even substep
         auto frags = [&](uint4 (&a)[FI], uint4 (&b)[FJ], int s) {
+            const int ac = I8 ? 4 * (s >> 1) + 2 * hi + (s & 1) : 2 * s + hi;
 #pragma unroll
             for (int i = 0; i < FI; i++)
-                a[i] = *reinterpret_cast<const uint4*>(sa + ar[i] * ROWA + (((2 * s + hi) ^ lds_swz(ar[i])) << 4));
+                a[i] = *reinterpret_cast<const uint4*>(sa + ar[i] * ROWA + ((ac ^ lds_swz(ar[i])) << 4));
 #pragma unroll
             for (int j = 0; j < FJ; j++) {
-                if constexpr (I8) {  // K values 16 s + 8 hi .. + 7: half hi of chunk s
-                    const uint2 q = *reinterpret_cast<const uint2*>(sb + br[j] * ROWB + ((s ^ lds_swz8(br[j])) << 4) + 8 * hi);
-                    b[j] = i8x8_to_f16_ordered(q.x, q.y);
+                if constexpr (I8) {
+                    if ((s & 1) == 0) {
+                        const uint4 q = *reinterpret_cast<const uint4*>(sb + br[j] * ROWB + (((s + hi) ^ lds_swz8(br[j])) << 4));
+                        b[j] = i8x8_to_f16_ordered(q.x, q.y);
+                        rest[j] = make_uint2(q.z, q.w);
+                    } else {
+                        b[j] = i8x8_to_f16_ordered(rest[j].x, rest[j].y);
+                    }
                 } else {
                     b[j] = *reinterpret_cast<const uint4*>(sb + br[j] * ROWB + (((2 * s + hi) ^ lds_swz(br[j])) << 4));
                 }
