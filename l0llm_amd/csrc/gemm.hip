@@ -543,9 +543,9 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
     const int hi = lane / 32;
     // K substep s reads chunk 2 s + lane / 32 of each 16-bit fragment row. int8 weights: substeps
     // 2P and 2P + 1 take the two halves of one 16-byte weight chunk, 2P + hi (K 32 P + 16 hi + 8 t
-    // .. + 7 for substep 2P + t), read whole in substep 2P (an 8-byte read per substep would leave
-    // half of every 16-byte slot unread by each 32-lane group: a two-way bank conflict), so the
-    // activation chunk of substep 2P + t is 4 P + 2 hi + t: both operands carry the same K values.
+    // .. + 7 for substep 2P + t), read whole in substep 2P (one LDS read per two MFMAs instead of
+    // an 8-byte read per MFMA), so the activation chunk of substep 2P + t is 4 P + 2 hi + t: both
+    // operands carry the same K values.
     // The fragments of substep s + 1 are read before substep s's MFMAs are issued (two sets); a
     // scheduling barrier per substep keeps the compiler from hoisting all four substeps' reads.
     auto compute = [&](int buf) {
