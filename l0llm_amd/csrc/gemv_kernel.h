@@ -675,10 +675,24 @@ int dispatch_mr(hipStream_t s, const GemvParams& p, int mr) {
 
 // Rows per wave item (R) and 16-byte chunks per row per lane (U), chosen by the row length so an
 // item carries about 8 KiB of real weights for int8 (R * U KiB): C <= 64 chunks per row -> 8 rows
-// x 1 chunk per lane, C <= 128 -> 4 x 2, else 2 x 4. Several activation rows use 2 x 4.
+// x 1 chunk per lane, C <= 128 -> 4 x 2, else 2 x 4; short rows of a matrix with few rows take 2-row
+// items (2 x 1, 2 x 2). Several activation rows use 2 x 4.
 template <int WT>
 int dispatch_wt(hipStream_t s, const GemvParams& p, int mr) {
     const int C = p.k / WTraits<WT>::kElems;
+    // Short rows (at most 128 chunks): the 8- or 4-row items suit long streams (every wave gets at
+    // least four of them); fewer rows leave most of the grid idle, so those take 2-row items, one
+    // item per wave or a few. Measured (int8, K = 896, graph replay, cold weights): 896 -> 4864
+    // 4.30 -> 3.45 us, 896 -> 1152 3.96 -> 2.55, 896 -> 9728 5.43 -> 4.45; 896 -> 151936 keeps
+    // 8-row items (28.7 us against 39.5 with 2-row ones).
+    if (mr == 1 && C <= 128) {
+        const long waves = (long)(p.max_blocks > 0 ? p.max_blocks : 512) * kWaves;
+        const int r_long = C <= 64 ? 8 : 4;
+        if (ceil_div(p.n, r_long) < 4 * waves) {
+            if (C <= 64) return dispatch_mr<WT, 2, 1>(s, p, mr);
+            return dispatch_mr<WT, 2, 2>(s, p, mr);
+        }
+    }
     if (mr == 1 && C <= 64) return dispatch_mr<WT, 8, 1>(s, p, mr);
     if (mr == 1 && C <= 128) return dispatch_mr<WT, 4, 2>(s, p, mr);
     return dispatch_mr<WT, 2, 4>(s, p, mr);
