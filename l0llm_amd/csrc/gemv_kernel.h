@@ -676,7 +676,7 @@ int dispatch_mr(hipStream_t s, const GemvParams& p, int mr) {
 // Rows per wave item (R) and 16-byte chunks per row per lane (U), chosen by the row length so an
 // item carries about 8 KiB of real weights for int8 (R * U KiB): C <= 64 chunks per row -> 8 rows
 // x 1 chunk per lane, C <= 128 -> 4 x 2, else 2 x 4; short rows of a matrix with few rows take 2-row
-// items (2 x 1, 2 x 2). Several activation rows use 2 x 4.
+// items (2 x 1, 2 x 2), long ones 1-row items (1 x 4). Several activation rows use 2 x 4.
 template <int WT>
 int dispatch_wt(hipStream_t s, const GemvParams& p, int mr) {
     const int C = p.k / WTraits<WT>::kElems;
@@ -691,6 +691,22 @@ int dispatch_wt(hipStream_t s, const GemvParams& p, int mr) {
         if (ceil_div(p.n, r_long) < 4 * waves) {
             if (C <= 64) return dispatch_mr<WT, 2, 1>(s, p, mr);
             return dispatch_mr<WT, 2, 2>(s, p, mr);
+        }
+    }
+    // Long rows of a matrix with fewer than two rows per wave of the grid (plain store epilogue):
+    // 1-row items keep twice as many waves streaming. Measured (graph replay, cold weights,
+    // 4864 -> 896): int8 5.21 -> 4.59 us, fp16 4.87 -> 4.52 us; 1 x 2 and 1 x 1 items were slower.
+    if (mr == 1 && C > 128 && p.epilogue == EPI_STORE && !p.norm_w) {
+        const long waves = (long)(p.max_blocks > 0 ? p.max_blocks : 512) * kWaves;
+        if (ceil_div(p.n, 2) < waves) {
+            switch (staged_chunks(p)) {
+            case 1: return launch_fast<WT, 1, 4, 1, 1, false, EPI_STORE>(s, p);
+            case 2: return launch_fast<WT, 1, 4, 1, 2, false, EPI_STORE>(s, p);
+            case 4: return launch_fast<WT, 1, 4, 1, 4, false, EPI_STORE>(s, p);
+            case 8: return launch_fast<WT, 1, 4, 1, 8, false, EPI_STORE>(s, p);
+            case 16: return launch_fast<WT, 1, 4, 1, 16, false, EPI_STORE>(s, p);
+            default: return fail(L0H_ERR_UNSUPPORTED, "GEMV activation row exceeds the LDS tile");
+            }
         }
     }
     if (mr == 1 && C <= 64) return dispatch_mr<WT, 8, 1>(s, p, mr);

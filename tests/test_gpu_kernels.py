@@ -23,6 +23,7 @@ GEMV_SHAPES = [
     (4864, 896),    # Qwen2.5-0.5B up-proj: config 1
     (1152, 896),    # fused QKV 896 -> 1152
     (896, 4864),    # down-proj
+    (517, 2080),    # odd row count, long rows, fewer rows than waves: 1-row items
     (6144, 4096),   # Llama-3.1-8B fused QKV
     (4096, 14336),  # Llama-3.1-8B down-proj (last batch of each row half filled)
     (100, 48),      # small
