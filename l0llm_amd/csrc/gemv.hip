@@ -226,22 +226,22 @@ __global__ void kn_slice_sum_kernel(const float* part, float* y, int splits, siz
 
 // One activation row in narrow column tiles: block (tile t of 8 chunks = 128 bytes of every weight
 // row, K slice s). Lane l reads chunk l % 8 of row l / 8 of each group of 8 rows, so one wave
-// instruction covers 8 whole 128-byte row segments and the block's 4 waves take rows 32 apart.
+// instruction covers 8 whole 128-byte row segments and the block's NW waves take rows 8 * NW apart.
 // The slice's rows go in batches of kNarrowU per lane, the next batch requested before the current
 // one is computed; x comes from LDS (zero past the slice, where the clamped rows add nothing). The
 // 8 lanes of a chunk are summed over DPP and row swaps, the waves through LDS in a fixed order.
 constexpr int kNarrowU = 8;      // row groups per lane per batch
-constexpr int kNarrowRPS = 32;   // rows per block step (8 per wave instruction, 4 waves)
-constexpr int kNarrowLds = kKnLds - 4096;  // dynamic LDS for x (the wave reduction is static)
+constexpr int kNarrowLds = kKnLds - 16384;  // dynamic LDS for x (the wave reduction is static)
 
-template <int WT>
-__global__ __launch_bounds__(kBlock) void gemv_kn_narrow_kernel(int N, int K, int ks, const float* x, const void* w,
-                                                                float* out) {
+template <int WT, int NW>
+__global__ __launch_bounds__(NW * 64) void gemv_kn_narrow_kernel(int N, int K, int ks, const float* x, const void* w,
+                                                                 float* out) {
     constexpr int EPC = WT == L0H_F16 ? 8 : 4;  // columns per 16-byte chunk
     constexpr int TC = 8 * EPC;                 // columns per tile
+    constexpr int kNarrowRPS = 8 * NW;          // rows per block step (8 per wave instruction)
     extern __shared__ float kn_smem[];
     float* xs = kn_smem;                         // [steps rounded to batches * kNarrowRPS]
-    __shared__ float red[kWaves][TC];
+    __shared__ float red[NW][TC];
     const int CN = N / EPC;
     const int t = blockIdx.x, sl = blockIdx.y;
     const int lane = threadIdx.x & 63;
@@ -251,7 +251,7 @@ __global__ __launch_bounds__(kBlock) void gemv_kn_narrow_kernel(int N, int K, in
     const int steps = (k1 - k0 + kNarrowRPS - 1) / kNarrowRPS;
     const int batches = (steps + kNarrowU - 1) / kNarrowU;
     const int nx = batches * kNarrowU * kNarrowRPS;
-    for (int i = threadIdx.x; i < nx; i += kBlock) xs[i] = k0 + i < k1 ? x[k0 + i] : 0.f;
+    for (int i = threadIdx.x; i < nx; i += NW * 64) xs[i] = k0 + i < k1 ? x[k0 + i] : 0.f;
     __syncthreads();
     const uint4* wp = static_cast<const uint4*>(w) + min(t * 8 + cj, CN - 1);
     float acc[EPC];
@@ -314,7 +314,7 @@ __global__ __launch_bounds__(kBlock) void gemv_kn_narrow_kernel(int N, int K, in
         const int c = t * TC + threadIdx.x;
         float v = red[0][threadIdx.x];
 #pragma unroll
-        for (int ww = 1; ww < kWaves; ww++) v += red[ww][threadIdx.x];
+        for (int ww = 1; ww < NW; ww++) v += red[ww][threadIdx.x];
         if (c < N) out[(size_t)sl * N + c] = v;
     }
 }
@@ -380,18 +380,27 @@ int launch_kn_tile(hipStream_t s, int n, int k, int ks, int splits, const float*
     return launch_status("gemv_kn_tile");
 }
 
-template <int WT>
-int launch_kn_narrow(hipStream_t s, int n, int k, int ks, int splits, const float* x, const void* w, float* out) {
+template <int WT, int NW>
+int launch_kn_narrow_nw(hipStream_t s, int n, int k, int ks, int splits, const float* x, const void* w, float* out) {
     constexpr int EPC = WT == L0H_F16 ? 8 : 4;
+    constexpr int kNarrowRPS = 8 * NW;
     const unsigned tiles = ceil_div((size_t)(n / EPC), 8);
     const int steps = (ks + kNarrowRPS - 1) / kNarrowRPS;
     const size_t shmem = (size_t)((steps + kNarrowU - 1) / kNarrowU) * kNarrowU * kNarrowRPS * sizeof(float);
-    auto kern = gemv_kn_narrow_kernel<WT>;
+    if (shmem > (size_t)kNarrowLds) return fail(L0H_ERR_UNSUPPORTED, "GEMV K slice exceeds the LDS tile");
+    auto kern = gemv_kn_narrow_kernel<WT, NW>;
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, kNarrowLds);
     if (attr != hipSuccess) return fail(L0H_ERR_DEVICE, std::string("hipFuncSetAttribute: ") + hipGetErrorString(attr));
-    kern<<<dim3(tiles, splits), kBlock, shmem, s>>>(n, k, ks, x, w, out);
+    kern<<<dim3(tiles, splits), NW * 64, shmem, s>>>(n, k, ks, x, w, out);
     return launch_status("gemv_kn_narrow");
+}
+
+template <int WT>
+int launch_kn_narrow(hipStream_t s, int nw, int n, int k, int ks, int splits, const float* x, const void* w,
+                     float* out) {
+    return nw == 16 ? launch_kn_narrow_nw<WT, 16>(s, n, k, ks, splits, x, w, out)
+                    : launch_kn_narrow_nw<WT, 4>(s, n, k, ks, splits, x, w, out);
 }
 
 template <int WT>
@@ -409,11 +418,23 @@ KnPlan plan_gemv_kn(int rows, int n, int k, int w_dtype, int compute_units, size
     const int epc = w_dtype == L0H_F16 ? 8 : 4;
     if (rows == 1) {
         // Narrow tiles: no K split from min_tiles tiles up (a K split costs a second launch for the
-        // slice sum); else slices of whole batches (at least 256 rows) up to about one block per CU.
+        // slice sum); else slices of whole batches (at least 256 or 1024 rows) up to about one block
+        // per CU.
         KnPlan pl;
         pl.narrow = true;
         const int tiles = (int)ceil_div((size_t)(n / epc), 8);
-        const int batch_rows = kNarrowU * kNarrowRPS;
+        static const int nw_env = [] {  // waves per block, 4 or 16 (tuning)
+            const char* e = std::getenv("L0H_GEMV_KN_NW");
+            return e ? std::atoi(e) : 0;
+        }();
+        // 16 waves when all of K is one batch of theirs (1024 rows) and the tiles are few: each
+        // wave then has one batch to stream. Measured (fp16, graph replay, cold weights): Qwen2.5-0.5B
+        // O 896 -> 896 5.6 (split in 3 + slice sum) -> 4.5 us, q|k|v 4.9 -> 4.5, 896 -> 4864 5.4 -> 5.2,
+        // gate|up 6.7 -> 6.4; longer K (down 4864 -> 896: 7.4 -> 9.7) and many tiles (lm_head, 2374
+        // tiles: 45.3 -> 49.3) stay at 4.
+        pl.nw = nw_env == 4 || nw_env == 16 ? nw_env : k <= kNarrowU * 8 * 16 && tiles <= 512 ? 16 : 4;
+        const int rps = 8 * pl.nw;
+        const int batch_rows = kNarrowU * rps;
         const int max_ks = (kNarrowLds / 4) / batch_rows * batch_rows;  // the slice's x fits the LDS
         static const int min_tiles_env = [] {  // tiles from which no K split is made (tuning)
             const char* e = std::getenv("L0H_GEMV_KN_TILES");
@@ -428,7 +449,7 @@ KnPlan plan_gemv_kn(int rows, int n, int k, int w_dtype, int compute_units, size
         const size_t per_split = (size_t)n * sizeof(float);
         if (splits > 1 && (size_t)splits * per_split > ws_bytes)
             splits = std::max((int)ceil_div((size_t)k, (size_t)max_ks), (int)std::min<size_t>(splits, ws_bytes / per_split));
-        pl.ks = (int)ceil_div((size_t)ceil_div((size_t)k, (size_t)std::max(splits, 1)), (size_t)kNarrowRPS) * kNarrowRPS;
+        pl.ks = (int)ceil_div((size_t)ceil_div((size_t)k, (size_t)std::max(splits, 1)), (size_t)rps) * rps;
         pl.ks = std::min(pl.ks, max_ks);
         pl.splits = (int)ceil_div((size_t)k, (size_t)pl.ks);
         return pl;
@@ -486,8 +507,8 @@ int launch_gemv_kn(hipStream_t s, int rows, int n, int k, const float* x, const 
         float* out = pl.splits > 1 ? ws : yr;
         int st;
         if (pl.narrow)
-            st = w_dtype == L0H_F16 ? launch_kn_narrow<L0H_F16>(s, n, k, pl.ks, pl.splits, xr, w, out)
-                                    : launch_kn_narrow<L0H_F32>(s, n, k, pl.ks, pl.splits, xr, w, out);
+            st = w_dtype == L0H_F16 ? launch_kn_narrow<L0H_F16>(s, pl.nw, n, k, pl.ks, pl.splits, xr, w, out)
+                                    : launch_kn_narrow<L0H_F32>(s, pl.nw, n, k, pl.ks, pl.splits, xr, w, out);
         else
             st = w_dtype == L0H_F16 ? launch_kn_rows<L0H_F16>(s, pl.mr, n, k, pl.ks, pl.splits, xr, w, out)
                                     : launch_kn_rows<L0H_F32>(s, pl.mr, n, k, pl.ks, pl.splits, xr, w, out);

@@ -77,6 +77,7 @@ struct KnPlan {
     int ks = 0;      // weight rows per K slice
     int splits = 1;  // K slices
     bool narrow = false;  // one activation row: 64-column (fp16) tiles, 8 rows per wave instruction
+    int nw = 4;           // waves per block of the one-row kernel
 };
 // ws_bytes caps the slices (fewer slices, or fewer rows per launch, when it is small).
 KnPlan plan_gemv_kn(int rows, int n, int k, int w_dtype, int compute_units, size_t ws_bytes);

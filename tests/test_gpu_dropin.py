@@ -93,6 +93,32 @@ def test_gemv_kn_tiled_matches_oracle(device, suite, n, k, rows, wdt):
         b.free()
 
 
+@pytest.mark.parametrize("n,k", [(896, 896), (896, 4864), (896, 14336)])
+def test_gemv_kn_split_merge_repeats_bit_exact(device, suite, n, k):
+    """One-row K-split launches (partials + a fixed-order slice sum): eager repeats and graph replays
+    give the same bits as the first call."""
+    rng = np.random.default_rng(n + 5 * k)
+    w = rng.normal(0, 0.02, (k, n)).astype(np.float16).view(np.uint16)
+    x = rng.normal(0, 1, k).astype(np.float32)
+    wb, xb, yb = up(device, w), up(device, x), device.alloc(n * 4)
+    suite.gemv_execute(n, k, xb, wb, yb, w_dtype=l0.F16)
+    first = yb.read(np.float32, n)
+    assert rel_err(first, orc.gemv_kn(l0.F16, w, x[None])[0]) < 2e-5
+    for _ in range(3):
+        yb.zero()
+        suite.gemv_execute(n, k, xb, wb, yb, w_dtype=l0.F16)
+        np.testing.assert_array_equal(yb.read(np.float32, n), first)
+    device.begin_recording()
+    suite.gemv_execute(n, k, xb, wb, yb, w_dtype=l0.F16)
+    device.end_recording()
+    for _ in range(3):
+        yb.zero()
+        device.replay_recording(2)
+        np.testing.assert_array_equal(yb.read(np.float32, n), first)
+    for b in (wb, xb, yb):
+        b.free()
+
+
 # ---- memory a recording uses ----------------------------------------------------------------------
 
 def test_replay_refused_after_free_or_workspace_growth():
