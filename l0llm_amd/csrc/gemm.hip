@@ -24,8 +24,9 @@
 // From 256 rows, 16-bit weights take gemm_dma_kernel instead: both operands pass through a ring of
 // LDS stages that LDS-direct loads (global_load_lds_dwordx4) fill, so two stages of both operands
 // are in flight while one is computed and no registers stage them; block tiles of 128 x 256,
-// 256 x 128 or 128 x 128 with 64 x 64 wave tiles, and an epilogue that goes through LDS so each
-// output row segment is written by consecutive lanes.
+// 256 x 128 or 128 x 128 with 64 x 64 wave tiles (128 x 64 with 64 x 32 ones for wide shapes that
+// the larger tiles leave short of blocks, also from 65 rows), and an epilogue that goes through LDS
+// so each output row segment is written by consecutive lanes.
 //
 // Shapes with fewer blocks than the GPU has CUs split K across blocks into fp32 partials that a
 // second pass sums in a fixed order (deterministic). Blocks are renumbered so the blocks that
@@ -788,7 +789,8 @@ int launch_tiles(hipStream_t s, int m, int n, int k, const void* x, const void* 
     return launch_status("gemm splitk reduce");
 }
 
-// Two-operand LDS tiles (gemm_dma_kernel) for M >= 256 and K a multiple of 64. The largest tile
+// Two-operand LDS tiles (gemm_dma_kernel) for M >= 256 (and wide 16-bit shapes from 65 rows, below)
+// and K a multiple of 64. The largest tile
 // that gives about one block per CU (3/4 of the CUs or more) without a K split, else the K split
 // (power of two, at least 8 stages of 64 per split) that gets there with the fewest partials; used
 // unless that split leaves less than 1024 of K per block, where gemm_nk_kernel without a split is
@@ -798,6 +800,7 @@ int launch_tiles(hipStream_t s, int m, int n, int k, const void* x, const void* 
 // 344, 2047 x 4096 x 4096 83 against 107; 512 x 2048 x 2048 (split 4) 18.4 against 15.2.
 struct LdsPlan {
     int bm = 0, bn = 0, splits = 1;
+    int waves = 0;  // 0: the tile's default wave grid
 };
 
 bool lds_plan_for(int dtype, int m, int n, int k, int cus, LdsPlan& out) {
@@ -809,10 +812,13 @@ bool lds_plan_for(int dtype, int m, int n, int k, int cus, LdsPlan& out) {
         const char* e = std::getenv("L0H_GEMM_LDS_I8");
         return e ? std::atoi(e) : 1;
     }();
-    static const LdsPlan forced = [] {  // tuning: "bm,bn,splits" for every shape the kernel takes
-        LdsPlan f{0, 0, 1};
-        if (const char* e = std::getenv("L0H_GEMM_LDS_PLAN")) std::sscanf(e, "%d,%d,%d", &f.bm, &f.bn, &f.splits);
-        const bool tile = (f.bm == 128 && (f.bn == 128 || f.bn == 256)) || (f.bm == 256 && (f.bn == 128 || f.bn == 256));
+    static const LdsPlan forced = [] {  // tuning: "bm,bn,splits[,waves]" for every shape the kernel takes
+        LdsPlan f{0, 0, 1, 0};
+        if (const char* e = std::getenv("L0H_GEMM_LDS_PLAN"))
+            std::sscanf(e, "%d,%d,%d,%d", &f.bm, &f.bn, &f.splits, &f.waves);
+        const bool tile = (f.bm == 128 && (f.bn == 64 || f.bn == 128 || f.bn == 256)) ||
+                          (f.bm == 256 && (f.bn == 128 || f.bn == 256)) || (f.bm == 64 && (f.bn == 64 || f.bn == 128));
+        if (f.waves != 4 || f.bm != 128 || f.bn != 256) f.waves = 0;
         if (!tile || f.splits < 1 || f.splits > kMaxSplits || (f.splits & (f.splits - 1))) f.bm = 0;
         return f;
     }();
@@ -822,10 +828,22 @@ bool lds_plan_for(int dtype, int m, int n, int k, int cus, LdsPlan& out) {
         out = forced;
         return true;
     }
-    if (m < 256) return false;
     static const int tiles[][2] = {{128, 256}, {256, 128}, {128, 128}};
     const size_t want = (size_t)std::max(cus, 1) * 3 / 4;
     auto blocks = [&](int bm, int bn) { return (size_t)ceil_div(m, bm) * ceil_div(n, bn); };
+    // 16-bit weights, 128 x 64 blocks where they make 3/4 of a block per CU without a K split and
+    // the larger tiles do not: Llama-3.2-1B bf16 q|k|v at M = 512 (2048 -> 3072) 22.3 -> 20.4 us
+    // (128 x 128 needed a K split in 2 and its sum), gate|up at M = 128 (2048 -> 16384) 28.0 ->
+    // 24.0 us against the register-staged kernel. Where it would need a K split, or on the other
+    // Llama-3.2-1B shapes, it is slower (O 15.9 -> 19.6, down 37.8 -> 56.9 at M = 512).
+    const bool narrow = dtype != L0H_I8PC && blocks(128, 64) >= want;
+    if (m < 256) {
+        if (narrow && m > 64 && k >= 1024) {
+            out = LdsPlan{128, 64, 1};
+            return true;
+        }
+        return false;
+    }
     static const bool big = [] {  // tuning: L0H_GEMM_LDS_256=0 keeps tall shapes on 128 x 256
         const char* e = std::getenv("L0H_GEMM_LDS_256");
         return !e || std::atoi(e) != 0;
@@ -841,6 +859,10 @@ bool lds_plan_for(int dtype, int m, int n, int k, int cus, LdsPlan& out) {
             out = LdsPlan{t[0], t[1], 1};
             return true;
         }
+    if (narrow) {
+        out = LdsPlan{128, 64, 1};
+        return true;
+    }
     for (int sp = 2; sp <= kMaxSplits && k / sp >= 8 * 64; sp *= 2)
         for (const auto& t : tiles)
             if (blocks(t[0], t[1]) * sp >= want) {
@@ -901,8 +923,16 @@ int launch_lds_plan(hipStream_t s, const LdsPlan& p, int m, int n, int k, const 
                     const uint16_t* scales, void* y, int y_dtype, int epi, float* ws) {
     if (p.bm == 256 && p.bn == 256)
         return launch_lds<WT, 256, 256, 2, 4>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws);
+    if (p.bm == 128 && p.bn == 256 && p.waves == 4)
+        return launch_lds<WT, 128, 256, 2, 2>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws);
     if (p.bm == 128 && p.bn == 256)
         return launch_lds<WT, 128, 256, 2, 4>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws);
+    if (p.bm == 128 && p.bn == 64)
+        return launch_lds<WT, 128, 64, 2, 2>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws);
+    if (p.bm == 64 && p.bn == 128)
+        return launch_lds<WT, 64, 128, 2, 2>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws);
+    if (p.bm == 64 && p.bn == 64)
+        return launch_lds<WT, 64, 64, 2, 2>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws);
     if (p.bm == 256 && p.bn == 128)
         return launch_lds<WT, 256, 128, 4, 2>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws);
     return launch_lds<WT, 128, 128, 2, 2>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws);
