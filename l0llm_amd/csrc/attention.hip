@@ -876,6 +876,7 @@ __global__ __launch_bounds__(kBlock) void attn_prefill_mfma_kernel(const AttnPar
     const int qtok = qi / gsize;
     const bool qvalid = qtok < tq_tokens && t0 + qtok < tokens;
     const int lim = qvalid ? pos0 + t0 + qtok : -1;
+    const int lim_min = pos0 + t0;  // the last position the block's first query sees
     const float qscale = 1.4426950408889634f / sqrtf((float)HD);
     uint4 qf[KS];  // Q[qi][32 kk + 8 lg .. +7] as fp16
 #pragma unroll
@@ -964,43 +965,56 @@ __global__ __launch_bounds__(kBlock) void attn_prefill_mfma_kernel(const AttnPar
             }
         }
         // Online softmax for query l % 16 over the tile's 64 positions (this lane: 16 of them).
-        float mt = -INFINITY;
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int pos = kt * kPK + 16 * j + 4 * lg + r;
-                if (pos > lim) st[j][r] = -INFINITY;
-                mt = fmaxf(mt, st[j][r]);
-            }
-        mt = fmaxf(mt, __shfl_xor(mt, 16));
-        mt = fmaxf(mt, __shfl_xor(mt, 32));
-        const float mn = fmaxf(m, mt);
-        const float corr = mn == -INFINITY ? 1.f : exp2_hw(m - mn);
-        float ps = 0.f;
+        // MASKED: the tile reaches past some query's last position (the diagonal tiles). Other
+        // tiles are whole for every query of the block, so no score is masked and the running
+        // maximum is finite after them (m = -inf only before the first tile, where exp2(-inf)
+        // = 0 scales the still-zero sums); the lanes of invalid queries compute values never stored.
         uint32_t ph[4][2];  // P as fp16 pairs: sub-tile j, rows r = 0,1 and 2,3
+        auto softmax = [&](auto masked) {
+            constexpr bool MASKED = decltype(masked)::value;
+            float mt = -INFINITY;
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            float pr[4];
+            for (int j = 0; j < 4; j++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                pr[r] = mn == -INFINITY ? 0.f : exp2_hw(st[j][r] - mn);
-                ps += pr[r];
+                for (int r = 0; r < 4; r++) {
+                    if constexpr (MASKED) {
+                        const int pos = kt * kPK + 16 * j + 4 * lg + r;
+                        if (pos > lim) st[j][r] = -INFINITY;
+                    }
+                    mt = fmaxf(mt, st[j][r]);
+                }
+            mt = fmaxf(mt, __shfl_xor(mt, 16));
+            mt = fmaxf(mt, __shfl_xor(mt, 32));
+            const float mn = fmaxf(m, mt);
+            const float corr = MASKED && mn == -INFINITY ? 1.f : exp2_hw(m - mn);
+            float ps = 0.f;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                float pr[4];
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    pr[r] = MASKED && mn == -INFINITY ? 0.f : exp2_hw(st[j][r] - mn);
+                    ps += pr[r];
+                }
+                ph[j][0] = pack_half2(pr[0], pr[1]);
+                ph[j][1] = pack_half2(pr[2], pr[3]);
             }
-            ph[j][0] = pack_half2(pr[0], pr[1]);
-            ph[j][1] = pack_half2(pr[2], pr[3]);
-        }
-        ps += __shfl_xor(ps, 16);
-        ps += __shfl_xor(ps, 32);
-        l = l * corr + ps;
-        m = mn;
+            ps += __shfl_xor(ps, 16);
+            ps += __shfl_xor(ps, 32);
+            l = l * corr + ps;
+            m = mn;
 #pragma unroll
-        for (int i = 0; i < NI; i++) {
-            o[i][0] *= corr;
-            o[i][1] *= corr;
-            o[i][2] *= corr;
-            o[i][3] *= corr;
-        }
+            for (int i = 0; i < NI; i++) {
+                o[i][0] *= corr;
+                o[i][1] *= corr;
+                o[i][2] *= corr;
+                o[i][3] *= corr;
+            }
+        };
+        if (kt * kPK + kPK - 1 <= lim_min)
+            softmax(std::false_type{});
+        else
+            softmax(std::true_type{});
         // O^T[dims][q] += V^T[dims][pos] P^T[pos][q], chunks c of 32 positions.
 #pragma unroll
         for (int c = 0; c < 2; c++) {
