@@ -272,12 +272,40 @@ def _median_s(fn, runs: int) -> float:
     return float(np.median(ts))
 
 
-def cpu_baseline(model, cfg, tokens: int, position: int) -> dict:
+def greedy_ids_check(model, om, cfg, ctx: int, first: int, ids, count: int) -> dict:
+    """The timed run's first `count` greedy ids against the oracle: the oracle's caches are seeded
+    with the device's rows 0 .. ctx - 1 (the prefilled prompt), then it runs the same tokens at the
+    same positions (teacher-forced with the device's ids). An id may differ only where the oracle's
+    own top-2 gap is below 1e-2 of max|logit|: twice the 5e-3 that the device's fp16 storage of the
+    attention and SwiGLU outputs is allowed to move the logits over 32 layers (a tie, not a bug)."""
+    import l0llm_amd as l0
+    from oracle import pyoracle as orc
+
+    kv_bytes = ctx * cfg.num_key_value_heads * cfg.head_dim * 2
+    for layer in range(cfg.num_layers):
+        kp, vp = model.kv_cache(layer)
+        om.load_cache(layer, l0.Buffer(model.device, kv_bytes, ptr=kp, owned=False).read(np.uint8),
+                      l0.Buffer(model.device, kv_bytes, ptr=vp, owned=False).read(np.uint8))
+    tok, equal, flips = first, 0, 0
+    for i in range(count):
+        onext, olg = om.step(tok, ctx + i)
+        got = int(ids[i])
+        if got == onext:
+            equal += 1
+        elif orc.top2_margin(olg) < 1e-2 * float(np.max(np.abs(olg))):
+            flips += 1
+        tok = got
+    return dict(checked=count, equal=equal, tie_flips=flips, match=equal + flips == count,
+                oracle="fp64 C restatement, caches seeded with the device's prefill rows, teacher-forced")
+
+
+def cpu_baseline(model, cfg, tokens: int, position: int, ids_check=None) -> dict:
     """The CPU restatements timed on this host's cores: the fp64 check loop (the reference's own CPU
     matmul semantics, LlmMatrixTests.cs:71-80) and an fp32-accumulating, vectorised, OpenMP form of the
     same operations; all cores and one core. The int8 GEMV 896 -> 4864 is the median of 21 runs per
-    form; the 8B decode step is the median over `tokens` steps (fp32 form, all cores: the `value`),
-    fewer for the slow forms, so the whole leg stays around half a minute."""
+    form; the 8B decode steps are the median over `tokens` steps per form and core count (at least 8),
+    so the whole leg stays around a minute. ids_check = (ctx, first, ids, count): before timing, the
+    same model's oracle checks the timed run's first greedy ids (greedy_ids_check)."""
     from oracle import pyoracle as orc
 
     all_cores = orc.num_threads()
@@ -310,6 +338,7 @@ def cpu_baseline(model, cfg, tokens: int, position: int) -> dict:
              num_layers=cfg.num_layers, num_attention_heads=cfg.num_attention_heads,
              num_key_value_heads=cfg.num_key_value_heads, head_dim=cfg.head_dim, rms_norm_eps=cfg.rms_norm_eps)
     om = orc.Model(c, w, inv, att, orc.F16, position + 3 * tokens + 8)
+    ids = greedy_ids_check(model, om, cfg, *ids_check) if ids_check else None
     pos = [position]
 
     def step():
@@ -319,22 +348,21 @@ def cpu_baseline(model, cfg, tokens: int, position: int) -> dict:
     steps = {}
     orc.set_fast_projections(True)
     step()  # pages the weights in
-    for cores, n in ((all_cores, tokens), (1, max(1, tokens // 4))):
+    for cores in (all_cores, 1):
         orc.set_threads(cores)
-        t = _median_s(step, n)
-        steps[f"fp32_vectorised_{cores}_cores"] = dict(tokens_per_s=round(1 / t, 4), tokens=n)
+        t = _median_s(step, tokens)
+        steps[f"fp32_vectorised_{cores}_cores"] = dict(tokens_per_s=round(1 / t, 4), tokens=tokens)
     orc.set_threads(all_cores)
     orc.set_fast_projections(False)
-    n = max(1, tokens // 4)
-    t = _median_s(step, n)
-    steps[f"fp64_check_loop_{all_cores}_cores"] = dict(tokens_per_s=round(1 / t, 4), tokens=n)
+    t = _median_s(step, tokens)
+    steps[f"fp64_check_loop_{all_cores}_cores"] = dict(tokens_per_s=round(1 / t, 4), tokens=tokens)
     value = steps[f"fp32_vectorised_{all_cores}_cores"]["tokens_per_s"]
     return dict(value=value, unit="tokens/s", cores=all_cores, kind="port",
                 sample=f"median decode step of the same int8 Llama-3.1-8B-shaped model (32 layers + lm_head + "
                        f"argmax, positions from {position}) over {tokens} steps: the fp32-accumulating vectorised "
                        f"C restatement on {all_cores} OpenMP threads; the other forms and core counts below",
                 step=steps, gemv_int8_896x4864=gemv, cpu_model=host_cpu_model(),
-                host_cpus=len(os.sched_getaffinity(0)), nproc=os.cpu_count())
+                host_cpus=len(os.sched_getaffinity(0)), nproc=os.cpu_count(), greedy_ids=ids)
 
 
 def host_cpu_model() -> str:
@@ -357,8 +385,8 @@ def main() -> int:
     ap.add_argument("--profile-rounds", type=int, default=4,
                     help="passes over all layers when timing each kernel kind for the roofline")
     ap.add_argument("--cpu-tokens", type=int, default=8,
-                    help="decode steps in the CPU baseline's fp32 all-core sample (a quarter of that for the other "
-                         "forms; 0: skip the CPU baseline)")
+                    help="decode steps per form and core count in the CPU baseline (its median; 0: skip the CPU "
+                         "baseline and the greedy-id check)")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the per-configuration kernel measurements (GEMV, prefill GEMM, attention)")
     ap.add_argument("--eager-step", action="store_true",
@@ -445,8 +473,9 @@ def main() -> int:
     cpu = None
     if args.cpu_tokens > 0:
         log("CPU baseline: exporting the model and running the oracle")
-        cpu = cpu_baseline(model, cfg, args.cpu_tokens, pos)
-        log(f"CPU baseline {cpu['value']} tokens/s on {cpu['cores']} threads")
+        cpu = cpu_baseline(model, cfg, args.cpu_tokens, pos,
+                           ids_check=(args.ctx, first, toks, min(8, args.steps)))
+        log(f"CPU baseline {cpu['value']} tokens/s on {cpu['cores']} threads; greedy ids {cpu['greedy_ids']}")
 
     line = {
         "metric": METRIC,
@@ -479,6 +508,7 @@ def main() -> int:
         "prefill": prefill,
         "configs": configs,
         "cpu_baseline": cpu,
+        "greedy_ids_match": cpu["greedy_ids"]["match"] if cpu else None,
     }
     print(json.dumps(line), flush=True)
     model.dispose()

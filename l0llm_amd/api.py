@@ -583,6 +583,13 @@ class LlmModel:
         check(lib.l0h_model_kv_cache(self.handle, layer, ctypes.byref(k), ctypes.byref(v)))
         return k.value, v.value
 
+    def last_logits(self) -> np.ndarray:
+        """The logits the last decode step left in device memory, read back."""
+        p = ctypes.c_void_p()
+        check(lib.l0h_model_logits(self.handle, ctypes.byref(p)))
+        vocab = self.config.vocab_size
+        return Buffer(self.device, 4 * vocab, ptr=p.value, owned=False).read(np.float32, vocab)
+
     @property
     def step_path(self) -> str:
         """'graph', 'eager' or 'persistent': how a decode step runs."""

@@ -123,13 +123,23 @@ __device__ __forceinline__ u32x4_t perm_f16x8(const uint4& a) {  // a0 a2 a1 a3 
                    (a.z >> 16) | (a.w & 0xFFFF0000u)};
 }
 
+// Whether a gated launch does its work (LaunchGate): a block-uniform scalar test at kernel start.
+__device__ __forceinline__ bool gate_closed(const LaunchGate& g) {
+    return g.run_flag && ((*g.run_flag != 0u) != (g.run_when_set != 0));
+}
+
+// SwiGLU output o stored in y_dtype: reports a value that an fp16 store saturates (or NaN).
+__device__ __forceinline__ void note_range(const LaunchGate& g, int y_dtype, float o) {
+    if (g.range_flag && y_dtype == L0H_F16 && !(fabsf(o) <= 65504.f)) *g.range_flag = 1u;
+}
+
 // WT: weight storage (F16, BF16, or I8PC with fp16 activations and one fp16 scale per weight row).
 // NWV: waves per block (each owns NW columns), so one activation tile in LDS feeds NWV * NW columns.
 template <int WT, int BM, int NW, bool NT, int P = ring_depth(BM, NW), int MF = (NW % 32 == 0 ? 32 : 16),
           int SPS = 1, int NWV = 4>
 __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(1, 2))) void gemm_nk_kernel(
     int M, int N, int K, int k_per_split, const uint16_t* __restrict__ X, const void* __restrict__ Wv,
-    const uint16_t* __restrict__ scales, void* Y, int y_dtype, int epi, float* partial) {
+    const uint16_t* __restrict__ scales, void* Y, int y_dtype, int epi, float* partial, LaunchGate gate) {
     constexpr bool I8 = WT == L0H_I8PC;
     constexpr int DT = I8 ? L0H_F16 : WT;  // MFMA operand type
     constexpr int S = BK * MF / 512;       // MFMAs per K step (k of one MFMA = 512 / MF)
@@ -142,6 +152,7 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(1, 2))
     static_assert(AC >= 1 && MI >= 1 && NJ >= 1, "tile too small");
     __shared__ __attribute__((aligned(16))) uint16_t sa[2][SPS][BM * kLds];
 
+    if (gate_closed(gate)) return;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     // Renumber blocks so that consecutive ids land on one XCD, then walk them as groups of G row
     // blocks: rows of the group first, then K splits, then column blocks, then the next group.
@@ -303,8 +314,11 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(1, 2))
         // brings the up value to the gate lane.
         each_out([&](int row, int col, float v) {
             const float up = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xf, 0xf, false));
-            if (row < M && col < N && (lane & 1) == 0)
-                store_act_sat(Y, y_dtype, (size_t)row * (N / 2) + col / 2, v / (1.0f + __expf(-v)) * up);
+            if (row < M && col < N && (lane & 1) == 0) {
+                const float o = v / (1.0f + __expf(-v)) * up;
+                note_range(gate, y_dtype, o);
+                store_act_sat(Y, y_dtype, (size_t)row * (N / 2) + col / 2, o);
+            }
         });
     } else if (epi == EPI_RESIDUAL) {
         each_out([&](int row, int col, float v) {
@@ -387,7 +401,7 @@ __device__ __forceinline__ uint32_t act_bits16(int dt, float v) {
 // (column pairs (gate, up) -> silu(gate) * up into Y of width N / 2). One vector access where the
 // four columns are inside N and the destination is aligned, else element by element.
 __device__ __forceinline__ void store4(int epi, float* partial, int bz, void* Y, int y_dtype, int M, int N, int row,
-                                       int col, float4 v) {
+                                       int col, float4 v, const LaunchGate& gate) {
     if (row >= M || col >= N) return;
     const float e[4] = {v.x, v.y, v.z, v.w};
     const bool whole = col + 4 <= N;
@@ -403,6 +417,8 @@ __device__ __forceinline__ void store4(int epi, float* partial, int bz, void* Y,
     if (epi == EPI_SWIGLU) {  // N even, col even: pairs (col, col + 1) and (col + 2, col + 3)
         const float o0 = v.x / (1.0f + __expf(-v.x)) * v.y, o1 = v.z / (1.0f + __expf(-v.z)) * v.w;
         const size_t idx = (size_t)row * (N / 2) + col / 2;
+        note_range(gate, y_dtype, o0);
+        if (col + 2 < N) note_range(gate, y_dtype, o1);
         if (whole && y_dtype != L0H_F32 && ((uintptr_t)(static_cast<uint16_t*>(Y) + idx) & 3) == 0) {
             auto sat = [&](float o) {  // as store_act_sat: fp16 saturates at +-65504, NaN stays NaN
                 return y_dtype == L0H_F16 && fabsf(o) > 65504.f ? copysignf(65504.f, o) : o;
@@ -461,7 +477,7 @@ constexpr size_t dma_tile_bytes(int bm, int bn) {
 template <int WT, int BM, int BN, int WGM, int WGN, int NS>
 __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(WGM * WGN / 4, WGM * WGN / 4))) void gemm_dma_kernel(
     int M, int N, int K, int k_per_split, const uint16_t* __restrict__ X, const void* __restrict__ Wv,
-    const uint16_t* __restrict__ scales, void* Y, int y_dtype, int epi, float* partial) {
+    const uint16_t* __restrict__ scales, void* Y, int y_dtype, int epi, float* partial, LaunchGate gate) {
     constexpr bool I8 = WT == L0H_I8PC;
     static_assert(WT == L0H_BF16 || WT == L0H_F16 || I8, "16-bit or int8 weights");
     constexpr int DT = I8 ? L0H_F16 : WT;     // MFMA operand type (int8 weights: fp16 activations)
@@ -482,6 +498,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
     const char* lds = reinterpret_cast<const char*>(gemm_dma_smem);
     const uint32_t lds0 = (uint32_t)(uintptr_t)((__attribute__((address_space(3))) char*)gemm_dma_smem);
 
+    if (gate_closed(gate)) return;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave % WGM, wn = wave / WGM;
@@ -642,14 +659,16 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
         for (int r0 = 0; r0 < BMP; r0 += RPP) {
             const int rl = r0 + tid / C4;
             const float4 v = *reinterpret_cast<const float4*>(tile + rl * LDT + 4 * c4);
-            store4(epi, partial, bz, Y, y_dtype, M, N, m0 + pass * BMP + rl, n0 + 4 * c4, v);
+            store4(epi, partial, bz, Y, y_dtype, M, N, m0 + pass * BMP + rl, n0 + 4 * c4, v, gate);
         }
     }
 }
 
 // Sum of the K splits' partials in split order, then the epilogue: store, add to fp32 Y, or (one
 // thread per column pair) silu(gate) * up into Y[row][c].
-__global__ void splitk_reduce_kernel(const float* partial, int splits, size_t mn, void* Y, int y_dtype, int epi) {
+__global__ void splitk_reduce_kernel(const float* partial, int splits, size_t mn, void* Y, int y_dtype, int epi,
+                                     LaunchGate gate) {
+    if (gate_closed(gate)) return;
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (epi == EPI_SWIGLU) {
         if (2 * i >= mn) return;
@@ -659,7 +678,9 @@ __global__ void splitk_reduce_kernel(const float* partial, int splits, size_t mn
             g += t.x;
             u += t.y;
         }
-        store_act_sat(Y, y_dtype, i, g / (1.0f + __expf(-g)) * u);
+        const float o = g / (1.0f + __expf(-g)) * u;
+        note_range(gate, y_dtype, o);
+        store_act_sat(Y, y_dtype, i, o);
         return;
     }
     if (i >= mn) return;
@@ -749,7 +770,7 @@ Plan plan_for(int m, int n, int k, int cus) {
 
 template <int WT, int BM, int NW, int NWV = 4>
 int launch_tiles(hipStream_t s, int m, int n, int k, const void* x, const void* w, const uint16_t* scales, void* y,
-                 int y_dtype, int epi, int splits, float* ws) {
+                 int y_dtype, int epi, int splits, float* ws, const LaunchGate& gate) {
     constexpr int MF = NW % 32 == 0 ? 32 : 16;
     // Stages of two K steps where K allows, except the 128 x 64 wave tile (its two-step ring, with
     // fewer stages to fit the registers, measured slower) and 128-row eight-wave blocks below
@@ -769,23 +790,23 @@ int launch_tiles(hipStream_t s, int m, int n, int k, const void* x, const void* 
         constexpr int P2 = BM == 256 ? 3 : ring_depth2(NW);  // 256 rows: three stages fit the registers
         if (two && nt)
             gemm_nk_kernel<WT, BM, NW, true, P2, MF, 2, NWV><<<grid, 64 * NWV, 0, s>>>(m, n, k, k_per_split, xp, w,
-                                                                                      scales, y, y_dtype, epi, part);
+                                                                                      scales, y, y_dtype, epi, part, gate);
         else if (two)
             gemm_nk_kernel<WT, BM, NW, false, P2, MF, 2, NWV><<<grid, 64 * NWV, 0, s>>>(m, n, k, k_per_split, xp, w,
-                                                                                       scales, y, y_dtype, epi, part);
+                                                                                       scales, y, y_dtype, epi, part, gate);
     }
     constexpr int P1 = NWV == 8 ? 4 : ring_depth(BM, NW);
     if (!two && nt)
         gemm_nk_kernel<WT, BM, NW, true, P1, MF, 1, NWV><<<grid, 64 * NWV, 0, s>>>(m, n, k, k_per_split, xp, w, scales,
-                                                                                   y, y_dtype, epi, part);
+                                                                                   y, y_dtype, epi, part, gate);
     else if (!two)
         gemm_nk_kernel<WT, BM, NW, false, P1, MF, 1, NWV><<<grid, 64 * NWV, 0, s>>>(m, n, k, k_per_split, xp, w, scales,
-                                                                                    y, y_dtype, epi, part);
+                                                                                    y, y_dtype, epi, part, gate);
     int st = launch_status("gemm_nk");
     if (st || splits == 1) return st;
     const size_t mn = (size_t)m * n;
     const size_t threads = epi == EPI_SWIGLU ? mn / 2 : mn;
-    splitk_reduce_kernel<<<ceil_div(threads, 256), 256, 0, s>>>(ws, splits, mn, y, y_dtype, epi);
+    splitk_reduce_kernel<<<ceil_div(threads, 256), 256, 0, s>>>(ws, splits, mn, y, y_dtype, epi, gate);
     return launch_status("gemm splitk reduce");
 }
 
@@ -877,7 +898,7 @@ bool lds_plan_for(int dtype, int m, int n, int k, int cus, LdsPlan& out) {
 
 template <int WT, int BM, int BN, int WGM, int WGN>
 int launch_lds(hipStream_t s, int m, int n, int k, const void* x, const void* w, const uint16_t* scales, void* y,
-               int y_dtype, int epi, int splits, float* ws) {
+               int y_dtype, int epi, int splits, float* ws, const LaunchGate& gate) {
     constexpr int NT = 64 * WGM * WGN;
     constexpr size_t stage = (size_t)BM * 128 + (size_t)BN * (WT == L0H_I8PC ? 64 : 128);
     constexpr int kFit = (int)(160 * 1024 / stage);  // ring stages that fit the LDS
@@ -899,7 +920,7 @@ int launch_lds(hipStream_t s, int m, int n, int k, const void* x, const void* w,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
         if (attr != hipSuccess) return fail(L0H_ERR_DEVICE, std::string("hipFuncSetAttribute: ") + hipGetErrorString(attr));
         gemm_dma_kernel<WT, BM, BN, WGM, WGN, NS><<<grid, NT, bytes, s>>>(
-            m, n, k, k_per_split, static_cast<const uint16_t*>(x), w, scales, y, y_dtype, epi, splits > 1 ? ws : nullptr);
+            m, n, k, k_per_split, static_cast<const uint16_t*>(x), w, scales, y, y_dtype, epi, splits > 1 ? ws : nullptr, gate);
         return L0H_OK;
     };
     int st;
@@ -914,40 +935,40 @@ int launch_lds(hipStream_t s, int m, int n, int k, const void* x, const void* w,
     if (st || splits == 1) return st;
     const size_t mn = (size_t)m * n;
     const size_t threads = epi == EPI_SWIGLU ? mn / 2 : mn;
-    splitk_reduce_kernel<<<ceil_div(threads, 256), 256, 0, s>>>(ws, splits, mn, y, y_dtype, epi);
+    splitk_reduce_kernel<<<ceil_div(threads, 256), 256, 0, s>>>(ws, splits, mn, y, y_dtype, epi, gate);
     return launch_status("gemm splitk reduce");
 }
 
 template <int WT>
 int launch_lds_plan(hipStream_t s, const LdsPlan& p, int m, int n, int k, const void* x, const void* w,
-                    const uint16_t* scales, void* y, int y_dtype, int epi, float* ws) {
+                    const uint16_t* scales, void* y, int y_dtype, int epi, float* ws, const LaunchGate& gate) {
     if (p.bm == 256 && p.bn == 256)
-        return launch_lds<WT, 256, 256, 2, 4>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws);
+        return launch_lds<WT, 256, 256, 2, 4>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws, gate);
     if (p.bm == 128 && p.bn == 256 && p.waves == 4)
-        return launch_lds<WT, 128, 256, 2, 2>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws);
+        return launch_lds<WT, 128, 256, 2, 2>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws, gate);
     if (p.bm == 128 && p.bn == 256)
-        return launch_lds<WT, 128, 256, 2, 4>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws);
+        return launch_lds<WT, 128, 256, 2, 4>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws, gate);
     if (p.bm == 128 && p.bn == 64)
-        return launch_lds<WT, 128, 64, 2, 2>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws);
+        return launch_lds<WT, 128, 64, 2, 2>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws, gate);
     if (p.bm == 64 && p.bn == 128)
-        return launch_lds<WT, 64, 128, 2, 2>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws);
+        return launch_lds<WT, 64, 128, 2, 2>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws, gate);
     if (p.bm == 64 && p.bn == 64)
-        return launch_lds<WT, 64, 64, 2, 2>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws);
+        return launch_lds<WT, 64, 64, 2, 2>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws, gate);
     if (p.bm == 256 && p.bn == 128)
-        return launch_lds<WT, 256, 128, 4, 2>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws);
-    return launch_lds<WT, 128, 128, 2, 2>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws);
+        return launch_lds<WT, 256, 128, 4, 2>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws, gate);
+    return launch_lds<WT, 128, 128, 2, 2>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws, gate);
 }
 
 template <int WT>
 int launch_plan(hipStream_t s, const Plan& p, int m, int n, int k, const void* x, const void* w,
-                const uint16_t* scales, void* y, int y_dtype, int epi, float* ws) {
+                const uint16_t* scales, void* y, int y_dtype, int epi, float* ws, const LaunchGate& gate) {
     if (p.bm == 256 && p.nw == 32 && p.waves == 8)
-        return launch_tiles<WT, 256, 32, 8>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws);
+        return launch_tiles<WT, 256, 32, 8>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws, gate);
     if (p.bm == 128 && p.nw == 32 && p.waves == 8)
-        return launch_tiles<WT, 128, 32, 8>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws);
+        return launch_tiles<WT, 128, 32, 8>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws, gate);
 #define L0H_GEMM_CASE(BM_, NW_)                                                                                  \
     if (p.bm == BM_ && p.nw == NW_ && p.waves == 4)                                                              \
-        return launch_tiles<WT, BM_, NW_>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws);
+        return launch_tiles<WT, BM_, NW_>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws, gate);
     L0H_GEMM_CASE(64, 16)
     L0H_GEMM_CASE(64, 32)
     L0H_GEMM_CASE(64, 64)
@@ -970,7 +991,8 @@ size_t gemm_workspace_bytes(int m, int n, int k, int compute_units) {
 }
 
 int launch_gemm_nk(hipStream_t s, int dtype, int m, int n, int k, const void* x, const void* w,
-                   void* y, int y_dtype, float* ws, size_t ws_bytes, int cus, const uint16_t* scales, int epilogue) {
+                   void* y, int y_dtype, float* ws, size_t ws_bytes, int cus, const uint16_t* scales, int epilogue,
+                   const LaunchGate& gate) {
     if (m <= 0 || n <= 0 || k <= 0) return fail(L0H_ERR_INVALID_ARG, "GEMM sizes must be positive");
     if (epilogue != EPI_STORE && epilogue != EPI_RESIDUAL && epilogue != EPI_SWIGLU)
         return fail(L0H_ERR_INVALID_ARG, "GEMM epilogue is store, residual or SwiGLU");
@@ -983,7 +1005,8 @@ int launch_gemm_nk(hipStream_t s, int dtype, int m, int n, int k, const void* x,
         if (!scales) return fail(L0H_ERR_INVALID_ARG, "int8 GEMM needs the per-row scales");
         if (!aligned) return fail(L0H_ERR_UNSUPPORTED, "int8 GEMM needs K a multiple of 32 and 16-byte aligned operands");
     } else if (!aligned) {
-        if (epilogue != EPI_STORE) return fail(L0H_ERR_UNSUPPORTED, "fused GEMM epilogues need K a multiple of 32");
+        if (epilogue != EPI_STORE || gate.run_flag)
+            return fail(L0H_ERR_UNSUPPORTED, "fused or gated GEMM launches need K a multiple of 32");
         const size_t mn = (size_t)m * n;
         gemm_nk_generic_kernel<<<ceil_div(mn, 256), 256, 0, s>>>(dtype, m, n, k, static_cast<const uint16_t*>(x),
                                                                  static_cast<const uint16_t*>(w), y, y_dtype);
@@ -993,17 +1016,17 @@ int launch_gemm_nk(hipStream_t s, int dtype, int m, int n, int k, const void* x,
     if (lds_plan_for(dtype, m, n, k, cus, lp)) {
         while (lp.splits > 1 && (size_t)lp.splits * m * n * sizeof(float) > ws_bytes) lp.splits /= 2;
         switch (dtype) {
-        case L0H_BF16: return launch_lds_plan<L0H_BF16>(s, lp, m, n, k, x, w, nullptr, y, y_dtype, epilogue, ws);
-        case L0H_F16: return launch_lds_plan<L0H_F16>(s, lp, m, n, k, x, w, nullptr, y, y_dtype, epilogue, ws);
-        default: return launch_lds_plan<L0H_I8PC>(s, lp, m, n, k, x, w, scales, y, y_dtype, epilogue, ws);
+        case L0H_BF16: return launch_lds_plan<L0H_BF16>(s, lp, m, n, k, x, w, nullptr, y, y_dtype, epilogue, ws, gate);
+        case L0H_F16: return launch_lds_plan<L0H_F16>(s, lp, m, n, k, x, w, nullptr, y, y_dtype, epilogue, ws, gate);
+        default: return launch_lds_plan<L0H_I8PC>(s, lp, m, n, k, x, w, scales, y, y_dtype, epilogue, ws, gate);
         }
     }
     Plan p = plan_for(m, n, k, cus);
     while (p.splits > 1 && (size_t)p.splits * m * n * sizeof(float) > ws_bytes) p.splits /= 2;
     switch (dtype) {
-    case L0H_BF16: return launch_plan<L0H_BF16>(s, p, m, n, k, x, w, nullptr, y, y_dtype, epilogue, ws);
-    case L0H_F16: return launch_plan<L0H_F16>(s, p, m, n, k, x, w, nullptr, y, y_dtype, epilogue, ws);
-    default: return launch_plan<L0H_I8PC>(s, p, m, n, k, x, w, scales, y, y_dtype, epilogue, ws);
+    case L0H_BF16: return launch_plan<L0H_BF16>(s, p, m, n, k, x, w, nullptr, y, y_dtype, epilogue, ws, gate);
+    case L0H_F16: return launch_plan<L0H_F16>(s, p, m, n, k, x, w, nullptr, y, y_dtype, epilogue, ws, gate);
+    default: return launch_plan<L0H_I8PC>(s, p, m, n, k, x, w, scales, y, y_dtype, epilogue, ws, gate);
     }
 }
 

@@ -7,11 +7,7 @@ namespace l0h {
 namespace {
 
 // Any shape: one wave per (activation row, output row), scalar loads. STORE / RESIDUAL only.
-__global__ __launch_bounds__(kBlock) void gemv_nk_generic_kernel(const GemvParams p) {
-    const int lane = threadIdx.x & 63;
-    const size_t task = (size_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
-    if (task >= (size_t)p.m * p.n) return;
-    const int mr = (int)(task / p.n), row = (int)(task % p.n);
+__device__ void generic_task(const GemvParams& p, int lane, int mr, int row) {
     const int K = p.k;
     float acc = 0.f;
     for (int k = lane; k < K; k += 64) {
@@ -34,6 +30,15 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_generic_kernel(const GemvParam
         else
             store_act(p.y, p.y_dtype, (size_t)mr * p.n + row, acc);
     }
+}
+
+__global__ __launch_bounds__(kBlock) void gemv_nk_generic_kernel(const GemvParams p) {
+    if (p.run_flag && ((*p.run_flag != 0u) != (p.run_when_set != 0))) return;  // gated launch
+    const int lane = threadIdx.x & 63;
+    // one wave per (activation row, output) task, grid-stride over the tasks
+    for (size_t task = (size_t)blockIdx.x * kWaves + (threadIdx.x >> 6); task < (size_t)p.m * p.n;
+         task += (size_t)gridDim.x * kWaves)
+        generic_task(p, lane, (int)(task / p.n), (int)(task % p.n));
 }
 
 }  // namespace
@@ -88,11 +93,16 @@ int launch_gemv_nk(hipStream_t s, const GemvParams& p0) {
     }
     if (p0.argmax_keys && (p0.m != 1 || p0.epilogue != EPI_STORE))
         return fail(L0H_ERR_INVALID_ARG, "per-wave argmax keys need one activation row and the store epilogue");
-    if (!aligned || !fits) {
+    // A gated launch (a rarely taken fallback decided on the device) is one launch of the generic
+    // kernel over every activation row: the fast path below issues one launch per group of rows.
+    if (!aligned || !fits || p0.run_flag) {
         if (fused || p0.argmax_keys) return fail(L0H_ERR_UNSUPPORTED, "fused GEMV shape not supported");
         GemvParams p = p0;
         const size_t tasks = (size_t)p.m * p.n;
-        gemv_nk_generic_kernel<<<ceil_div(tasks, kWaves), kBlock, 0, s>>>(p);
+        // at most 8 blocks per CU, striding over the tasks (a gated launch that does nothing
+        // dispatches no more than that)
+        const size_t cap = (size_t)8 * std::max(1, p.compute_units > 0 ? p.compute_units : 256);
+        gemv_nk_generic_kernel<<<(unsigned)std::min<size_t>(ceil_div(tasks, kWaves), cap), kBlock, 0, s>>>(p);
         return launch_status("gemv_nk_generic");
     }
     // Activation rows in groups of 8/4/2/1 (each group reads W once), as many as fit the tile.

@@ -630,6 +630,8 @@ int launch_fast(hipStream_t s, const GemvParams& p) {
         const unsigned cap = std::min<unsigned>((unsigned)p.max_blocks, (unsigned)(occ_blocks * std::max(1, p.compute_units)));
         grid = std::min(grid, cap);
     }
+    if (p.argmax_keys && (size_t)grid * kWaves > (size_t)std::max(0, p.argmax_capacity))
+        return fail(L0H_ERR_INVALID_OP, "GEMV greedy keys: the launch has more waves than the key buffer holds");
     if (p.launched_waves) *p.launched_waves = (int)(grid * kWaves);
     kern<<<grid, kBlock, shmem, s>>>(p, k_pad);
     return launch_status("gemv_nk");

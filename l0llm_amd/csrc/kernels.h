@@ -14,6 +14,17 @@ enum GemvEpilogue : int {
     EPI_QKV = 3,       // fused q|k|v rows, RoPE on q/k, k/v written to the cache (:296-322)
 };
 
+// Device-side gating of a GEMM / GEMV launch, and range reporting of a 16-bit SwiGLU output: the
+// launch does its work only when (*run_flag != 0) == run_when_set (always when run_flag is null),
+// and a SwiGLU epilogue that stores fp16 sets *range_flag when a value is beyond fp16's range or
+// NaN (the stored value saturates at +-65504). The prefill uses both to run a layer's down
+// projection on fp32 rows instead of the saturated fp16 ones.
+struct LaunchGate {
+    const unsigned* run_flag = nullptr;
+    int run_when_set = 0;
+    unsigned* range_flag = nullptr;
+};
+
 struct GemvParams {
     // weights [N, K]
     int w_dtype = L0H_I8PC;
@@ -55,9 +66,14 @@ struct GemvParams {
     int compute_units = 0;  // with max_blocks: caps the grid at the blocks resident in one round
     // EPI_STORE with one activation row: every wave also writes the greedy key (greedy_key) of the
     // largest value it stored to argmax_keys[wave of the grid], so an argmax needs only those keys;
-    // launched_waves (host memory) receives the launch's wave count.
+    // launched_waves (host memory) receives the launch's wave count; argmax_capacity is the number
+    // of keys argmax_keys holds, and a launch whose grid has more waves is refused.
     unsigned long long* argmax_keys = nullptr;
+    int argmax_capacity = 0;
     int* launched_waves = nullptr;
+    // The launch does its work only when (*run_flag != 0) == run_when_set (null: always).
+    const unsigned* run_flag = nullptr;
+    int run_when_set = 0;
 };
 
 // Persistent-grid size for weight-streaming kernels on a device with `compute_units` CUs:
@@ -153,7 +169,7 @@ bool attention_prefill_tiled(const AttnParams& p);
 size_t gemm_workspace_bytes(int m, int n, int k, int compute_units);
 int launch_gemm_nk(hipStream_t s, int dtype, int m, int n, int k, const void* x, const void* w,
                    void* y, int y_dtype, float* ws, size_t ws_bytes, int compute_units,
-                   const uint16_t* scales = nullptr, int epilogue = EPI_STORE);
+                   const uint16_t* scales = nullptr, int epilogue = EPI_STORE, const LaunchGate& gate = LaunchGate{});
 
 // ---- persistent decode step (step_kernel.hip) ----
 // One weight-streaming phase of the step: a projection with its epilogue.

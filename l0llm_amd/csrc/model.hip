@@ -121,10 +121,14 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_rows16_kernel(const float* x, 
     for (int i = threadIdx.x; i < n; i += kBlock) o[i] = cvt(xr[i] * inv * w[i]);
 }
 
-// fp32 activations -> the weight dtype (F16 / BF16) for the MFMA GEMM (fp16 saturating).
-__global__ void to_16bit_kernel(const float* x, uint16_t* y, size_t n, int dt) {
+// fp32 activations -> the weight dtype (F16 / BF16) for the MFMA GEMM (fp16 saturating; *flag is
+// set where an fp16 value saturates or is NaN).
+__global__ void to_16bit_kernel(const float* x, uint16_t* y, size_t n, int dt, unsigned* flag) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) store_act_sat(y, dt, i, x[i]);
+    if (i >= n) return;
+    const float v = x[i];
+    if (dt == L0H_F16 && !(fabsf(v) <= 65504.f)) *flag = 1u;
+    store_act_sat(y, dt, i, v);
 }
 
 }  // namespace
@@ -168,6 +172,7 @@ struct l0h_model {
     // Greedy keys the lm_head GEMV writes, one per wave of its grid (lm_waves, set when the lm_head
     // launch is enqueued; 0 before), so the argmax reads those keys instead of the logits.
     unsigned long long* lm_keys = nullptr;
+    int lm_keys_capacity = 0;
     int lm_waves = 0;
     float* probe_buf = nullptr;  // a probe's stage values, allocated by the first probe step
     int attn_splits = 1;
@@ -177,6 +182,9 @@ struct l0h_model {
     float *pf_hidden = nullptr, *pf_xn = nullptr, *pf_qkv = nullptr, *pf_q = nullptr, *pf_attn = nullptr,
           *pf_gu = nullptr, *pf_act = nullptr, *pf_ws = nullptr;
     uint16_t* pf_x16 = nullptr;
+    // Per layer: set when a value of the chunk's fp16 SwiGLU rows (down's GEMM input) saturated;
+    // that layer's down projection then runs on the fp32 rows instead. Cleared per chunk.
+    unsigned* pf_flags = nullptr;
     int* pf_ids = nullptr;
     size_t pf_ws_bytes = 0;
     hipGraphExec_t step_exec = nullptr;
@@ -553,6 +561,7 @@ int launch_op(l0h_model* m, hipStream_t s, int kind, int li, float* store_to = n
         g.y = m->logits;
         g.y_dtype = L0H_F32;
         g.argmax_keys = m->lm_keys;
+        g.argmax_capacity = m->lm_keys_capacity;
         g.launched_waves = &m->lm_waves;
         return launch_gemv_nk(s, g);
     default: {  // LlmModel.cs:398, plus device-side feedback for back-to-back decode
@@ -585,6 +594,7 @@ int enqueue_step(l0h_model* m, hipStream_t s, StepTimer* t = nullptr) {
     return st;
 }
 
+#ifdef L0H_WITH_STEP_KERNEL
 // Sets up the persistent step: the phase table (four projections per layer, then lm_head), its
 // buffers, and the LDS tile sizes. Leaves m->persistent false where the kernel does not apply.
 int setup_persistent(l0h_model* m) {
@@ -677,10 +687,15 @@ int setup_persistent(l0h_model* m) {
     return L0H_OK;
 }
 
+#endif  // L0H_WITH_STEP_KERNEL
+
 // After a persistent step: a grid barrier that ran out of spins leaves the error flag set; the
 // counters are reset and the step is reported as failed.
 int check_persistent(l0h_model* m) {
     if (!m->persistent) return L0H_OK;
+#ifndef L0H_WITH_STEP_KERNEL
+    return fail(L0H_ERR_UNSUPPORTED, "the persistent decode step is not built into this library");
+#else
     unsigned e = 0;
     int st = l0h_read(m->dev, m->sp.err, 0, &e, sizeof e);
     if (st) return st;
@@ -688,6 +703,7 @@ int check_persistent(l0h_model* m) {
     (void)l0h_fill_zero(m->dev, m->sp.bar, 4 * sizeof(unsigned));
     (void)l0h_synchronize(m->dev);
     return fail(L0H_ERR_DEVICE, "the persistent decode step's grid barrier timed out; its results are invalid");
+#endif
 }
 
 int ensure_graph(l0h_model* m) {
@@ -715,7 +731,9 @@ int ensure_graph(l0h_model* m) {
 // One step with whatever token/position the device holds: the captured graph, or the same
 // kernels enqueued one by one in eager mode.
 int launch_step(l0h_model* m) {
+#ifdef L0H_WITH_STEP_KERNEL
     if (m->persistent) return launch_decode_step(m->dev->stream, m->sp, m->step_blocks);
+#endif
     if (m->eager) return enqueue_step(m, m->dev->stream);
     L0H_HIP_TRY(hipGraphLaunch(m->step_exec, m->dev->stream));
     return L0H_OK;
@@ -767,7 +785,8 @@ int ensure_prefill(l0h_model* m) {
     if ((st = alloc_t(m, T * H, &m->pf_hidden)) || (st = alloc_t(m, T * H, &m->pf_xn)) ||
         (st = alloc_t(m, T * nqkv, &m->pf_qkv)) || (st = alloc_t(m, (size_t)T * m->qd, &m->pf_q)) ||
         (st = alloc_t(m, (size_t)T * m->qd, &m->pf_attn)) || (st = alloc_t(m, T * 2 * I, &m->pf_gu)) ||
-        (st = alloc_t(m, T * I, &m->pf_act)) || (st = alloc_t(m, (size_t)T, &m->pf_ids)))
+        (st = alloc_t(m, T * I, &m->pf_act)) || (st = alloc_t(m, (size_t)T, &m->pf_ids)) ||
+        (st = alloc_t(m, (size_t)c.num_layers, &m->pf_flags)))
         return st;
     if (m->storage != L0H_F32) {
         const size_t kmax = std::max<size_t>({H, I, (size_t)m->qd});
@@ -788,7 +807,7 @@ int ensure_prefill(l0h_model* m) {
 // y = x W^T for T rows on the multi-row GEMV (fp32 activations): STORE into y (+ bias) or
 // RESIDUAL into resid.
 int gemv_rows(l0h_model* m, hipStream_t s, const Proj& P, const float* x, int T, float* y, const float* bias,
-              int epilogue, float* resid) {
+              int epilogue, float* resid, const unsigned* run_if_set = nullptr) {
     GemvParams g;
     g.w_dtype = m->storage;
     g.w = P.w;
@@ -805,15 +824,17 @@ int gemv_rows(l0h_model* m, hipStream_t s, const Proj& P, const float* x, int T,
     g.resid = resid;
     g.max_blocks = gemv_max_blocks(m->dev->compute_units);
     g.compute_units = m->dev->compute_units;
+    g.run_flag = run_if_set;
+    g.run_when_set = 1;
     return launch_gemv_nk(s, g);
 }
 
 // y = x16 W^T for T rows on the MFMA GEMM (x16 in the operand dtype) with the GEMM's epilogue:
 // STORE (+ bias, fp32 y), RESIDUAL (fp32 y += result) or SWIGLU (y of width n / 2 in y_dtype).
 int gemm_rows(l0h_model* m, hipStream_t s, const Proj& P, const uint16_t* x16, int T, void* y, int y_dtype,
-              const float* bias, int epilogue) {
+              const float* bias, int epilogue, const LaunchGate& gate = LaunchGate{}) {
     int st = launch_gemm_nk(s, m->storage, T, P.n, P.k, x16, P.w, y, y_dtype, m->pf_ws, m->pf_ws_bytes,
-                            m->dev->compute_units, P.s, epilogue);
+                            m->dev->compute_units, P.s, epilogue, gate);
     if (st || !bias) return st;
     return launch_bias_add(s, static_cast<float*>(y), bias, P.n, T);
 }
@@ -833,6 +854,9 @@ int prefill_chunk(l0h_model* m, const int* ids, int pos0, int T) {
     uint16_t* act16 = reinterpret_cast<uint16_t*>(m->pf_gu);  // T x I 16-bit rows in the gate|up buffer
     int st = l0h_write(m->dev, m->pf_ids, 0, ids, (size_t)T * sizeof(int));
     if (st) return st;
+    // fp16 SwiGLU rows for down's GEMM: each layer's flag records a saturated value
+    const bool flagged = gemm_i && xdt == L0H_F16;
+    if (flagged && (st = launch_fill(s, reinterpret_cast<float*>(m->pf_flags), 0.f, c.num_layers))) return st;
     if ((st = launch_embedding(s, m->pf_ids, m->embedding, m->pf_hidden, H, (size_t)T * H))) return st;
     auto norm = [&](const float* w) {
         if (!gemm_h) return launch_rmsnorm(s, m->pf_hidden, nullptr, w, m->pf_xn, c.rms_norm_eps, H, T, 0);
@@ -878,8 +902,11 @@ int prefill_chunk(l0h_model* m, const int* ids, int pos0, int T) {
         if (st) return st;
         if ((st = norm(L.post_norm))) return st;
         const size_t na = (size_t)T * I;
+        unsigned* flag = m->pf_flags + li;
+        LaunchGate report;  // the gate|up launch that writes fp16 rows flags a saturated value
+        if (flagged) report.range_flag = flag;
         if (gemm_h) {  // SwiGLU in the GEMM epilogue, in the dtype down reads
-            st = gemm_i ? gemm_rows(m, s, L.gu, m->pf_x16, T, act16, xdt, nullptr, EPI_SWIGLU)
+            st = gemm_i ? gemm_rows(m, s, L.gu, m->pf_x16, T, act16, xdt, nullptr, EPI_SWIGLU, report)
                         : gemm_rows(m, s, L.gu, m->pf_x16, T, m->pf_act, L0H_F32, nullptr, EPI_SWIGLU);
             if (st) return st;
         } else {
@@ -887,13 +914,31 @@ int prefill_chunk(l0h_model* m, const int* ids, int pos0, int T) {
             swiglu_rows_kernel<<<ceil_div(na, 256), 256, 0, s>>>(m->pf_gu, m->pf_act, na);
             if ((st = launch_status("swiglu_rows"))) return st;
             if (gemm_i) {  // the gate|up buffer is free again: the 16-bit rows go there
-                to_16bit_kernel<<<ceil_div(na, 256), 256, 0, s>>>(m->pf_act, act16, na, xdt);
+                to_16bit_kernel<<<ceil_div(na, 256), 256, 0, s>>>(m->pf_act, act16, na, xdt, flag);
                 if ((st = launch_status("to_16bit"))) return st;
             }
         }
-        st = gemm_i ? gemm_rows(m, s, L.down, act16, T, m->pf_hidden, L0H_F32, nullptr, EPI_RESIDUAL)
-                    : gemv_rows(m, s, L.down, m->pf_act, T, nullptr, nullptr, EPI_RESIDUAL, m->pf_hidden);
-        if (st) return st;
+        if (!gemm_i) {
+            if ((st = gemv_rows(m, s, L.down, m->pf_act, T, nullptr, nullptr, EPI_RESIDUAL, m->pf_hidden))) return st;
+            continue;
+        }
+        // down on the 16-bit rows unless the layer's flag is set; otherwise (decided on the device)
+        // the fp32 SwiGLU rows (recomputed by the GEMM where only the 16-bit ones were written) through
+        // the multi-row GEMV, as a decode step's down reads the fp32 row of a flagged layer.
+        LaunchGate unless_flagged;
+        if (flagged) {
+            unless_flagged.run_flag = flag;
+            unless_flagged.run_when_set = 0;
+        }
+        if ((st = gemm_rows(m, s, L.down, act16, T, m->pf_hidden, L0H_F32, nullptr, EPI_RESIDUAL, unless_flagged)))
+            return st;
+        if (!flagged) continue;
+        LaunchGate if_flagged;
+        if_flagged.run_flag = flag;
+        if_flagged.run_when_set = 1;
+        if (gemm_h && (st = gemm_rows(m, s, L.gu, m->pf_x16, T, m->pf_act, L0H_F32, nullptr, EPI_SWIGLU, if_flagged)))
+            return st;
+        if ((st = gemv_rows(m, s, L.down, m->pf_act, T, nullptr, nullptr, EPI_RESIDUAL, m->pf_hidden, flag))) return st;
     }
     return L0H_OK;
 }
@@ -1028,19 +1073,21 @@ int l0h_model_create(l0h_device* dev, const l0h_model_config* cfg, int precision
     a.splits = m->attn_splits;
     if ((st = alloc_owned(m, attention_partials_bytes(a), reinterpret_cast<void**>(&m->attn_partials)))) return bail(st);
     if ((st = alloc_t(m, (size_t)argmax_blocks(c.vocab_size), &m->argmax_partials))) return bail(st);
-    // at most one wave per row group of two rows (the GEMV's smallest), plus a block's spare waves
-    if ((st = alloc_t(m, (size_t)c.vocab_size / 2 + 8, &m->lm_keys))) return bail(st);
+    // one key per wave of the lm_head launch: at most one wave per row (1-row items), plus a block's
+    // spare waves; the launch checks its wave count against this capacity
+    m->lm_keys_capacity = c.vocab_size + kWaves;
+    if ((st = alloc_t(m, (size_t)m->lm_keys_capacity, &m->lm_keys))) return bail(st);
     if ((st = alloc_t(m, 1, &m->argmax_ticket))) return bail(st);
     if ((st = l0h_fill_zero(dev, m->argmax_ticket, sizeof(unsigned)))) return bail(st);
     const int zeros[4] = {0, 0, 0, 0};
     if ((st = l0h_write(dev, m->token, 0, zeros, sizeof(zeros)))) return bail(st);
     // L0H_STEP_KERNEL=1 asks for the persistent decode step (step_kernel.hip). Its first GPU run
     // ended in an illegal-address fault whose cause is not established (the kernel's indexing
-    // checks out on the CPU), so the request is refused and the graph step is the only one.
+    // checks out on the CPU), so it is not compiled into the library, the request is refused and
+    // the graph step is the only one.
     const char* step_env = std::getenv("L0H_STEP_KERNEL");
     if (step_env && std::atoi(step_env) == 1)
         return bail(fail(L0H_ERR_UNSUPPORTED, "the persistent decode step is disabled (unexplained GPU fault)"));
-    (void)setup_persistent;
     if ((st = l0h_synchronize(dev))) return bail(st);
     *out = m;
     return L0H_OK;

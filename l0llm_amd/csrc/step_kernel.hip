@@ -21,6 +21,11 @@
 // written by control waves only, published with an agent-scope release fence before the arrival at
 // a grid barrier and read after an agent-scope acquire fence. Every grid-barrier wait has a spin
 // limit; a wait that runs out sets an error flag and the kernel finishes without waiting again.
+//
+// Not part of the library build: its first GPU run ended in an illegal-address fault whose cause is
+// not established, so the file compiles to nothing unless L0H_WITH_STEP_KERNEL is defined (the CPU
+// emulation test defines it; the library build does not).
+#ifdef L0H_WITH_STEP_KERNEL
 #include <cmath>
 
 #include "gemv_kernel.h"
@@ -650,3 +655,4 @@ int step_attention_splits(int blocks, int n_kv, int group) {
 }
 
 }  // namespace l0h
+#endif  // L0H_WITH_STEP_KERNEL

@@ -463,6 +463,13 @@ float orc_top2_margin(const float* logits, int n) {
 
 static int g_fast_projections = 0;
 void orc_set_fast_projections(int on) { g_fast_projections = on; }
+static int g_device_rounding = 0;
+void orc_set_device_rounding(int on) { g_device_rounding = on; }
+
+/* v rounded to fp16 and back (round to nearest even). */
+static void round_f16(float* v, int n) {
+    for (int i = 0; i < n; i++) v[i] = orc_f16_to_f32(orc_f32_to_f16(v[i]));
+}
 
 static void project(const orc_matrix* m, const float* x, float* y) {
     if (g_fast_projections)
@@ -502,11 +509,17 @@ void orc_layer_forward(const orc_model* m, int li, float* hidden, int position) 
     orc_kv_store(k, v, m->k_cache[li], m->v_cache[li], m->cache_dtype, position, kvd, 1); /* :322 */
     orc_attention_decode(q, m->k_cache[li], m->v_cache[li], m->cache_dtype, attn, c->head_dim,
                          c->n_heads, c->n_kv_heads, position + 1, m->max_seq_len); /* :325-327 */
+    if (g_device_rounding && m->cache_dtype == ORC_F16) round_f16(attn, qd); /* stored as fp16 */
     project(&L->o, attn, proj);                                                 /* :333 */
     orc_rmsnorm(hidden, proj, L->post_norm, normed, c->eps, h, 1, 1);           /* :183-184 */
     project(&L->gate, normed, gate);                                            /* :188 */
     project(&L->up, normed, up);
     orc_swiglu(gate, up, inter); /* :189 */
+    if (g_device_rounding) { /* the fp16 copy, unless a value is beyond fp16's range (or NaN) */
+        int wide = 0;
+        for (int i = 0; i < inter; i++) wide |= !(fabsf(gate[i]) <= 65504.f);
+        if (!wide) round_f16(gate, inter);
+    }
     project(&L->down, gate, down); /* :190 */
     orc_add(hidden, down, h);      /* :194 */
 

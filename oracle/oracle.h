@@ -196,6 +196,12 @@ void orc_gemv_nk_f32acc(int wdtype, int rows, int N, int K, const float* x, cons
 /* 1: orc_model_step / orc_layer_forward project with orc_gemv_nk_f32acc (the timed CPU baseline);
  * 0 (default): with the fp64 check loop orc_gemv_nk. */
 void orc_set_fast_projections(int on);
+/* 1: orc_layer_forward also rounds the two activations that the HIP decode step stores as fp16
+ * between its kernels (for int8 / 16-bit weights with an fp16 cache): the attention output, and the
+ * SwiGLU output when every value of it is within fp16's range (the step keeps the fp32 row
+ * otherwise). Not the reference's arithmetic (which keeps both in fp32): it separates that
+ * documented storage choice from arithmetic errors in deep-model comparisons. 0 (default): off. */
+void orc_set_device_rounding(int on);
 
 #ifdef __cplusplus
 }

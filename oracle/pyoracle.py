@@ -72,6 +72,7 @@ _sig("orc_top2_margin", [P, ctypes.c_int], ctypes.c_float)
 _sig("orc_num_threads", [], ctypes.c_int)
 _sig("orc_set_threads", [ctypes.c_int])
 _sig("orc_set_fast_projections", [ctypes.c_int])
+_sig("orc_set_device_rounding", [ctypes.c_int])
 _sig("orc_gemv_nk_f32acc", [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, P, P, P, P])
 
 
@@ -92,6 +93,12 @@ def set_threads(n: int) -> None:
 
 def set_fast_projections(on: bool) -> None:
     _lib.orc_set_fast_projections(int(bool(on)))
+
+
+def set_device_rounding(on: bool) -> None:
+    """Rounds the attention and SwiGLU outputs to fp16 inside the model step, where the HIP decode
+    step stores them as fp16 (orc_set_device_rounding); off by default (the reference's fp32)."""
+    _lib.orc_set_device_rounding(int(bool(on)))
 
 
 def num_threads() -> int:

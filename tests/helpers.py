@@ -99,3 +99,13 @@ def rel_err(a, b) -> float:
     a = np.asarray(a, dtype=np.float64)
     b = np.asarray(b, dtype=np.float64)
     return float(np.max(np.abs(a - b)) / max(np.max(np.abs(b)), 1e-30))
+
+
+def elementwise_excess(got, want, rtol: float = 1e-2, floor_frac: float = 1e-4) -> float:
+    """Per-element relative bound for 16-bit outputs: |got - want| <= rtol * |want| + floor, where
+    floor = floor_frac * max|want| stands in for the relative bound at values near zero (where a
+    relative error is undefined). Returns the largest |got - want| / bound; at most 1 passes."""
+    got = np.asarray(got, dtype=np.float64)
+    want = np.asarray(want, dtype=np.float64)
+    bound = rtol * np.abs(want) + floor_frac * max(float(np.max(np.abs(want))), 1e-30)
+    return float(np.max(np.abs(got - want) / bound))

@@ -56,7 +56,7 @@ def build(out_dir: str) -> str:
         raise FileNotFoundError("clang++ not found")
     src = generate(out_dir)
     exe = os.path.join(out_dir, "step_emu")
-    cmd = [cxx, "-std=c++20", "-O1", "-g", "-fsanitize=address", "-fno-omit-frame-pointer",
+    cmd = [cxx, "-std=c++20", "-O1", "-g", "-DL0H_WITH_STEP_KERNEL", "-fsanitize=address", "-fno-omit-frame-pointer",
            "-I", os.path.join(HERE, "include"), "-I", out_dir, "-I", CSRC, src,
            os.path.join(CSRC, "errors.cpp"), "-o", exe, "-lpthread"]
     subprocess.run(cmd, check=True, capture_output=True, text=True)

@@ -8,7 +8,7 @@ import pytest
 
 import l0llm_amd as l0
 from oracle import pyoracle as orc
-from tests.helpers import bf16_bits, dequant, rel_err, stored
+from tests.helpers import bf16_bits, dequant, elementwise_excess, rel_err, stored
 
 pytestmark = pytest.mark.gpu
 
@@ -339,7 +339,8 @@ def test_attention_decode_batched_fp16(device, suite, batch, seq):
     for b in range(batch):
         want = orc.attention_decode(q[b].astype(np.float32), kf[b].view(np.uint16), vf[b].view(np.uint16), l0.F16,
                                     hd, nh, nkv, seq, seq)
-        assert np.max(np.abs(out[b] - want)) <= 1e-2 * np.max(np.abs(want)), b
+        # fp16 output: relative error at most 1e-2 per element (floor 1e-4 of max|out| near zero)
+        assert elementwise_excess(out[b], want) <= 1.0, b
 
 
 # (head_dim, q heads, kv heads, pos0, tokens, max_seq, cache): query-tiled kernels for head_dim 64

@@ -39,8 +39,9 @@ def load_model(device, d, precision, cache, max_seq=64):
     return m
 
 
-def exported_oracle(m: l0.LlmModel, cfg: dict, cache: int, max_seq: int) -> orc.Model:
-    """Oracle over the weights exactly as the device stores them (read back through the ABI)."""
+def exported_oracle(m: l0.LlmModel, cfg: dict, cache: int, max_seq: int, copies: int = 1):
+    """Oracle over the weights exactly as the device stores them (read back through the ABI); with
+    copies > 1, that many oracles (own caches) sharing one host copy of the weights."""
     H, L = cfg["hidden_size"], cfg["num_layers"]
     w = {"model.embed_tokens.weight": m.export_vector("model.embed_tokens.weight", cfg["vocab_size"] * H),
          "model.norm.weight": m.export_vector("model.norm.weight", H)}
@@ -57,6 +58,8 @@ def exported_oracle(m: l0.LlmModel, cfg: dict, cache: int, max_seq: int) -> orc.
                              ("v", cfg["num_key_value_heads"])):
                 w[p + f"self_attn.{n}_proj.bias"] = m.export_vector(p + f"self_attn.{n}_proj.bias", width * cfg["head_dim"])
     inv, att = rope_table_for(cfg)
+    if copies > 1:
+        return [orc.Model(cfg, w, inv, att, cache, max_seq) for _ in range(copies)]
     return orc.Model(cfg, w, inv, att, cache, max_seq)
 
 

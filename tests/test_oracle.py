@@ -23,6 +23,8 @@ reference's goldens come from) built from a config with seeded weights.
     embedding / argmax       known answers; numpy.argmax first-maximum rule
     model step               transformers Llama (llama3 RoPE) and Qwen2 (bias, tied) logits and
                              greedy continuations
+    device rounding          the step composed from the primitives above with numpy fp16 casts of
+                             the attention and SwiGLU outputs (bit for bit)
 """
 from __future__ import annotations
 
@@ -394,3 +396,77 @@ def test_fp32_baseline_gemv_matches_fp64_restatement(wdtype):
     # a wrong accumulation (one term dropped) would not pass
     bad = orc.gemv_nk_f32acc(dt, np.ascontiguousarray(ws[:, :-1]), x[:, :-1], s)
     assert np.max(np.abs(bad - want)) > 1e-5 * np.max(np.abs(want))
+
+
+@pytest.mark.parametrize("wide_layer", [None, 1])
+def test_device_rounding_rounds_attention_and_swiglu_outputs(wide_layer):
+    """orc_set_device_rounding: a decode step with it on equals the step composed from the oracle's
+    separately pinned primitives with numpy fp16 casts of the attention output and of the SwiGLU
+    output (the latter only when every value is within fp16's range), bit for bit; off, the step
+    differs. wide_layer: that layer's gate / up weights scaled so its SwiGLU output exceeds 65504
+    (kept in fp32)."""
+    from tests.helpers import stored
+    rng = np.random.default_rng(4242)
+    H, I, L, nh, nkv, hd, V, max_seq = 64, 128, 2, 4, 2, 16, 50, 8
+    cfg = dict(vocab_size=V, hidden_size=H, intermediate_size=I, num_layers=L, num_attention_heads=nh,
+               num_key_value_heads=nkv, head_dim=hd, rms_norm_eps=1e-5)
+    shapes = {"self_attn.q_proj.weight": (nh * hd, H), "self_attn.k_proj.weight": (nkv * hd, H),
+              "self_attn.v_proj.weight": (nkv * hd, H), "self_attn.o_proj.weight": (H, nh * hd),
+              "mlp.gate_proj.weight": (I, H), "mlp.up_proj.weight": (I, H), "mlp.down_proj.weight": (H, I)}
+    w = {"model.embed_tokens.weight": rng.normal(0, 1, V * H).astype(np.float32),
+         "model.norm.weight": rng.normal(1, 0.1, H).astype(np.float32),
+         "lm_head.weight": stored(orc.I8PC, rng.normal(0, 0.05, (V, H)))}
+    for i in range(L):
+        p = f"model.layers.{i}."
+        for n, shp in shapes.items():
+            scale = 30.0 if (i == wide_layer and n.startswith("mlp.") and "down" not in n) else 0.1
+            w[p + n] = stored(orc.I8PC, rng.normal(0, scale, shp))
+        w[p + "input_layernorm.weight"] = rng.normal(1, 0.1, H).astype(np.float32)
+        w[p + "post_attention_layernorm.weight"] = rng.normal(1, 0.1, H).astype(np.float32)
+    inv, att = orc.rope_frequencies(hd, 10000.0, 4096)
+    model = orc.Model(cfg, w, inv, att, orc.F16, max_seq)
+    plain = orc.Model(cfg, w, inv, att, orc.F16, max_seq)
+    kvd = nkv * hd
+    kc = [np.zeros(max_seq * kvd * 2, np.uint8) for _ in range(L)]
+    vc = [np.zeros(max_seq * kvd * 2, np.uint8) for _ in range(L)]
+
+    def proj(name, x):
+        dt, ws, s = w[name]
+        return orc.gemv_nk(dt, ws, x, s)[0]
+
+    def composed(tok, pos):
+        hidden = orc.embedding([tok], w["model.embed_tokens.weight"], H, H)
+        wide_seen = False
+        for i in range(L):
+            p = f"model.layers.{i}."
+            _, normed = orc.rmsnorm(hidden, w[p + "input_layernorm.weight"], 1e-5)
+            q = proj(p + "self_attn.q_proj.weight", normed)
+            k = proj(p + "self_attn.k_proj.weight", normed)
+            v = proj(p + "self_attn.v_proj.weight", normed)
+            q, k = orc.rope_table(q, k, [pos], inv, hd, nh, nkv, att)
+            orc.kv_store(k, v, kc[i], vc[i], orc.F16, pos, kvd, 1)
+            a = orc.attention_decode(q, kc[i], vc[i], orc.F16, hd, nh, nkv, pos + 1, max_seq)
+            a = a.astype(np.float16).astype(np.float32)
+            hidden, normed = orc.rmsnorm(hidden, w[p + "post_attention_layernorm.weight"], 1e-5,
+                                         residual=proj(p + "self_attn.o_proj.weight", a))
+            act = orc.swiglu(proj(p + "mlp.gate_proj.weight", normed), proj(p + "mlp.up_proj.weight", normed))
+            if np.all(np.abs(act) <= 65504.0):
+                act = act.astype(np.float16).astype(np.float32)
+            else:
+                wide_seen = True
+            hidden = orc.add(hidden, proj(p + "mlp.down_proj.weight", act))
+        _, normed = orc.rmsnorm(hidden, w["model.norm.weight"], 1e-5)
+        return proj("lm_head.weight", normed), wide_seen
+
+    try:
+        for pos, tok in enumerate([3, 17, 41, 9]):
+            orc.set_device_rounding(True)
+            _, got = model.step(tok, pos)
+            orc.set_device_rounding(False)
+            _, ref = plain.step(tok, pos)
+            want, wide_seen = composed(tok, pos)
+            np.testing.assert_array_equal(got, want)
+            assert not np.array_equal(got, ref)  # the rounding is not a no-op
+            assert wide_seen == (wide_layer is not None)
+    finally:
+        orc.set_device_rounding(False)
