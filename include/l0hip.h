@@ -418,6 +418,10 @@ int l0h_model_projection_bytes(l0h_model* model, long long* bytes);
 #define L0H_STEP_EAGER 1
 #define L0H_STEP_PERSISTENT 2
 int l0h_model_step_path(l0h_model* model, int* path);
+/* Kernel launches in one decode step: the nodes of the step's HIP graph (captured if it was not
+ * yet), the same kernels an eager step enqueues. No reference counterpart (the reference counts no
+ * launches; LlmDecoderLayer.cs:164-195, :291-334 enqueue about 21 operators per layer). */
+int l0h_model_step_launches(l0h_model* model, int* launches);
 /* LlmModel.Position (LlmModel.cs:219). */
 int l0h_model_position(l0h_model* model, int* position);
 /* LlmModel.ResetSequence (LlmModel.cs:221). */

@@ -591,6 +591,13 @@ class LlmModel:
         return Buffer(self.device, 4 * vocab, ptr=p.value, owned=False).read(np.float32, vocab)
 
     @property
+    def step_launches(self) -> int:
+        """Kernel launches in one decode step (the nodes of the step's HIP graph)."""
+        n = ctypes.c_int()
+        check(lib.l0h_model_step_launches(self.handle, ctypes.byref(n)))
+        return n.value
+
+    @property
     def step_path(self) -> str:
         """'graph', 'eager' or 'persistent': how a decode step runs."""
         v = ctypes.c_int()

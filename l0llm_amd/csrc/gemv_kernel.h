@@ -123,6 +123,35 @@ __device__ __forceinline__ void chunk_fma(const uint4& w, const float* x, float&
     }
 }
 
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+// acc += dot(int8 chunk, x) with x staged as fp16 (XH): each weight byte becomes an exact fp16
+// integer (byte ^ 0x80 placed under the exponent of 1024 by v_perm_b32 is 1152 + q; a packed fp16
+// add of -1152 leaves q) and v_dot2_f32_f16 multiplies pairs into the fp32 accumulator (products of
+// two fp16 values are exact in fp32). xa / xb: the chunk's 16 activations, 8 per 16 bytes, each 4
+// stored as (x0, x2), (x1, x3): the order of the weight bytes that one v_perm_b32 pairs up.
+__device__ __forceinline__ float chunk_dot_h(const uint4& w, const uint4& xa, const uint4& xb, float acc) {
+    const uint32_t d[4] = {w.x, w.y, w.z, w.w};
+    const uint32_t xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+    const half2_t bias = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const uint32_t u = d[j] ^ 0x80808080u;
+        const half2_t lo = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, u, 0x04020400u)) + bias;
+        const half2_t hi = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, u, 0x04030401u)) + bias;
+        acc = __builtin_amdgcn_fdot2(lo, __builtin_bit_cast(half2_t, xv[2 * j]), acc, false);
+        acc = __builtin_amdgcn_fdot2(hi, __builtin_bit_cast(half2_t, xv[2 * j + 1]), acc, false);
+    }
+    return acc;
+}
+
+// 8 fp16 activations (x0 .. x7 in two-byte order) rearranged for chunk_dot_h: (x0, x2), (x1, x3),
+// (x4, x6), (x5, x7).
+__device__ __forceinline__ uint4 pair_halves(const uint4& c) {
+    return make_uint4(__builtin_amdgcn_perm(c.y, c.x, 0x05040100u), __builtin_amdgcn_perm(c.y, c.x, 0x07060302u),
+                      __builtin_amdgcn_perm(c.w, c.z, 0x05040100u), __builtin_amdgcn_perm(c.w, c.z, 0x07060302u));
+}
+
 // The 16 bytes of an activation chunk as fp32 (4 fp32 values or 8 fp16 / bf16 values).
 __device__ __forceinline__ int chunk_to_float(const uint4& c, int dt, float* f) {
     const uint32_t d[4] = {c.x, c.y, c.z, c.w};
@@ -256,10 +285,16 @@ __device__ __forceinline__ float lane_group_sum(float v) {
     return v;
 }
 
-template <int WT, int R, int U, int MR, int KX, bool NORM, int EPI>
+// XH (int8 weights, one fp16 activation row, no RMSNorm, store / residual epilogue): the row is
+// staged as fp16 in two planes of k_pad / 16 slots of 16 bytes, the first 8 and the last 8
+// activations of every weight chunk (pair_halves order), and chunks are computed by chunk_dot_h;
+// there are no bias terms.
+template <int WT, int R, int U, int MR, int KX, bool NORM, int EPI, bool XH = false>
 __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p, int k_pad) {
+    static_assert(!XH || (WT == L0H_I8PC && MR == 1 && !NORM && EPI == EPI_STORE), "fp16-row int8 GEMV");
     extern __shared__ float4 smem4[];
     float* xs = reinterpret_cast<float*>(smem4);  // [MR, k_pad], zero past K
+    uint4* xh = reinterpret_cast<uint4*>(smem4);  // XH: [2, k_pad / 16] slots, zero past K
     // int8: [MR, k_pad / 16] bias terms, -128 * (sum of the 16 activations of each weight chunk)
     float* xc = xs + (size_t)MR * k_pad;
     const int kc_pad = k_pad / 16;
@@ -361,7 +396,14 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p, int
             ss = wave_sum(ss);
             if (lane == 0) red[wave] = ss;
         }
-        if (wide) {
+        if constexpr (XH) {
+            // chunk idx of x is 8 fp16 activations: half idx & 1 of weight chunk idx >> 1
+#pragma unroll
+            for (int i = 0; i < KX; i++) {
+                const int idx = i * kBlock + tid;
+                if (idx < nxc) xh[(idx & 1) * kc_pad + (idx >> 1)] = pair_halves(xr[i]);
+            }
+        } else if (wide) {
             // the fp32 twin, in groups of 16 values (K % 16 == 0 where a twin is given)
             const float4* xw = reinterpret_cast<const float4*>(p.x_wide);
             for (int g16 = tid; g16 < K / 16; g16 += kBlock) {
@@ -409,9 +451,16 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p, int
                 }
             }
         }
-        for (int i = K + tid; i < k_pad; i += kBlock) xs[i] = 0.f;
-        if constexpr (WT == L0H_I8PC)
-            for (int c = K / 16 + tid; c < kc_pad; c += kBlock) xc[c] = 0.f;
+        if constexpr (XH) {
+            for (int c = K / 16 + tid; c < kc_pad; c += kBlock) {
+                xh[c] = make_uint4(0u, 0u, 0u, 0u);
+                xh[kc_pad + c] = make_uint4(0u, 0u, 0u, 0u);
+            }
+        } else {
+            for (int i = K + tid; i < k_pad; i += kBlock) xs[i] = 0.f;
+            if constexpr (WT == L0H_I8PC)
+                for (int c = K / 16 + tid; c < kc_pad; c += kBlock) xc[c] = 0.f;
+        }
     }
     if constexpr (EPI == EPI_QKV) {
         // cos/sin of this position for every rotated pair, once per block (accurate sincos of
@@ -439,6 +488,16 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p, int
         for (int r = 0; r < R; r++) acc[mr][r] = 0.f;
 
     auto compute = [&](const uint4 (&w)[U][R], int batch) {
+        if constexpr (XH) {
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int c = batch * KB + u * 64 + lane;  // < nb * KB: x is zero past K
+                const uint4 xa = xh[c], xb = xh[kc_pad + c];
+#pragma unroll
+                for (int r = 0; r < R; r++) acc[0][r] = chunk_dot_h(w[u][r], xa, xb, acc[0][r]);
+            }
+            return;
+        }
 #pragma unroll
         for (int u = 0; u < U; u++) {
             const int c = batch * KB + u * 64 + lane;  // < nb * KB: x is zero past K
@@ -603,12 +662,12 @@ size_t tile_bytes(int mr, int k_pad) {
     return (size_t)mr * per_row * sizeof(float);
 }
 
-template <int WT, int R, int U, int MR, int KX, bool NORM, int EPI>
+template <int WT, int R, int U, int MR, int KX, bool NORM, int EPI, bool XH = false>
 int launch_fast(hipStream_t s, const GemvParams& p) {
     const int k_pad = padded_k<WT, U>(p.k);
-    const size_t shmem = tile_bytes<WT>(MR, k_pad);
+    const size_t shmem = XH ? (size_t)k_pad * 2 : tile_bytes<WT>(MR, k_pad);
     if (shmem > kLdsBudget) return fail(L0H_ERR_UNSUPPORTED, "GEMV activation tile exceeds LDS");
-    auto kern = gemv_nk_kernel<WT, R, U, MR, KX, NORM, EPI>;
+    auto kern = gemv_nk_kernel<WT, R, U, MR, KX, NORM, EPI, XH>;
     // The dynamic tile may reach kLdsBudget on top of the static LDS: raise the limit once.
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsBudget);
@@ -638,8 +697,26 @@ int launch_fast(hipStream_t s, const GemvParams& p) {
 }
 
 // One activation row: the fused epilogues and the RMSNorm prologue live here.
+// L0H_GEMV_XH=0 keeps fp16 activation rows of int8 GEMVs on the fp32 staging (A/B measurements).
+inline bool xh_enabled() {
+    static const bool on = [] {
+        const char* e = std::getenv("L0H_GEMV_XH");
+        return !e || std::atoi(e) != 0;
+    }();
+    return on;
+}
+
+// int8 weights against one fp16 activation row without a fused prologue or an fp32 twin: the fp16
+// staging and v_dot2 compute (XH).
+inline bool use_xh(const GemvParams& p) {
+    return p.w_dtype == L0H_I8PC && p.m == 1 && p.x_dtype == L0H_F16 && !p.norm_w && !p.x_wide &&
+           (p.epilogue == EPI_STORE || p.epilogue == EPI_RESIDUAL) && xh_enabled();
+}
+
 template <int WT, int R, int U, int KX>
 int dispatch_one(hipStream_t s, const GemvParams& p) {
+    if constexpr (WT == L0H_I8PC)
+        if (use_xh(p)) return launch_fast<WT, R, U, 1, KX, false, EPI_STORE, true>(s, p);
     switch (p.epilogue) {
     case EPI_SWIGLU: return launch_fast<WT, R, U, 1, KX, true, EPI_SWIGLU>(s, p);
     case EPI_QKV: return launch_fast<WT, R, U, 1, KX, true, EPI_QKV>(s, p);
@@ -701,6 +778,16 @@ int dispatch_wt(hipStream_t s, const GemvParams& p, int mr) {
     if (mr == 1 && C > 128 && p.epilogue == EPI_STORE && !p.norm_w) {
         const long waves = (long)(p.max_blocks > 0 ? p.max_blocks : 512) * kWaves;
         if (ceil_div(p.n, 2) < waves) {
+            if constexpr (WT == L0H_I8PC)
+                if (use_xh(p)) {
+                    switch (staged_chunks(p)) {
+                    case 1: return launch_fast<WT, 1, 4, 1, 1, false, EPI_STORE, true>(s, p);
+                    case 2: return launch_fast<WT, 1, 4, 1, 2, false, EPI_STORE, true>(s, p);
+                    case 4: return launch_fast<WT, 1, 4, 1, 4, false, EPI_STORE, true>(s, p);
+                    case 8: return launch_fast<WT, 1, 4, 1, 8, false, EPI_STORE, true>(s, p);
+                    default: return fail(L0H_ERR_UNSUPPORTED, "GEMV activation row exceeds the LDS tile");
+                    }
+                }
             switch (staged_chunks(p)) {
             case 1: return launch_fast<WT, 1, 4, 1, 1, false, EPI_STORE>(s, p);
             case 2: return launch_fast<WT, 1, 4, 1, 2, false, EPI_STORE>(s, p);

@@ -188,6 +188,7 @@ struct l0h_model {
     int* pf_ids = nullptr;
     size_t pf_ws_bytes = 0;
     hipGraphExec_t step_exec = nullptr;
+    int step_nodes = 0;  // kernel nodes of the captured step
     bool eager = false;  // L0H_EAGER_STEP=1: enqueue the step's kernels instead of replaying the graph
     // Persistent decode step (step_kernel.hip): the whole step in one launch, for int8 models with an
     // fp16 cache where the kernel's shape limits allow it.
@@ -719,6 +720,8 @@ int ensure_graph(l0h_model* m) {
         return st;
     }
     if (e != hipSuccess) return fail(L0H_ERR_DEVICE, std::string("capture: ") + hipGetErrorString(e));
+    size_t nodes = 0;
+    if (hipGraphGetNodes(g, nullptr, &nodes) == hipSuccess) m->step_nodes = (int)nodes;
     e = hipGraphInstantiate(&m->step_exec, g, nullptr, nullptr, 0);
     (void)hipGraphDestroy(g);
     if (e != hipSuccess) {
@@ -1306,6 +1309,15 @@ int l0h_model_projection_bytes(l0h_model* m, long long* bytes) {
 int l0h_model_step_path(l0h_model* m, int* path) {
     L0H_CHECK_ARG(m && path, "null argument");
     *path = m->persistent ? L0H_STEP_PERSISTENT : (m->eager ? L0H_STEP_EAGER : L0H_STEP_GRAPH);
+    return L0H_OK;
+}
+
+int l0h_model_step_launches(l0h_model* m, int* launches) {
+    L0H_CHECK_ARG(m && launches, "null argument");
+    int st = check_ready(m);
+    if (st) return st;
+    if ((st = ensure_graph(m))) return st;
+    *launches = m->step_nodes;
     return L0H_OK;
 }
 

@@ -145,3 +145,4 @@ def test_greedy_generation_is_deterministic_across_runs(device):
         np.testing.assert_array_equal(runs[0][2], runs[1][2])
         # the same ids through LlmModel.GenerateGreedy (the prompt's last token picks the first one)
         assert m.generate_greedy(prompt, 17) == [runs[0][0]] + runs[0][1].tolist()
+
