@@ -299,7 +299,66 @@ def greedy_ids_check(model, om, cfg, ctx: int, first: int, ids, count: int) -> d
                 oracle="fp64 C restatement, caches seeded with the device's prefill rows, teacher-forced")
 
 
-def cpu_baseline(model, cfg, tokens: int, position: int, ids_check=None) -> dict:
+def export_weights(model, cfg) -> dict:
+    """The model's weights as the device holds them, in HuggingFace names and order: projections as
+    (storage, int8 [N, K], fp16 scales), vectors as fp32 (read back through the ABI)."""
+    H = cfg.hidden_size
+    w = {"model.embed_tokens.weight": model.export_vector("model.embed_tokens.weight", cfg.vocab_size * H),
+         "model.norm.weight": model.export_vector("model.norm.weight", H),
+         "lm_head.weight": model.export_matrix("lm_head.weight")}
+    for i in range(cfg.num_layers):
+        p = f"model.layers.{i}."
+        for n in PROJECTIONS:
+            w[p + n] = model.export_matrix(p + n)
+        for n in ("input_layernorm.weight", "post_attention_layernorm.weight"):
+            w[p + n] = model.export_vector(p + n, H)
+    return w
+
+
+def dropin_path(dev, model, cfg, w: dict, ctx: int, first: int, next_id: int, reps: int = 20, tokens: int = 5) -> dict:
+    """The reference's own decode step on this library's operator entry points (the drop-in path:
+    an unchanged LlmModel.Step over LlmDecoderLayer.Forward / MixFull, l0llm_amd.reference_step),
+    with the same weights (separate q, k, v, gate and up matrices in the int8 weight-only format),
+    a copy of the model's prefilled caches and fp32 activations between operators. Timed as one
+    recorded token replayed back to back (replay), recorded afresh per token as Step does
+    (record_per_token, host clock, the sampled id read back each token), and issued without
+    recording (eager, host clock); checked against the model's greedy id at position ctx."""
+    from l0llm_amd.reference_step import ReferenceStep
+
+    ref = ReferenceStep(dev, cfg, w, model.max_seq_len, [model.kv_cache(i) for i in range(cfg.num_layers)])
+    try:
+        ref.set_token(first, ctx)
+        ref.record_step(ctx)  # runs it once
+        launches = dev.recording_launches
+        picked, dl = ref.read_sampled(), ref.read_logits()
+        replay_ms = dev.replay_recording(reps)
+        t0 = time.perf_counter()
+        for i in range(tokens):
+            ref.set_token(first, ctx + i)
+            ref.record_step(ctx + i)
+            ref.read_sampled()
+        rec_s = (time.perf_counter() - t0) / tokens
+        t0 = time.perf_counter()
+        for i in range(tokens):
+            ref.set_token(first, ctx + i)
+            ref.step(ctx + i)
+            ref.read_sampled()
+        eager_s = (time.perf_counter() - t0) / tokens
+    finally:
+        ref.close()
+    ml = model.compute_logits(first, ctx)  # the model's own step at the same position and token
+    rel = float(np.max(np.abs(dl - ml)) / np.max(np.abs(ml)))
+    return dict(
+        launches_per_step=launches, operators_per_step=18 * cfg.num_layers + 5,
+        replay=dict(ms_per_token=round(replay_ms, 4), tokens_per_s=round(1000.0 / replay_ms, 1), reps=reps),
+        record_per_token=dict(ms_per_token=round(rec_s * 1e3, 3), tokens_per_s=round(1.0 / rec_s, 1), tokens=tokens),
+        eager=dict(ms_per_token=round(eager_s * 1e3, 3), tokens_per_s=round(1.0 / eager_s, 1), tokens=tokens),
+        greedy_id=picked, greedy_id_match=picked == next_id, logits_rel_to_model=round(rel, 6),
+        path="reference operator sequence (LlmDecoderLayer.Forward / MixFull, LlmModel.Step) on l0h_*_execute entry "
+             "points: int8 weight-only GemvQ8 with fp32 activations, fp16 KV cache, split-K attention")
+
+
+def cpu_baseline(model, cfg, tokens: int, position: int, ids_check=None, w: dict | None = None) -> dict:
     """The CPU restatements timed on this host's cores: the fp64 check loop (the reference's own CPU
     matmul semantics, LlmMatrixTests.cs:71-80) and an fp32-accumulating, vectorised, OpenMP form of the
     same operations; all cores and one core. The int8 GEMV 896 -> 4864 is the median of 21 runs per
@@ -324,15 +383,8 @@ def cpu_baseline(model, cfg, tokens: int, position: int, ids_check=None) -> dict
     orc.set_threads(all_cores)
 
     H = cfg.hidden_size
-    w = {"model.embed_tokens.weight": model.export_vector("model.embed_tokens.weight", cfg.vocab_size * H),
-         "model.norm.weight": model.export_vector("model.norm.weight", H),
-         "lm_head.weight": model.export_matrix("lm_head.weight")}
-    for i in range(cfg.num_layers):
-        p = f"model.layers.{i}."
-        for n in PROJECTIONS:
-            w[p + n] = model.export_matrix(p + n)
-        for n in ("input_layernorm.weight", "post_attention_layernorm.weight"):
-            w[p + n] = model.export_vector(p + n, H)
+    if w is None:
+        w = export_weights(model, cfg)
     inv, att = orc.rope_frequencies(cfg.head_dim, cfg.rope_theta, cfg.max_position_embeddings)
     c = dict(vocab_size=cfg.vocab_size, hidden_size=H, intermediate_size=cfg.intermediate_size,
              num_layers=cfg.num_layers, num_attention_heads=cfg.num_attention_heads,
@@ -389,6 +441,8 @@ def main() -> int:
                          "baseline and the greedy-id check)")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the per-configuration kernel measurements (GEMV, prefill GEMM, attention)")
+    ap.add_argument("--no-dropin", action="store_true",
+                    help="skip the reference operator sequence on the operator entry points (the drop-in path)")
     ap.add_argument("--eager-step", action="store_true",
                     help="enqueue the decode step's kernels one by one instead of replaying its HIP graph "
                          "(same kernels; for profilers that cannot trace graph launches)")
@@ -470,11 +524,19 @@ def main() -> int:
         log("timing the per-configuration kernels")
         configs = measure_configs(dev)
 
+    weights = export_weights(model, cfg) if (args.cpu_tokens > 0 or not args.no_dropin) else None
+    dropin = None
+    if not args.no_dropin:
+        log("drop-in path: the reference's operator sequence on the operator entry points")
+        dropin = dropin_path(dev, model, cfg, weights, args.ctx, first, int(toks[0]))
+        log(f"drop-in path: {dropin['replay']['tokens_per_s']} tokens/s replayed, {dropin['launches_per_step']} launches "
+            f"per token; greedy id match {dropin['greedy_id_match']}")
+
     cpu = None
     if args.cpu_tokens > 0:
-        log("CPU baseline: exporting the model and running the oracle")
+        log("CPU baseline: running the oracle")
         cpu = cpu_baseline(model, cfg, args.cpu_tokens, pos,
-                           ids_check=(args.ctx, first, toks, min(8, args.steps)))
+                           ids_check=(args.ctx, first, toks, min(8, args.steps)), w=weights)
         log(f"CPU baseline {cpu['value']} tokens/s on {cpu['cores']} threads; greedy ids {cpu['greedy_ids']}")
 
     line = {
@@ -509,6 +571,8 @@ def main() -> int:
         "configs": configs,
         "cpu_baseline": cpu,
         "greedy_ids_match": cpu["greedy_ids"]["match"] if cpu else None,
+        "dropin": dropin,
+        "step_launches": model.step_launches,
     }
     print(json.dumps(line), flush=True)
     model.dispose()

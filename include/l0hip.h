@@ -97,6 +97,9 @@ int l0h_abort_recording(l0h_device* dev);
  * without the recording). L0H_ERR_INVALID_OP when nothing has been recorded, or when memory the
  * recording may use was freed or moved since (l0h_free, workspace or scratch growth). */
 int l0h_replay_recording(l0h_device* dev, int count, float* ms_per_replay);
+/* Measurement aid, no counterpart in the reference: the kernel launches (graph nodes) of the last
+ * recording. */
+int l0h_recording_launches(l0h_device* dev, int* launches);
 /* ComputeDevice.IsRecording (LlmModel.cs:353, :417). */
 int l0h_is_recording(l0h_device* dev, int* out);
 /* Wait for every queued operation. */

@@ -132,6 +132,13 @@ class Device:
         return ms.value
 
     @property
+    def recording_launches(self) -> int:
+        """Kernel launches (graph nodes) of the last recording."""
+        n = ctypes.c_int()
+        check(lib.l0h_recording_launches(self.handle, ctypes.byref(n)))
+        return n.value
+
+    @property
     def is_recording(self) -> bool:
         v = ctypes.c_int()
         check(lib.l0h_is_recording(self.handle, ctypes.byref(v)))

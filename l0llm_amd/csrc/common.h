@@ -49,6 +49,7 @@ struct l0h_device {
     int compute_units = 0;
     bool recording = false;
     hipGraphExec_t cached_exec = nullptr;  // reused by l0h_end_recording via hipGraphExecUpdate
+    int recorded_nodes = 0;                 // kernel nodes of the last recording
     // Set when the kept graph was dropped because memory it may address was freed or moved
     // (l0h_free, workspace growth): l0h_replay_recording then refuses until a new recording.
     bool recording_dropped = false;

@@ -286,6 +286,8 @@ int l0h_end_recording(l0h_device* dev) {
     dev->recording = false;
     hipGraph_t graph = nullptr;
     L0H_HIP_TRY(hipStreamEndCapture(dev->stream, &graph));
+    size_t nodes = 0;
+    dev->recorded_nodes = hipGraphGetNodes(graph, nullptr, &nodes) == hipSuccess ? (int)nodes : 0;
     bool reused = false;
     if (dev->cached_exec) {
         hipGraphNode_t err_node = nullptr;
@@ -312,6 +314,12 @@ int l0h_end_recording(l0h_device* dev) {
     (void)hipGraphDestroy(graph);
     if (e != hipSuccess) return fail(L0H_ERR_DEVICE, std::string("hipGraphLaunch: ") + hipGetErrorString(e));
     L0H_HIP_TRY(hipStreamSynchronize(dev->stream));
+    return L0H_OK;
+}
+
+int l0h_recording_launches(l0h_device* dev, int* launches) {
+    L0H_CHECK_ARG(dev && launches, "null argument");
+    *launches = dev->recorded_nodes;
     return L0H_OK;
 }
 

@@ -25,8 +25,12 @@ def clang() -> str | None:
 def generate(out_dir: str) -> str:
     os.makedirs(out_dir, exist_ok=True)
     lines = open(os.path.join(CSRC, "gemv_kernel.h")).read().split("\n")
-    cut = next(i for i, l in enumerate(lines) if l.startswith("template <int WT, int R, int U, int MR, int KX, bool NORM, int EPI>"))
+    cut = next(i for i, l in enumerate(lines) if l.startswith("// XH (int8 weights, one fp16 activation row"))
     head = "\n".join(lines[:cut])
+    # the fp16-row helpers (v_perm_b32 / v_dot2 builtins) are not used by the step kernel
+    xh0 = head.index("typedef _Float16 half2_t")
+    xh1 = head.index("// The 16 bytes of an activation chunk as fp32")
+    head = head[:xh0] + head[xh1:]
     head = head.replace('asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");', "")
     head = head.replace('asm volatile("" ::: "memory");', "")
     head = head.replace('#include "dpp.h"', f'#include "{CSRC}/dpp.h"').replace('#include "kernels.h"', f'#include "{CSRC}/kernels.h"')

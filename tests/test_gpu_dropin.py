@@ -171,3 +171,55 @@ def test_attention_recorded_without_reserve_uses_the_workspace_it_has():
             suite.attention_execute(qb, kc, vc, ob, hd, nh, nkv, seq, max_seq, cache_dtype=l0.F16)
             dev.end_recording()
             assert rel_err(ob.read(np.float32), want) < 1e-4
+
+
+# ---- the reference's decode step, operator by operator (the drop-in path) -----------------------
+
+def test_reference_operator_sequence_matches_oracle_and_model(device):
+    """LlmModel.Step over LlmDecoderLayer.Forward / MixFull as an unchanged C# host would issue them
+    on this library (l0llm_amd.reference_step: 18 operators per layer, 5 per token, fp32 activations
+    between them), on the 2-layer Llama-3.1-8B-shaped int8 model after a 300-token prefill by the
+    model: recorded steps against the oracle seeded with the same cache rows (both keep fp32
+    activations: 1e-4 of max|logit|) and against the model's fused step (fp16 attention and SwiGLU
+    outputs between kernels: 2e-3), greedy ids equal unless the oracle's top-2 gap is within the
+    bound, and eager steps equal to the recorded ones bit for bit. The recording holds 19 kernels per
+    layer (the attention's split and merge) and the 5 of the head."""
+    import dataclasses
+
+    from l0llm_amd.reference_step import ReferenceStep
+    from tests.test_gpu_model import LLAMA8B, _as_cfg, exported_oracle, exported_weights
+
+    hf = dataclasses.replace(LLAMA8B, num_layers=2)
+    n, max_seq = 300, 340
+    prompt = np.random.default_rng(300).integers(0, hf.vocab_size, n).tolist()
+    with l0.LlmModel(device, hf, precision=l0.PRECISION_INT8, cache_dtype=l0.F16, max_seq_len=max_seq) as m:
+        m.init_random(301, 0.02)
+        first = int(np.argmax(m.prefill(prompt)))
+        w = exported_weights(m, _as_cfg(hf))
+        om = exported_oracle(m, _as_cfg(hf), orc.F16, max_seq)
+        kv_bytes = n * hf.num_key_value_heads * hf.head_dim * 2
+        for layer in range(hf.num_layers):  # the prompt's rows 0 .. n - 1, as the device holds them
+            kp, vp = m.kv_cache(layer)
+            om.load_cache(layer, l0.Buffer(device, kv_bytes, ptr=kp, owned=False).read(np.uint8),
+                          l0.Buffer(device, kv_bytes, ptr=vp, owned=False).read(np.uint8))
+        ref = ReferenceStep(device, hf, w, max_seq, [m.kv_cache(i) for i in range(hf.num_layers)])
+        try:
+            tok = first
+            for t in range(n, n + 4):
+                ref.set_token(tok, t)
+                ref.record_step(t)
+                if t == n:
+                    launches = device.recording_launches
+                got, picked = ref.read_logits(), ref.read_sampled()
+                ref.step(t)  # the same operators without a recording
+                np.testing.assert_array_equal(ref.read_logits(), got)
+                onext, olg = om.step(tok, t)
+                assert rel_err(got, olg) < 1e-4, (t, rel_err(got, olg))
+                assert rel_err(got, m.compute_logits(tok, t)) < 2e-3, t
+                assert picked == int(np.argmax(got))
+                if picked != onext:
+                    assert orc.top2_margin(olg) < 2e-4 * np.max(np.abs(olg)), (t, picked, onext)
+                tok = onext
+            assert launches >= 19 * hf.num_layers + 5, launches
+        finally:
+            ref.close()

@@ -39,9 +39,9 @@ def load_model(device, d, precision, cache, max_seq=64):
     return m
 
 
-def exported_oracle(m: l0.LlmModel, cfg: dict, cache: int, max_seq: int, copies: int = 1):
-    """Oracle over the weights exactly as the device stores them (read back through the ABI); with
-    copies > 1, that many oracles (own caches) sharing one host copy of the weights."""
+def exported_weights(m: l0.LlmModel, cfg: dict) -> dict:
+    """The weights exactly as the device stores them (read back through the ABI), HuggingFace names:
+    projections as (storage, stored array, fp16 scales or None), vectors as fp32."""
     H, L = cfg["hidden_size"], cfg["num_layers"]
     w = {"model.embed_tokens.weight": m.export_vector("model.embed_tokens.weight", cfg["vocab_size"] * H),
          "model.norm.weight": m.export_vector("model.norm.weight", H)}
@@ -57,6 +57,13 @@ def exported_oracle(m: l0.LlmModel, cfg: dict, cache: int, max_seq: int, copies:
             for n, width in (("q", cfg["num_attention_heads"]), ("k", cfg["num_key_value_heads"]),
                              ("v", cfg["num_key_value_heads"])):
                 w[p + f"self_attn.{n}_proj.bias"] = m.export_vector(p + f"self_attn.{n}_proj.bias", width * cfg["head_dim"])
+    return w
+
+
+def exported_oracle(m: l0.LlmModel, cfg: dict, cache: int, max_seq: int, copies: int = 1):
+    """Oracle over the weights exactly as the device stores them; with copies > 1, that many
+    oracles (own caches) sharing one host copy of the weights."""
+    w = exported_weights(m, cfg)
     inv, att = rope_table_for(cfg)
     if copies > 1:
         return [orc.Model(cfg, w, inv, att, cache, max_seq) for _ in range(copies)]
