@@ -110,7 +110,13 @@ __host__ __device__ constexpr int partial_stride(int G, int HD) { return G * HD 
 template <int NG>
 __device__ __forceinline__ void split_range(const AttnParams& p, int seq_len_step, int b, int split, int& lo, int& n,
                                             int& len) {
-    len = (p.seq_len_device ? *p.seq_len_device + p.seq_len_add : p.seq_len) + b * seq_len_step;
+    // The device-side length is read unconditionally (from q, then ignored, when the length is a
+    // launch argument; the empty asm consumes the value on both paths, so the compiler cannot sink
+    // the read into a branch): a branch here would split the kernel's argument loads into more rounds.
+    const bool on_device = p.seq_len_device != nullptr;
+    int dev_len = *(on_device ? p.seq_len_device : static_cast<const int*>(p.q));
+    asm volatile("" : "+s"(dev_len));
+    len = (on_device ? dev_len + p.seq_len_add : p.seq_len) + b * seq_len_step;
     len = max(0, min(len, p.max_seq_len));
     constexpr int kStep = NG * kUnroll;
     int chunk = (len + p.splits - 1) / p.splits;
@@ -434,7 +440,12 @@ __global__ __launch_bounds__(kBlock) void attn_merge_kernel(const AttnParams p) 
     const int h = cc * 4 / HD;
     const int gsize = p.nh / p.nkv;
     const int S = p.splits;
-    const float* all = p.partials + ((size_t)b * p.nkv + g) * S * PS;
+    // The empty asm makes the partials address live before the loop, so its argument load joins
+    // the kernel's first load round instead of a round of its own after the loop guard (the
+    // address-space cast keeps the loads global ones, which the asm would otherwise hide).
+    const float* allp = p.partials + ((size_t)b * p.nkv + g) * S * PS;
+    asm volatile("" : "+s"(allp));
+    const __attribute__((address_space(1))) float* all = (const __attribute__((address_space(1))) float*)allp;
     float M = -INFINITY, den = 0.f;
     float4 num = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int s0 = j; s0 < S; s0 += 8 * J) {
@@ -442,8 +453,10 @@ __global__ __launch_bounds__(kBlock) void attn_merge_kernel(const AttnParams p) 
         float4 v[8];
 #pragma unroll
         for (int u = 0; u < 8; u++) {
-            const float* ps = all + (size_t)min(s0 + u * J, S - 1) * PS;
-            v[u] = *reinterpret_cast<const float4*>(ps + cc * 4);
+            const __attribute__((address_space(1))) float* ps = all + (size_t)min(s0 + u * J, S - 1) * PS;
+            typedef float f32x4_t __attribute__((ext_vector_type(4)));
+            const f32x4_t t = *reinterpret_cast<const __attribute__((address_space(1))) f32x4_t*>(ps + cc * 4);
+            v[u] = make_float4(t.x, t.y, t.z, t.w);
             ms[u] = ps[G * HD + h];
             ls[u] = ps[G * HD + G + h];
         }

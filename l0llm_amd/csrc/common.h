@@ -86,14 +86,11 @@ void drop_recording(l0h_device* dev);
 
 // ---------------------------------------------------------------- dtypes --
 
+// Bytes per element of a dtype (0 for an unknown one). Selects, not a switch: kernels size their
+// rows with it before their first loads, where a branch would split the argument loads.
 __host__ __device__ inline int dtype_size(int dt) {
-    switch (dt) {
-    case L0H_F32: return 4;
-    case L0H_F16:
-    case L0H_BF16: return 2;
-    case L0H_I8PC: return 1;
-    default: return 0;
-    }
+    const int s = dt == L0H_F32 ? 4 : (dt == L0H_F16 || dt == L0H_BF16) ? 2 : dt == L0H_I8PC ? 1 : 0;
+    return s;
 }
 
 __host__ __device__ inline float bf16_bits_to_float(uint32_t bits16) {

@@ -343,8 +343,14 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p, int
     // ---- one activation row: prologue loads first (x, norm weights, RoPE frequencies) ----
     // A 16-bit row with an fp32 twin (p.x_wide) whose writer flagged a value beyond the 16-bit
     // range is staged from the twin instead; the flag is read alongside the row's loads, so the
-    // common case waits for nothing more.
-    const unsigned wide = (MR == 1 && p.x_wide) ? *p.range_flag : 0u;
+    // common case waits for nothing more. The read is unconditional (from x, masked to 0, when there
+    // is no twin): a branch here would split the kernel's argument loads into two dependent rounds.
+    unsigned wide = 0u;
+    if constexpr (MR == 1) {
+        const bool twin = p.x_wide != nullptr;
+        const unsigned* wf = twin ? p.range_flag : static_cast<const unsigned*>(p.x);
+        wide = *wf & (twin ? 0xffffffffu : 0u);
+    }
     uint4 xr[KX], nr[NORM ? KX : 1];
     const int xdt = p.x_dtype;
     const int nxc = (int)((size_t)K * dtype_size(xdt) / 16);  // 16-byte chunks of x
