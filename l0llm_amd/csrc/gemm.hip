@@ -474,8 +474,12 @@ constexpr size_t dma_tile_bytes(int bm, int bn) {
 // (A rows first), one 1 KiB load per group; every load is unconditional (rows past M / N and
 // stages past the end re-read valid addresses, never used), so the in-order counter's wait for
 // stage t is exact.
-template <int WT, int BM, int BN, int WGM, int WGN, int NS>
-__global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(WGM * WGN / 4, WGM * WGN / 4))) void gemm_dma_kernel(
+// KG > 1: KG groups of WGM x WGN waves, group g computing K substeps [g * 4 / KG, (g + 1) * 4 / KG)
+// of every stage for the whole tile, so a block that would leave one wave per SIMD keeps KG; the
+// groups' sums are added in group order in the LDS epilogue (deterministic).
+// SPB > 1: the block meets once per SPB stages (SPB stages of loads requested together).
+template <int WT, int BM, int BN, int WGM, int WGN, int NS, int KG = 1, int SPB = 1>
+__global__ __launch_bounds__(64 * WGM * WGN * KG) __attribute__((amdgpu_waves_per_eu(WGM * WGN * KG / 4, WGM * WGN * KG / 4))) void gemm_dma_kernel(
     int M, int N, int K, int k_per_split, const uint16_t* __restrict__ X, const void* __restrict__ Wv,
     const uint16_t* __restrict__ scales, void* Y, int y_dtype, int epi, float* partial, LaunchGate gate) {
     constexpr bool I8 = WT == L0H_I8PC;
@@ -486,14 +490,16 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
     constexpr int ROWB = I8 ? SK : SK * 2;     // bytes per LDS row of B
     constexpr int RPB = 1024 / ROWB;           // B rows per 1 KiB load (8, or 16 for int8)
     constexpr int STAGE = BM * ROWA + BN * ROWB;  // bytes per stage
-    constexpr int NW = WGM * WGN;              // waves
+    static_assert(KG == 1 || KG == 2 || KG == 4, "K groups");
+    constexpr int NW = WGM * WGN * KG;         // waves
     constexpr int NT = 64 * NW;                // threads
     constexpr int TM = BM / WGM, TN = BN / WGN;
     constexpr int FI = TM / 32, FJ = TN / 32;
     constexpr int GA = BM / 8, GB = BN / RPB;  // 1 KiB loads per stage of A and B
     constexpr int DA = GA / NW, D = (GA + GB) / NW;  // loads per wave per stage (A, all)
     static_assert(FI >= 1 && FJ >= 1 && DA >= 1 && DA * NW == GA && D * NW == GA + GB, "tile shape");
-    static_assert(NS >= 2 && (NS - 2) * D < 64, "ring depth");
+    static_assert(SPB == 1 || SPB == 2, "stages per barrier");
+    static_assert(NS >= 2 * SPB && (NS - 2 * SPB + SPB - 1) * D < 64, "ring depth");
     extern __shared__ uint4 gemm_dma_smem[];
     const char* lds = reinterpret_cast<const char*>(gemm_dma_smem);
     const uint32_t lds0 = (uint32_t)(uintptr_t)((__attribute__((address_space(3))) char*)gemm_dma_smem);
@@ -501,7 +507,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
     if (gate_closed(gate)) return;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave % WGM, wn = wave / WGM;
+    const int wq = wave % (WGM * WGN), kg = wave / (WGM * WGN);
+    const int wm = wq % WGM, wn = wq / WGM;
     // Block order as in gemm_nk_kernel: consecutive ids on one XCD, groups of row blocks first, so
     // the row blocks that read the same weight columns share an XCD's L2.
     const int gx = gridDim.x, gy = gridDim.y, gz = gridDim.z;
@@ -571,15 +578,17 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
         const char* sb = sa + BM * ROWA;
         uint4 a0[FI], b0[FJ], a1[FI], b1[FJ];
         uint2 rest[FJ];  // int8: the second half of the chunk read in the even substep
-        auto frags = [&](uint4 (&a)[FI], uint4 (&b)[FJ], int s) {
-            const int ac = I8 ? 4 * (s >> 1) + 2 * hi + (s & 1) : 2 * s + hi;
+        // s: the substep (group base + local), odd: its parity (the base is even)
+        auto frags = [&](uint4 (&a)[FI], uint4 (&b)[FJ], int s, auto oddc) {
+            constexpr bool odd = decltype(oddc)::value;
+            const int ac = I8 ? 4 * (s >> 1) + 2 * hi + (odd ? 1 : 0) : 2 * s + hi;
 #pragma unroll
             for (int i = 0; i < FI; i++)
                 a[i] = *reinterpret_cast<const uint4*>(sa + ar[i] * ROWA + ((ac ^ lds_swz(ar[i])) << 4));
 #pragma unroll
             for (int j = 0; j < FJ; j++) {
                 if constexpr (I8) {
-                    if ((s & 1) == 0) {
+                    if constexpr (!odd) {
                         const uint4 q = *reinterpret_cast<const uint4*>(sb + br[j] * ROWB + (((s + hi) ^ lds_swz8(br[j])) << 4));
                         b[j] = i8x8_to_f16_ordered(q.x, q.y);
                         rest[j] = make_uint2(q.z, q.w);
@@ -597,14 +606,16 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
                 for (int j = 0; j < FJ; j++) acc[i][j] = mfma<DT, 32>(a[i], b[j], acc[i][j]);
         };
-        frags(a0, b0, 0);
-        for_each_index<SK / 16>([&](auto sc) {
+        constexpr int SG = SK / 16 / KG;  // substeps of a group
+        const int s0 = kg * SG;
+        frags(a0, b0, s0, std::false_type{});
+        for_each_index<SG>([&](auto sc) {
             constexpr int s = decltype(sc)::value;
             if constexpr (s % 2 == 0) {
-                if constexpr (s + 1 < SK / 16) frags(a1, b1, s + 1);
+                if constexpr (s + 1 < SG) frags(a1, b1, s0 + s + 1, std::true_type{});
                 mma(a0, b0);
             } else {
-                if constexpr (s + 1 < SK / 16) frags(a0, b0, s + 1);
+                if constexpr (s + 1 < SG) frags(a0, b0, s0 + s + 1, std::false_type{});
                 mma(a1, b1);
             }
             __builtin_amdgcn_sched_barrier(0);
@@ -613,15 +624,20 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
 
     if (nsteps > 0) {
 #pragma unroll
-        for (int t = 0; t < NS - 1; t++) issue(t, t);
-        int cur = 0, nxt = NS - 1;  // buffer of stage t, buffer stage t + NS - 1 goes to
-        for (int t = 0; t < nsteps; t++) {
-            wait_vmcnt<(NS - 2) * D>();  // this wave's loads of stage t have landed in LDS
-            lds_barrier();               // everyone's have; everyone is done with stage t - 1
-            issue(t + NS - 1, nxt);
+        for (int t = 0; t < NS - SPB; t++) issue(t, t);
+        int cur = 0;  // buffer of stage t
+        for (int t = 0; t < nsteps; t += SPB) {
+            wait_vmcnt<(NS - 2 * SPB) * D>();  // this wave's loads of stages t .. t + SPB - 1 have landed
+            lds_barrier();  // everyone's have; everyone is done with stages t - SPB .. t - 1
+#pragma unroll
+            for (int j = 0; j < SPB; j++) {  // stage t + NS - SPB + j into the buffer of stage t - SPB + j
+                const int tn = t + NS - SPB + j;
+                issue(tn, tn % NS);
+            }
             compute(cur);
-            nxt = cur;
-            cur = cur + 1 == NS ? 0 : cur + 1;
+            if constexpr (SPB == 2)
+                if (t + 1 < nsteps) compute(cur + 1 == NS ? 0 : cur + 1);
+            cur = (cur + SPB) % NS;
         }
         wait_vmcnt<0>();  // the clamped tail loads: none may still write LDS when the block exits
     }
@@ -640,18 +656,24 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
     for (int pass = 0; pass < EP; pass++) {
         lds_barrier();  // the stages (first pass) or the previous pass's rows are no longer read
-        if (wm * TM / BMP == pass) {
 #pragma unroll
-            for (int j = 0; j < FJ; j++) {
-                const int c = wn * TN + j * 32 + lane % 32;
-                // int8: the weight row's scale (output column c)
-                const float sc = I8 ? __half2float(__ushort_as_half(scales[min(n0 + c, N - 1)])) : 1.f;
+        for (int g = 0; g < KG; g++) {  // group 0 writes its sums, the others add theirs in order
+            if (g > 0) lds_barrier();
+            if (kg == g && wm * TM / BMP == pass) {
 #pragma unroll
-                for (int i = 0; i < FI; i++)
+                for (int j = 0; j < FJ; j++) {
+                    const int c = wn * TN + j * 32 + lane % 32;
+                    // int8: the weight row's scale (output column c)
+                    const float sc = I8 ? __half2float(__ushort_as_half(scales[min(n0 + c, N - 1)])) : 1.f;
 #pragma unroll
-                    for (int r = 0; r < 16; r++)
-                        tile[(wm * TM - pass * BMP + i * 32 + (r / 4) * 8 + (lane / 32) * 4 + (r % 4)) * LDT + c] =
-                            I8 ? acc[i][j][r] * sc : acc[i][j][r];
+                    for (int i = 0; i < FI; i++)
+#pragma unroll
+                        for (int r = 0; r < 16; r++) {
+                            float& t = tile[(wm * TM - pass * BMP + i * 32 + (r / 4) * 8 + (lane / 32) * 4 + (r % 4)) * LDT + c];
+                            const float v = I8 ? acc[i][j][r] * sc : acc[i][j][r];
+                            t = g == 0 ? v : t + v;
+                        }
+                }
             }
         }
         lds_barrier();
@@ -822,6 +844,8 @@ int launch_tiles(hipStream_t s, int m, int n, int k, const void* x, const void* 
 struct LdsPlan {
     int bm = 0, bn = 0, splits = 1;
     int waves = 0;  // 0: the tile's default wave grid
+    int kg = 1;     // K groups of waves per block
+    int spb = 1;    // ring stages per block barrier
 };
 
 bool lds_plan_for(int dtype, int m, int n, int k, int cus, LdsPlan& out) {
@@ -858,9 +882,13 @@ bool lds_plan_for(int dtype, int m, int n, int k, int cus, LdsPlan& out) {
     // 24.0 us against the register-staged kernel. Where it would need a K split, or on the other
     // Llama-3.2-1B shapes, it is slower (O 15.9 -> 19.6, down 37.8 -> 56.9 at M = 512).
     const bool narrow = dtype != L0H_I8PC && blocks(128, 64) >= want;
+    // The 128 x 64 blocks run two K groups of four waves (two waves per SIMD instead of one) and
+    // meet once per two stages of a six-stage ring: Llama-3.2-1B bf16 q|k|v at M = 512 19.7 -> 18.4
+    // us, gate|up at M = 128 24.3 -> 23.2 us (three interleaved runs each, cold weights).
+    const LdsPlan narrow_plan{128, 64, 1, 0, 2, 2};
     if (m < 256) {
         if (narrow && m > 64 && k >= 1024) {
-            out = LdsPlan{128, 64, 1};
+            out = narrow_plan;
             return true;
         }
         return false;
@@ -881,7 +909,7 @@ bool lds_plan_for(int dtype, int m, int n, int k, int cus, LdsPlan& out) {
             return true;
         }
     if (narrow) {
-        out = LdsPlan{128, 64, 1};
+        out = narrow_plan;
         return true;
     }
     for (int sp = 2; sp <= kMaxSplits && k / sp >= 8 * 64; sp *= 2)
@@ -896,19 +924,28 @@ bool lds_plan_for(int dtype, int m, int n, int k, int cus, LdsPlan& out) {
 }
 
 
-template <int WT, int BM, int BN, int WGM, int WGN>
+template <int WT, int BM, int BN, int WGM, int WGN, int KG = 1>
+int launch_lds_spb2(hipStream_t s, int m, int n, int k, const void* x, const void* w, const uint16_t* scales,
+                    void* y, int y_dtype, int epi, int splits, float* ws, const LaunchGate& gate, int ns_want);
+
+template <int WT, int BM, int BN, int WGM, int WGN, int KG = 1>
 int launch_lds(hipStream_t s, int m, int n, int k, const void* x, const void* w, const uint16_t* scales, void* y,
-               int y_dtype, int epi, int splits, float* ws, const LaunchGate& gate) {
-    constexpr int NT = 64 * WGM * WGN;
+               int y_dtype, int epi, int splits, float* ws, const LaunchGate& gate, int spb = 1) {
+    constexpr int NT = 64 * WGM * WGN * KG;
     constexpr size_t stage = (size_t)BM * 128 + (size_t)BN * (WT == L0H_I8PC ? 64 : 128);
     constexpr int kFit = (int)(160 * 1024 / stage);  // ring stages that fit the LDS
     static_assert(kFit >= 2, "two ring stages must fit");
     constexpr int kMaxNs = kFit >= 4 ? 4 : kFit;
     static const int ns_env = [] {
-        const char* e = std::getenv("L0H_GEMM_LDS_STAGES");  // tuning: LDS ring depth, 2 .. 4
-        return e ? std::atoi(e) : 3;
+        // tuning: LDS ring depth, 2 .. 4 (one stage per barrier; 4 or 6 with two, default 6)
+        const char* e = std::getenv("L0H_GEMM_LDS_STAGES");
+        return e ? std::atoi(e) : 0;
     }();
-    const int ns = std::max(2, std::min(ns_env, kMaxNs));
+    const int ns = std::max(2, std::min(ns_env > 0 ? ns_env : 3, kMaxNs));
+    if constexpr (kFit >= 4)
+        if (spb == 2)
+            return launch_lds_spb2<WT, BM, BN, WGM, WGN, KG>(s, m, n, k, x, w, scales, y, y_dtype, epi, splits, ws, gate,
+                                                              ns_env > 0 ? ns_env : 6);
     const int k_per_split = (k / 64 + splits - 1) / splits * 64;
     dim3 grid(ceil_div(m, BM), splits, ceil_div(n, BN));
     auto launch = [&](auto nsc) {
@@ -916,10 +953,10 @@ int launch_lds(hipStream_t s, int m, int n, int k, const void* x, const void* w,
         constexpr size_t bytes = std::max((size_t)NS * stage, dma_tile_bytes(BM, BN));
         static_assert(bytes <= 160 * 1024, "LDS budget");
         static const hipError_t attr =
-            hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_dma_kernel<WT, BM, BN, WGM, WGN, NS>),
+            hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_dma_kernel<WT, BM, BN, WGM, WGN, NS, KG>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
         if (attr != hipSuccess) return fail(L0H_ERR_DEVICE, std::string("hipFuncSetAttribute: ") + hipGetErrorString(attr));
-        gemm_dma_kernel<WT, BM, BN, WGM, WGN, NS><<<grid, NT, bytes, s>>>(
+        gemm_dma_kernel<WT, BM, BN, WGM, WGN, NS, KG><<<grid, NT, bytes, s>>>(
             m, n, k, k_per_split, static_cast<const uint16_t*>(x), w, scales, y, y_dtype, epi, splits > 1 ? ws : nullptr, gate);
         return L0H_OK;
     };
@@ -939,9 +976,50 @@ int launch_lds(hipStream_t s, int m, int n, int k, const void* x, const void* w,
     return launch_status("gemm splitk reduce");
 }
 
+template <int WT, int BM, int BN, int WGM, int WGN, int KG>
+int launch_lds_spb2(hipStream_t s, int m, int n, int k, const void* x, const void* w, const uint16_t* scales,
+                    void* y, int y_dtype, int epi, int splits, float* ws, const LaunchGate& gate, int ns_want) {
+    constexpr int NT = 64 * WGM * WGN * KG;
+    constexpr size_t stage = (size_t)BM * 128 + (size_t)BN * (WT == L0H_I8PC ? 64 : 128);
+    constexpr int kFit = (int)(160 * 1024 / stage);
+    const int k_per_split = (k / 64 + splits - 1) / splits * 64;
+    dim3 grid(ceil_div(m, BM), splits, ceil_div(n, BN));
+    auto launch = [&](auto nsc) {
+        constexpr int NS = decltype(nsc)::value;
+        constexpr size_t bytes = std::max((size_t)NS * stage, dma_tile_bytes(BM, BN));
+        static_assert(bytes <= 160 * 1024, "LDS budget");
+        auto kern = gemm_dma_kernel<WT, BM, BN, WGM, WGN, NS, KG, 2>;
+        static const hipError_t attr =
+            hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+        if (attr != hipSuccess) return fail(L0H_ERR_DEVICE, std::string("hipFuncSetAttribute: ") + hipGetErrorString(attr));
+        kern<<<grid, NT, bytes, s>>>(m, n, k, k_per_split, static_cast<const uint16_t*>(x), w, scales, y, y_dtype, epi,
+                                     splits > 1 ? ws : nullptr, gate);
+        return L0H_OK;
+    };
+    int st;
+    if constexpr (kFit >= 6)
+        st = ns_want >= 6 ? launch(std::integral_constant<int, 6>{}) : launch(std::integral_constant<int, 4>{});
+    else
+        st = launch(std::integral_constant<int, 4>{});
+    if (!st) st = launch_status("gemm_lds");
+    if (st || splits == 1) return st;
+    const size_t mn = (size_t)m * n;
+    const size_t threads = epi == EPI_SWIGLU ? mn / 2 : mn;
+    splitk_reduce_kernel<<<ceil_div(threads, 256), 256, 0, s>>>(ws, splits, mn, y, y_dtype, epi, gate);
+    return launch_status("gemm splitk reduce");
+}
+
 template <int WT>
 int launch_lds_plan(hipStream_t s, const LdsPlan& p, int m, int n, int k, const void* x, const void* w,
                     const uint16_t* scales, void* y, int y_dtype, int epi, float* ws, const LaunchGate& gate) {
+    if constexpr (WT != L0H_I8PC) {
+        if (p.kg == 2 && p.bm == 128 && p.bn == 64)
+            return launch_lds<WT, 128, 64, 2, 2, 2>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws, gate, p.spb);
+        if (p.kg == 2 && p.bm == 128 && p.bn == 128)
+            return launch_lds<WT, 128, 128, 2, 2, 2>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws, gate, p.spb);
+        if (p.kg == 2 && p.bm == 128 && p.bn == 256 && p.waves == 0)
+            return launch_lds<WT, 128, 256, 2, 4, 2>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws, gate, p.spb);
+    }
     if (p.bm == 256 && p.bn == 256)
         return launch_lds<WT, 256, 256, 2, 4>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws, gate);
     if (p.bm == 128 && p.bn == 256 && p.waves == 4)
@@ -949,7 +1027,7 @@ int launch_lds_plan(hipStream_t s, const LdsPlan& p, int m, int n, int k, const 
     if (p.bm == 128 && p.bn == 256)
         return launch_lds<WT, 128, 256, 2, 4>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws, gate);
     if (p.bm == 128 && p.bn == 64)
-        return launch_lds<WT, 128, 64, 2, 2>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws, gate);
+        return launch_lds<WT, 128, 64, 2, 2>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws, gate, p.spb);
     if (p.bm == 64 && p.bn == 128)
         return launch_lds<WT, 64, 128, 2, 2>(s, m, n, k, x, w, scales, y, y_dtype, epi, p.splits, ws, gate);
     if (p.bm == 64 && p.bn == 64)
@@ -1015,6 +1093,18 @@ int launch_gemm_nk(hipStream_t s, int dtype, int m, int n, int k, const void* x,
     LdsPlan lp;
     if (lds_plan_for(dtype, m, n, k, cus, lp)) {
         while (lp.splits > 1 && (size_t)lp.splits * m * n * sizeof(float) > ws_bytes) lp.splits /= 2;
+        // tuning: K groups per block (1 or 2, where the tile has a two-group form) and ring stages
+        // per barrier (1 or 2) for every shape the ring takes, over the plan's choice
+        static const int kg_env = [] {
+            const char* e = std::getenv("L0H_GEMM_LDS_KG");
+            return e ? std::atoi(e) : 0;
+        }();
+        static const int spb_env = [] {
+            const char* e = std::getenv("L0H_GEMM_LDS_SPB");
+            return e ? std::atoi(e) : 0;
+        }();
+        if (kg_env == 1 || kg_env == 2) lp.kg = kg_env;
+        if (spb_env == 1 || spb_env == 2) lp.spb = spb_env;
         switch (dtype) {
         case L0H_BF16: return launch_lds_plan<L0H_BF16>(s, lp, m, n, k, x, w, nullptr, y, y_dtype, epilogue, ws, gate);
         case L0H_F16: return launch_lds_plan<L0H_F16>(s, lp, m, n, k, x, w, nullptr, y, y_dtype, epilogue, ws, gate);

@@ -434,12 +434,15 @@ def test_recording_matches_eager_and_replays(device, suite):
 # (eight 128 x 64 wave tiles, the epilogue in two passes of 128 rows) with a ragged last row block
 # (1030 x 10240 x 256), and 256 x 128 blocks with a ragged last column block whose width (16102)
 # leaves rows that are not 16-byte aligned, so the epilogue stores element by element there
-# (300 x 16102 x 512); 128 x 64 blocks below 256 rows (100 x 16384 x 1024, ragged rows) and from
-# 256 rows with a ragged last column block (512 x 3080 x 1024).
+# (300 x 16102 x 512); 128 x 64 blocks (two K groups of four waves, two stages per barrier) below
+# 256 rows (100 x 16384 x 1024, ragged rows) and from 256 rows with a ragged last column block
+# (512 x 3080 x 1024), also with an odd stage count (512 x 3080 x 1088, 100 x 16384 x 1088: the last
+# barrier interval computes one stage).
 @pytest.mark.parametrize("m,n,k", [(64, 256, 512), (128, 3072, 2048), (512, 2048, 2048), (100, 200, 128),
                                    (128, 64, 8192), (33, 40, 70), (96, 300, 160), (512, 1024, 256),
                                    (1030, 10240, 256), (1030, 8192, 256), (300, 16384, 320), (300, 16102, 512),
-                                   (260, 640, 8192), (100, 16384, 1024), (512, 3080, 1024)])
+                                   (260, 640, 8192), (100, 16384, 1024), (512, 3080, 1024), (512, 3080, 1088),
+                                   (100, 16384, 1088)])
 @pytest.mark.parametrize("dtype", [l0.BF16, l0.F16])
 def test_gemm_nk_matches_oracle(device, suite, m, n, k, dtype):
     rng = np.random.default_rng(m + n + k)
