@@ -692,7 +692,12 @@ int launch_fast(hipStream_t s, const GemvParams& p) {
             occ_shmem = (int)shmem;
             occ_blocks = std::max(1, nb);
         }
-        const unsigned cap = std::min<unsigned>((unsigned)p.max_blocks, (unsigned)(occ_blocks * std::max(1, p.compute_units)));
+        // Rows of at most 64 chunks (int8 K <= 1024) take twice the blocks: their items are short
+        // and their small LDS tile leaves room. Measured (int8, K = 896, graph replay, cold
+        // weights, four blocks per CU against two): 896 -> 151936 28.5 -> 27.3 us, 896 -> 9728 4.23
+        // -> 3.84, 896 -> 4864 3.30 -> 3.23, 896 -> 1152 and 896 -> 896 unchanged.
+        const int per = MR == 1 && p.k / WTraits<WT>::kElems <= 64 ? 2 * p.max_blocks : p.max_blocks;
+        const unsigned cap = std::min<unsigned>((unsigned)per, (unsigned)(occ_blocks * std::max(1, p.compute_units)));
         grid = std::min(grid, cap);
     }
     if (p.argmax_keys && (size_t)grid * kWaves > (size_t)std::max(0, p.argmax_capacity))
