@@ -546,13 +546,16 @@ __global__ __launch_bounds__(64 * WGM * WGN * KG) __attribute__((amdgpu_waves_pe
     }
     const char* xa = reinterpret_cast<const char*>(X + kbeg);
     const char* wb = static_cast<const char*>(Wv) + (size_t)kbeg * WB;
-    auto issue = [&](int t, int buf) {
+    // Loads d0 .. d1 - 1 of this wave for stage t into ring buffer buf.
+    auto issue_part = [&](int t, int buf, auto d0c, auto d1c) {
+        constexpr int D0 = decltype(d0c)::value, D1 = decltype(d1c)::value;
         const int k0 = min(t, last) * SK;
         const uint32_t base = lds0 + (uint32_t)(buf * STAGE + wave * 1024);
 #pragma unroll
-        for (int d = 0; d < D; d++)
+        for (int d = D0; d < D1; d++)
             dma16(d < DA ? (const void*)(xa + 2 * k0) : (const void*)(wb + WB * k0), voff[d], base + d * NW * 1024);
     };
+    auto issue = [&](int t, int buf) { issue_part(t, buf, std::integral_constant<int, 0>{}, std::integral_constant<int, D>{}); };
 
     acc_t<32> acc[FI][FJ];
 #pragma unroll
@@ -573,7 +576,10 @@ __global__ __launch_bounds__(64 * WGM * WGN * KG) __attribute__((amdgpu_waves_pe
     // operands carry the same K values.
     // The fragments of substep s + 1 are read before substep s's MFMAs are issued (two sets); a
     // scheduling barrier per substep keeps the compiler from hoisting all four substeps' reads.
-    auto compute = [&](int buf) {
+    // it >= 0: the loads of stage it into ring buffer ib are issued a share per substep, between
+    // the fragment reads and the MFMAs (issued all at once, a stage's loads held every wave out of
+    // its MFMAs while they queued: 510 of 1939 cycles a stage on the 128 x 256 tile).
+    auto compute = [&](int buf, int it, int ib) {
         const char* sa = lds + buf * STAGE;
         const char* sb = sa + BM * ROWA;
         uint4 a0[FI], b0[FJ], a1[FI], b1[FJ];
@@ -611,11 +617,14 @@ __global__ __launch_bounds__(64 * WGM * WGN * KG) __attribute__((amdgpu_waves_pe
         frags(a0, b0, s0, std::false_type{});
         for_each_index<SG>([&](auto sc) {
             constexpr int s = decltype(sc)::value;
+            constexpr int d0 = s * D / SG, d1 = (s + 1) * D / SG;
             if constexpr (s % 2 == 0) {
                 if constexpr (s + 1 < SG) frags(a1, b1, s0 + s + 1, std::true_type{});
+                if (it >= 0) issue_part(it, ib, std::integral_constant<int, d0>{}, std::integral_constant<int, d1>{});
                 mma(a0, b0);
             } else {
                 if constexpr (s + 1 < SG) frags(a0, b0, s0 + s + 1, std::false_type{});
+                if (it >= 0) issue_part(it, ib, std::integral_constant<int, d0>{}, std::integral_constant<int, d1>{});
                 mma(a1, b1);
             }
             __builtin_amdgcn_sched_barrier(0);
@@ -629,14 +638,15 @@ __global__ __launch_bounds__(64 * WGM * WGN * KG) __attribute__((amdgpu_waves_pe
         for (int t = 0; t < nsteps; t += SPB) {
             wait_vmcnt<(NS - 2 * SPB) * D>();  // this wave's loads of stages t .. t + SPB - 1 have landed
             lds_barrier();  // everyone's have; everyone is done with stages t - SPB .. t - 1
-#pragma unroll
-            for (int j = 0; j < SPB; j++) {  // stage t + NS - SPB + j into the buffer of stage t - SPB + j
-                const int tn = t + NS - SPB + j;
-                issue(tn, tn % NS);
+            // stage t + NS - SPB + j goes into the buffer of stage t - SPB + j, during compute j
+            const int tn = t + NS - SPB;
+            compute(cur, tn, tn % NS);
+            if constexpr (SPB == 2) {
+                if (t + 1 < nsteps)
+                    compute(cur + 1 == NS ? 0 : cur + 1, tn + 1, (tn + 1) % NS);
+                else
+                    issue(tn + 1, (tn + 1) % NS);
             }
-            compute(cur);
-            if constexpr (SPB == 2)
-                if (t + 1 < nsteps) compute(cur + 1 == NS ? 0 : cur + 1);
             cur = (cur + SPB) % NS;
         }
         wait_vmcnt<0>();  // the clamped tail loads: none may still write LDS when the block exits
