@@ -288,10 +288,13 @@ __device__ __forceinline__ float lane_group_sum(float v) {
 // XH (int8 weights, one fp16 activation row, no RMSNorm, store / residual epilogue): the row is
 // staged as fp16 in two planes of k_pad / 16 slots of 16 bytes, the first 8 and the last 8
 // activations of every weight chunk (pair_halves order), and chunks are computed by chunk_dot_h;
-// there are no bias terms.
-template <int WT, int R, int U, int MR, int KX, bool NORM, int EPI, bool XH = false>
+// there are no bias terms. DX (with XH, for launches of one or two row groups a wave): no staging
+// and no block barrier; each lane reads the 32 bytes of x under each of its weight chunks with the
+// chunk (from L1 / L2: every wave reads the same row), and a clamped chunk past K adds 0.
+template <int WT, int R, int U, int MR, int KX, bool NORM, int EPI, bool XH = false, bool DX = false>
 __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p, int k_pad) {
     static_assert(!XH || (WT == L0H_I8PC && MR == 1 && !NORM && EPI == EPI_STORE), "fp16-row int8 GEMV");
+    static_assert(!DX || XH, "direct x reads: the fp16-row int8 GEMV");
     extern __shared__ float4 smem4[];
     float* xs = reinterpret_cast<float*>(smem4);  // [MR, k_pad], zero past K
     uint4* xh = reinterpret_cast<uint4*>(smem4);  // XH: [2, k_pad / 16] slots, zero past K
@@ -314,13 +317,23 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p, int
     const size_t row_bytes = (size_t)K * WTraits<WT>::kBytes;
     const float* any = static_cast<const float*>(p.x);
 
-    auto load_w = [&](uint4 (&w)[U][R], int group, int batch) {
+    // DX: xq[u] = the 16 fp16 activations of weight chunk batch * KB + u * 64 + lane (clamped)
+    auto load_w = [&](uint4 (&w)[U][R], uint4 (&xq)[DX ? U : 1][2], int group, int batch) {
         const int grp = min(group, ngroups - 1);
 #pragma unroll
         for (int r = 0; r < R; r++) {
             const uint4* rp = reinterpret_cast<const uint4*>(wbase + (size_t)min(grp * R + r, N - 1) * row_bytes);
 #pragma unroll
             for (int u = 0; u < U; u++) w[u][r] = ld_nt16(rp + min(batch * KB + u * 64 + lane, C - 1));
+        }
+        if constexpr (DX) {
+            const uint4* xp = static_cast<const uint4*>(p.x);
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int c = min(batch * KB + u * 64 + lane, C - 1);
+                xq[u][0] = xp[2 * c];
+                xq[u][1] = xp[2 * c + 1];
+            }
         }
     };
 
@@ -354,7 +367,7 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p, int
     uint4 xr[KX], nr[NORM ? KX : 1];
     const int xdt = p.x_dtype;
     const int nxc = (int)((size_t)K * dtype_size(xdt) / 16);  // 16-byte chunks of x
-    if constexpr (MR == 1) {
+    if constexpr (MR == 1 && !DX) {
         const uint4* xp = static_cast<const uint4*>(p.x);
 #pragma unroll
         for (int i = 0; i < KX; i++) xr[i] = xp[min(i * kBlock + tid, nxc - 1)];
@@ -374,12 +387,13 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p, int
     // ---- first weight item, issued once every wave of the block has issued its activation loads:
     // a CU's memory pipeline returns data in order, so the activations come back ahead of the
     // block's weight stream and are staged while the weights are in flight ----
-    __builtin_amdgcn_s_barrier();
+    if constexpr (!DX) __builtin_amdgcn_s_barrier();
     int g = blockIdx.x * kWaves + wave;
     uint4 wa[U][R], wb[U][R];
+    uint4 xqa[DX ? U : 1][2], xqb[DX ? U : 1][2];
     Side sa, sb;
     sa = load_side<WT, R, MR, EPI>(p, min(g, ngroups - 1), lane, any);
-    load_w(wa, g, 0);
+    load_w(wa, xqa, g, 0);
 
     // ---- stage the one activation row (and RMSNorm) in LDS ----
     // RMSNorm: x * w goes to LDS at once; the row's scale 1 / rms(x), one scalar, multiplies the
@@ -387,7 +401,7 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p, int
     // 4 values per chunk, matching the 4 norm weights) in `red`, and the barrier that publishes the
     // staged row publishes those too, so no block reduction waits before the stream starts.
     float norm_scale = 1.f;
-    if constexpr (MR == 1) {
+    if constexpr (MR == 1 && !DX) {
         if constexpr (NORM) {
             float ss = 0.f;
 #pragma unroll
@@ -478,7 +492,7 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p, int
             rope_sn[tid] = sn * p.rope_scale;
         }
     }
-    lds_barrier();
+    if constexpr (!DX) lds_barrier();
     if constexpr (NORM && MR == 1) {  // the waves' sums of squares in a fixed order
         float t = 0.f;
 #pragma unroll
@@ -493,7 +507,20 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p, int
 #pragma unroll
         for (int r = 0; r < R; r++) acc[mr][r] = 0.f;
 
-    auto compute = [&](const uint4 (&w)[U][R], int batch) {
+    auto compute = [&](const uint4 (&w)[U][R], const uint4 (&xq)[DX ? U : 1][2], int batch) {
+        if constexpr (DX) {
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const bool in = batch * KB + u * 64 + lane < C;
+                const uint4 xa = pair_halves(xq[u][0]), xb = pair_halves(xq[u][1]);
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    const float t = chunk_dot_h(w[u][r], xa, xb, 0.f);
+                    acc[0][r] += in ? t : 0.f;
+                }
+            }
+            return;
+        }
         if constexpr (XH) {
 #pragma unroll
             for (int u = 0; u < U; u++) {
@@ -611,7 +638,7 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p, int
         int i = 0;
         for (;;) {
             if (i + 1 == items) {
-                compute(wa, b);
+                compute(wa, xqa, b);
                 finish(g, sa);
                 break;
             }
@@ -619,15 +646,15 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p, int
                 int gn = g, bn = b;
                 advance(gn, bn);
                 sb = load_side<WT, R, MR, EPI>(p, gn, lane, any);
-                load_w(wb, gn, bn);
-                compute(wa, b);
+                load_w(wb, xqb, gn, bn);
+                compute(wa, xqa, b);
                 if (b == nb - 1) finish(g, sa);
                 g = gn;
                 b = bn;
                 i++;
             }
             if (i + 1 == items) {
-                compute(wb, b);
+                compute(wb, xqb, b);
                 finish(g, sb);
                 break;
             }
@@ -635,8 +662,8 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p, int
                 int gn = g, bn = b;
                 advance(gn, bn);
                 sa = load_side<WT, R, MR, EPI>(p, gn, lane, any);
-                load_w(wa, gn, bn);
-                compute(wb, b);
+                load_w(wa, xqa, gn, bn);
+                compute(wb, xqb, b);
                 if (b == nb - 1) finish(g, sb);
                 g = gn;
                 b = bn;
@@ -668,12 +695,12 @@ size_t tile_bytes(int mr, int k_pad) {
     return (size_t)mr * per_row * sizeof(float);
 }
 
-template <int WT, int R, int U, int MR, int KX, bool NORM, int EPI, bool XH = false>
+template <int WT, int R, int U, int MR, int KX, bool NORM, int EPI, bool XH = false, bool DX = false>
 int launch_fast(hipStream_t s, const GemvParams& p) {
     const int k_pad = padded_k<WT, U>(p.k);
-    const size_t shmem = XH ? (size_t)k_pad * 2 : tile_bytes<WT>(MR, k_pad);
+    const size_t shmem = DX ? 0 : XH ? (size_t)k_pad * 2 : tile_bytes<WT>(MR, k_pad);
     if (shmem > kLdsBudget) return fail(L0H_ERR_UNSUPPORTED, "GEMV activation tile exceeds LDS");
-    auto kern = gemv_nk_kernel<WT, R, U, MR, KX, NORM, EPI, XH>;
+    auto kern = gemv_nk_kernel<WT, R, U, MR, KX, NORM, EPI, XH, DX>;
     // The dynamic tile may reach kLdsBudget on top of the static LDS: raise the limit once.
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsBudget);
@@ -724,10 +751,28 @@ inline bool use_xh(const GemvParams& p) {
            (p.epilogue == EPI_STORE || p.epilogue == EPI_RESIDUAL) && xh_enabled();
 }
 
+// XH launches of rows of at most 64 chunks (K <= 1024) with at most two row groups a wave read x
+// with their weight chunks instead of staging it (DX). Measured (graph replay, cold weights, two
+// interleaved runs each): 896 -> 4864 3.24 -> 3.08 us, 896 -> 1152 and 896 -> 896 unchanged; longer
+// rows lose (4864 -> 896 3.47 -> 3.72 us; the 8B step with DX on its 4096-wide O projection 544.6
+// -> 541.1 tokens/s). L0H_GEMV_DX=0 keeps the staging (A/B measurements).
+inline bool use_dx(const GemvParams& p, int r) {
+    static const bool on = [] {
+        const char* e = std::getenv("L0H_GEMV_DX");
+        return !e || std::atoi(e) != 0;
+    }();
+    const long groups = (p.n + r - 1) / r;
+    const long blocks = p.max_blocks > 0 ? std::min<long>(p.max_blocks, (groups + kWaves - 1) / kWaves)
+                                         : (groups + kWaves - 1) / kWaves;
+    return on && p.k / 16 <= 64 && groups <= 2 * blocks * kWaves;
+}
+
 template <int WT, int R, int U, int KX>
 int dispatch_one(hipStream_t s, const GemvParams& p) {
     if constexpr (WT == L0H_I8PC)
-        if (use_xh(p)) return launch_fast<WT, R, U, 1, KX, false, EPI_STORE, true>(s, p);
+        if (use_xh(p))
+            return use_dx(p, R) ? launch_fast<WT, R, U, 1, 1, false, EPI_STORE, true, true>(s, p)
+                                : launch_fast<WT, R, U, 1, KX, false, EPI_STORE, true>(s, p);
     switch (p.epilogue) {
     case EPI_SWIGLU: return launch_fast<WT, R, U, 1, KX, true, EPI_SWIGLU>(s, p);
     case EPI_QKV: return launch_fast<WT, R, U, 1, KX, true, EPI_QKV>(s, p);

@@ -64,6 +64,29 @@ def test_gemv_int8_config1_fp16_io(device, suite):
     assert rel_err(y, want) < 1e-3
 
 
+@pytest.mark.parametrize("n,k", [(4864, 896), (1001, 64), (515, 1024), (3, 512), (1152, 896)])
+@pytest.mark.parametrize("y_dtype", [l0.F32, l0.F16])
+def test_int8_gemv_fp16_row_short_rows(device, suite, n, k, y_dtype):
+    """int8 rows of at most 1024 values against one fp16 row, one or two row groups a wave: each
+    lane reads the activations under its weight chunks itself (no staged row), and a chunk clamped
+    past K (k = 64: 4 chunks for 64 lanes; k = 896: 56) must add nothing. Odd and tiny row counts
+    clamp the last row group."""
+    rng = np.random.default_rng(n + 3 * k + y_dtype)
+    q = rng.integers(-127, 128, (n, k)).astype(np.int8)
+    q[0, :] = 127
+    q[-1, :] = -128
+    s = rng.uniform(1e-3, 1e-2, n).astype(np.float16)
+    x = rng.normal(0, 1, k).astype(np.float16)
+    want = orc.gemv_nk(orc.I8PC, q, x.astype(np.float32), s.view(np.uint16))[0]
+    ysize = 2 if y_dtype == l0.F16 else 4
+    qb, sb, xb, yb = up(device, q), up(device, s.view(np.uint16)), up(device, x), device.alloc(n * ysize)
+    suite.gemv_nk(l0.I8PC, 1, n, k, xb, l0.F16, qb, sb, yb, y_dtype)
+    y = yb.read(np.float16 if y_dtype == l0.F16 else np.float32, n).astype(np.float32)
+    assert rel_err(y, want) < (1e-3 if y_dtype == l0.F16 else 2e-5), rel_err(y, want)
+    for b in (qb, sb, xb, yb):
+        b.free()
+
+
 @pytest.mark.parametrize("rows", [2, 3, 5, 8])
 @pytest.mark.parametrize("storage", [l0.I8PC, l0.F16])
 def test_gemv_rows_read_weights_once_per_chunk(device, suite, storage, rows):
