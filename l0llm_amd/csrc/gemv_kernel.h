@@ -290,11 +290,14 @@ __device__ __forceinline__ float lane_group_sum(float v) {
 // activations of every weight chunk (pair_halves order), and chunks are computed by chunk_dot_h;
 // there are no bias terms. DX (with XH, for launches of one or two row groups a wave): no staging
 // and no block barrier; each lane reads the 32 bytes of x under each of its weight chunks with the
-// chunk (from L1 / L2: every wave reads the same row), and a clamped chunk past K adds 0.
-template <int WT, int R, int U, int MR, int KX, bool NORM, int EPI, bool XH = false, bool DX = false>
+// chunk (from L1 / L2: every wave reads the same row), and a clamped chunk past K adds 0. XHW (with
+// XH): the row has an fp32 twin (p.x_wide) and a range flag; a launch whose flag is set stages the
+// twin as fp32 and computes as the fp32 path does, otherwise it is XH (the LDS holds either tile).
+template <int WT, int R, int U, int MR, int KX, bool NORM, int EPI, bool XH = false, bool DX = false, bool XHW = false>
 __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p, int k_pad) {
     static_assert(!XH || (WT == L0H_I8PC && MR == 1 && !NORM && EPI == EPI_STORE), "fp16-row int8 GEMV");
-    static_assert(!DX || XH, "direct x reads: the fp16-row int8 GEMV");
+    static_assert(!DX || (XH && !XHW), "direct x reads: the fp16-row int8 GEMV without a twin");
+    static_assert(!XHW || XH, "the fp32 twin of an fp16-row int8 GEMV");
     extern __shared__ float4 smem4[];
     float* xs = reinterpret_cast<float*>(smem4);  // [MR, k_pad], zero past K
     uint4* xh = reinterpret_cast<uint4*>(smem4);  // XH: [2, k_pad / 16] slots, zero past K
@@ -416,7 +419,7 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p, int
             ss = wave_sum(ss);
             if (lane == 0) red[wave] = ss;
         }
-        if constexpr (XH) {
+        if (XH && !(XHW && wide)) {
             // chunk idx of x is 8 fp16 activations: half idx & 1 of weight chunk idx >> 1
 #pragma unroll
             for (int i = 0; i < KX; i++) {
@@ -471,7 +474,7 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p, int
                 }
             }
         }
-        if constexpr (XH) {
+        if (XH && !(XHW && wide)) {
             for (int c = K / 16 + tid; c < kc_pad; c += kBlock) {
                 xh[c] = make_uint4(0u, 0u, 0u, 0u);
                 xh[kc_pad + c] = make_uint4(0u, 0u, 0u, 0u);
@@ -521,7 +524,7 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p, int
             }
             return;
         }
-        if constexpr (XH) {
+        if (XH && !(XHW && wide)) {
 #pragma unroll
             for (int u = 0; u < U; u++) {
                 const int c = batch * KB + u * 64 + lane;  // < nb * KB: x is zero past K
@@ -695,12 +698,12 @@ size_t tile_bytes(int mr, int k_pad) {
     return (size_t)mr * per_row * sizeof(float);
 }
 
-template <int WT, int R, int U, int MR, int KX, bool NORM, int EPI, bool XH = false, bool DX = false>
+template <int WT, int R, int U, int MR, int KX, bool NORM, int EPI, bool XH = false, bool DX = false, bool XHW = false>
 int launch_fast(hipStream_t s, const GemvParams& p) {
     const int k_pad = padded_k<WT, U>(p.k);
-    const size_t shmem = DX ? 0 : XH ? (size_t)k_pad * 2 : tile_bytes<WT>(MR, k_pad);
+    const size_t shmem = DX ? 0 : (XH && !XHW) ? (size_t)k_pad * 2 : tile_bytes<WT>(MR, k_pad);
     if (shmem > kLdsBudget) return fail(L0H_ERR_UNSUPPORTED, "GEMV activation tile exceeds LDS");
-    auto kern = gemv_nk_kernel<WT, R, U, MR, KX, NORM, EPI, XH, DX>;
+    auto kern = gemv_nk_kernel<WT, R, U, MR, KX, NORM, EPI, XH, DX, XHW>;
     // The dynamic tile may reach kLdsBudget on top of the static LDS: raise the limit once.
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsBudget);
@@ -751,6 +754,17 @@ inline bool use_xh(const GemvParams& p) {
            (p.epilogue == EPI_STORE || p.epilogue == EPI_RESIDUAL) && xh_enabled();
 }
 
+// int8 weights against an fp16 row with an fp32 twin (the decode step's down projection): XH unless
+// the twin's range flag is set (XHW). L0H_GEMV_XHW=0 keeps such rows on the fp32 staging.
+inline bool use_xhw(const GemvParams& p) {
+    static const bool on = [] {
+        const char* e = std::getenv("L0H_GEMV_XHW");
+        return !e || std::atoi(e) != 0;
+    }();
+    return on && p.w_dtype == L0H_I8PC && p.m == 1 && p.x_dtype == L0H_F16 && !p.norm_w && p.x_wide &&
+           p.range_flag && (p.epilogue == EPI_STORE || p.epilogue == EPI_RESIDUAL) && xh_enabled();
+}
+
 // XH launches of rows of at most 64 chunks (K <= 1024) with at most two row groups a wave read x
 // with their weight chunks instead of staging it (DX). Measured (graph replay, cold weights, two
 // interleaved runs each): 896 -> 4864 3.24 -> 3.08 us, 896 -> 1152 and 896 -> 896 unchanged; longer
@@ -769,10 +783,12 @@ inline bool use_dx(const GemvParams& p, int r) {
 
 template <int WT, int R, int U, int KX>
 int dispatch_one(hipStream_t s, const GemvParams& p) {
-    if constexpr (WT == L0H_I8PC)
+    if constexpr (WT == L0H_I8PC) {
         if (use_xh(p))
             return use_dx(p, R) ? launch_fast<WT, R, U, 1, 1, false, EPI_STORE, true, true>(s, p)
                                 : launch_fast<WT, R, U, 1, KX, false, EPI_STORE, true>(s, p);
+        if (use_xhw(p)) return launch_fast<WT, R, U, 1, KX, false, EPI_STORE, true, false, true>(s, p);
+    }
     switch (p.epilogue) {
     case EPI_SWIGLU: return launch_fast<WT, R, U, 1, KX, true, EPI_SWIGLU>(s, p);
     case EPI_QKV: return launch_fast<WT, R, U, 1, KX, true, EPI_QKV>(s, p);
@@ -834,7 +850,7 @@ int dispatch_wt(hipStream_t s, const GemvParams& p, int mr) {
     if (mr == 1 && C > 128 && p.epilogue == EPI_STORE && !p.norm_w) {
         const long waves = (long)(p.max_blocks > 0 ? p.max_blocks : 512) * kWaves;
         if (ceil_div(p.n, 2) < waves) {
-            if constexpr (WT == L0H_I8PC)
+            if constexpr (WT == L0H_I8PC) {
                 if (use_xh(p)) {
                     switch (staged_chunks(p)) {
                     case 1: return launch_fast<WT, 1, 4, 1, 1, false, EPI_STORE, true>(s, p);
@@ -844,6 +860,16 @@ int dispatch_wt(hipStream_t s, const GemvParams& p, int mr) {
                     default: return fail(L0H_ERR_UNSUPPORTED, "GEMV activation row exceeds the LDS tile");
                     }
                 }
+                if (use_xhw(p)) {
+                    switch (staged_chunks(p)) {
+                    case 1: return launch_fast<WT, 1, 4, 1, 1, false, EPI_STORE, true, false, true>(s, p);
+                    case 2: return launch_fast<WT, 1, 4, 1, 2, false, EPI_STORE, true, false, true>(s, p);
+                    case 4: return launch_fast<WT, 1, 4, 1, 4, false, EPI_STORE, true, false, true>(s, p);
+                    case 8: return launch_fast<WT, 1, 4, 1, 8, false, EPI_STORE, true, false, true>(s, p);
+                    default: return fail(L0H_ERR_UNSUPPORTED, "GEMV activation row exceeds the LDS tile");
+                    }
+                }
+            }
             switch (staged_chunks(p)) {
             case 1: return launch_fast<WT, 1, 4, 1, 1, false, EPI_STORE>(s, p);
             case 2: return launch_fast<WT, 1, 4, 1, 2, false, EPI_STORE>(s, p);
