@@ -824,18 +824,18 @@ int dispatch_mr(hipStream_t s, const GemvParams& p, int mr) {
     return launch_fast<WT, R, U, 8, 1, false, EPI_STORE>(s, p);
 }
 
-// Rows per wave item (R) and 16-byte chunks per row per lane (U), chosen by the row length so an
-// item carries about 8 KiB of real weights for int8 (R * U KiB): C <= 64 chunks per row -> 8 rows
-// x 1 chunk per lane, C <= 128 -> 4 x 2, else 2 x 4; short rows of a matrix with few rows take 2-row
+// Rows per wave item (R) and 16-byte chunks per row per lane (U), chosen by the row length: C <= 64
+// chunks per row -> 4 rows x 1 chunk per lane (4 KiB of int8 weights an item), C <= 128 -> 4 x 2,
+// else 2 x 4 (8 KiB); short rows of a matrix with few rows take 2-row
 // items (2 x 1, 2 x 2), long ones 1-row items (1 x 4). Several activation rows use 2 x 4.
 template <int WT>
 int dispatch_wt(hipStream_t s, const GemvParams& p, int mr) {
     const int C = p.k / WTraits<WT>::kElems;
-    // Short rows (at most 128 chunks): the 8- or 4-row items suit long streams (every wave gets at
-    // least four of them); fewer rows leave most of the grid idle, so those take 2-row items, one
-    // item per wave or a few. Measured (int8, K = 896, graph replay, cold weights): 896 -> 4864
-    // 4.30 -> 3.45 us, 896 -> 1152 3.96 -> 2.55, 896 -> 9728 5.43 -> 4.45; 896 -> 151936 keeps
-    // 8-row items (28.7 us against 39.5 with 2-row ones).
+    // Short rows (at most 128 chunks): the 4-row items below suit long streams (matrices with at
+    // least four 8- or 4-row groups per wave of the grid); fewer rows leave most of the grid idle,
+    // so those take 2-row items, one item per wave or a few. Measured (int8, K = 896, graph replay,
+    // cold weights, 2-row items against 8-row ones): 896 -> 4864 4.30 -> 3.45 us, 896 -> 1152 3.96
+    // -> 2.55, 896 -> 9728 5.43 -> 4.45.
     if (mr == 1 && C <= 128) {
         const long waves = (long)(p.max_blocks > 0 ? p.max_blocks : 512) * kWaves;
         const int r_long = C <= 64 ? 8 : 4;
@@ -880,7 +880,11 @@ int dispatch_wt(hipStream_t s, const GemvParams& p, int mr) {
             }
         }
     }
-    if (mr == 1 && C <= 64) return dispatch_mr<WT, 8, 1>(s, p, mr);
+    // Rows of at most 64 chunks in a tall matrix: 4-row items (90 registers: 4 blocks per CU fit),
+    // not 8-row ones (142 registers: 3 blocks per CU). Measured (int8, 896 -> 151936, graph replay,
+    // cold weights, two runs each): 8 x 1 items at 3 blocks per CU 27.1 us, 4 x 1 at 4 blocks
+    // 24.6 us, 4 x 1 at 5 blocks 25.3 us, 2 x 1 at 6 blocks 24.4-24.6 us, at 8 blocks 25.3 us.
+    if (mr == 1 && C <= 64) return dispatch_mr<WT, 4, 1>(s, p, mr);
     if (mr == 1 && C <= 128) return dispatch_mr<WT, 4, 2>(s, p, mr);
     return dispatch_mr<WT, 2, 4>(s, p, mr);
 }
