@@ -464,6 +464,61 @@ constexpr size_t dma_tile_bytes(int bm, int bn) {
     return (size_t)(bm / dma_epi_passes(bm, bn)) * (bn + 8) * sizeof(float);
 }
 
+// Epilogue of the LDS-ring GEMMs through LDS: the fp32 tile (rows padded to BN + 8 floats) is
+// written fragment by fragment, then read back as 4 consecutive columns per thread, so each output
+// row segment is stored by consecutive lanes (16 / 8 / 4 contiguous bytes per lane instead of one
+// 2-byte value per lane spread over two rows). K groups (KG > 1): group 0 writes its sums, the
+// others add theirs in group order. The caller has waited for every load into LDS.
+template <int WT, int BM, int BN, int WGM, int WGN, int KG>
+__device__ __forceinline__ void dma_epilogue(const acc_t<32> (&acc)[BM / WGM / 32][BN / WGN / 32], float* tile, int tid,
+                                             int lane, int wave, int kg, int m0, int n0, int M, int N,
+                                             const uint16_t* __restrict__ scales, void* Y, int y_dtype, int epi,
+                                             float* partial, int bz, const LaunchGate& gate) {
+    constexpr bool I8 = WT == L0H_I8PC;
+    constexpr int NT = 64 * WGM * WGN * KG;
+    constexpr int TM = BM / WGM, TN = BN / WGN;
+    constexpr int FI = TM / 32, FJ = TN / 32;
+    const int wq = wave % (WGM * WGN);
+    const int wm = wq % WGM, wn = wq / WGM;
+    constexpr int LDT = BN + 8;  // 4 rows apart = 128 bytes mod 256: the two half-waves' rows use distinct banks
+    constexpr int EP = dma_epi_passes(BM, BN), BMP = BM / EP;  // passes, tile rows per pass
+    static_assert(BMP % TM == 0, "a wave's rows fall in one epilogue pass");
+    constexpr int C4 = BN / 4, RPP = NT / C4;  // threads per row, rows per store round
+    static_assert(NT % C4 == 0 && BMP % RPP == 0, "epilogue pass shape");
+    const int c4 = tid % C4;
+#pragma unroll
+    for (int pass = 0; pass < EP; pass++) {
+        lds_barrier();  // the stages (first pass) or the previous pass's rows are no longer read
+#pragma unroll
+        for (int g = 0; g < KG; g++) {  // group 0 writes its sums, the others add theirs in order
+            if (g > 0) lds_barrier();
+            if (kg == g && wm * TM / BMP == pass) {
+#pragma unroll
+                for (int j = 0; j < FJ; j++) {
+                    const int c = wn * TN + j * 32 + lane % 32;
+                    // int8: the weight row's scale (output column c)
+                    const float sc = I8 ? __half2float(__ushort_as_half(scales[min(n0 + c, N - 1)])) : 1.f;
+#pragma unroll
+                    for (int i = 0; i < FI; i++)
+#pragma unroll
+                        for (int r = 0; r < 16; r++) {
+                            float& t = tile[(wm * TM - pass * BMP + i * 32 + (r / 4) * 8 + (lane / 32) * 4 + (r % 4)) * LDT + c];
+                            const float v = I8 ? acc[i][j][r] * sc : acc[i][j][r];
+                            t = g == 0 ? v : t + v;
+                        }
+                }
+            }
+        }
+        lds_barrier();
+#pragma unroll 4
+        for (int r0 = 0; r0 < BMP; r0 += RPP) {
+            const int rl = r0 + tid / C4;
+            const float4 v = *reinterpret_cast<const float4*>(tile + rl * LDT + 4 * c4);
+            store4(epi, partial, bz, Y, y_dtype, M, N, m0 + pass * BMP + rl, n0 + 4 * c4, v, gate);
+        }
+    }
+}
+
 // Y[M, N] = X[M, K] W[N, K]^T for 16-bit operands, K a multiple of 64. Block tile BM x BN, waves
 // WGM x WGN with a (BM / WGM) x (BN / WGN) tile each of 32 x 32 x 16 MFMAs. K advances in stages of
 // 64 through NS LDS buffers: at stage t every wave waits for its own loads of stage t, the block
@@ -652,48 +707,8 @@ __global__ __launch_bounds__(64 * WGM * WGN * KG) __attribute__((amdgpu_waves_pe
         wait_vmcnt<0>();  // the clamped tail loads: none may still write LDS when the block exits
     }
 
-    // Epilogue through LDS: the fp32 tile (rows padded to BN + 8 floats) is written fragment by
-    // fragment, then read back as 4 consecutive columns per thread, so each output row segment is
-    // stored by consecutive lanes (16 / 8 / 4 contiguous bytes per lane instead of one 2-byte value
-    // per lane spread over two rows).
-    float* tile = reinterpret_cast<float*>(gemm_dma_smem);
-    constexpr int LDT = BN + 8;  // 4 rows apart = 128 bytes mod 256: the two half-waves' rows use distinct banks
-    constexpr int EP = dma_epi_passes(BM, BN), BMP = BM / EP;  // passes, tile rows per pass
-    static_assert(BMP % TM == 0, "a wave's rows fall in one epilogue pass");
-    constexpr int C4 = BN / 4, RPP = NT / C4;  // threads per row, rows per store round
-    static_assert(NT % C4 == 0 && BMP % RPP == 0, "epilogue pass shape");
-    const int c4 = tid % C4;
-#pragma unroll
-    for (int pass = 0; pass < EP; pass++) {
-        lds_barrier();  // the stages (first pass) or the previous pass's rows are no longer read
-#pragma unroll
-        for (int g = 0; g < KG; g++) {  // group 0 writes its sums, the others add theirs in order
-            if (g > 0) lds_barrier();
-            if (kg == g && wm * TM / BMP == pass) {
-#pragma unroll
-                for (int j = 0; j < FJ; j++) {
-                    const int c = wn * TN + j * 32 + lane % 32;
-                    // int8: the weight row's scale (output column c)
-                    const float sc = I8 ? __half2float(__ushort_as_half(scales[min(n0 + c, N - 1)])) : 1.f;
-#pragma unroll
-                    for (int i = 0; i < FI; i++)
-#pragma unroll
-                        for (int r = 0; r < 16; r++) {
-                            float& t = tile[(wm * TM - pass * BMP + i * 32 + (r / 4) * 8 + (lane / 32) * 4 + (r % 4)) * LDT + c];
-                            const float v = I8 ? acc[i][j][r] * sc : acc[i][j][r];
-                            t = g == 0 ? v : t + v;
-                        }
-                }
-            }
-        }
-        lds_barrier();
-#pragma unroll 4
-        for (int r0 = 0; r0 < BMP; r0 += RPP) {
-            const int rl = r0 + tid / C4;
-            const float4 v = *reinterpret_cast<const float4*>(tile + rl * LDT + 4 * c4);
-            store4(epi, partial, bz, Y, y_dtype, M, N, m0 + pass * BMP + rl, n0 + 4 * c4, v, gate);
-        }
-    }
+    dma_epilogue<WT, BM, BN, WGM, WGN, KG>(acc, reinterpret_cast<float*>(gemm_dma_smem), tid, lane, wave, kg, m0, n0,
+                                           M, N, scales, Y, y_dtype, epi, partial, bz, gate);
 }
 
 // Sum of the K splits' partials in split order, then the epilogue: store, add to fp32 Y, or (one
