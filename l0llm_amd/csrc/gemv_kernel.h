@@ -293,11 +293,30 @@ __device__ __forceinline__ float lane_group_sum(float v) {
 // chunk (from L1 / L2: every wave reads the same row), and a clamped chunk past K adds 0. XHW (with
 // XH): the row has an fp32 twin (p.x_wide) and a range flag; a launch whose flag is set stages the
 // twin as fp32 and computes as the fp32 path does, otherwise it is XH (the LDS holds either tile).
-template <int WT, int R, int U, int MR, int KX, bool NORM, int EPI, bool XH = false, bool DX = false, bool XHW = false>
+// Issue priority from progress: 3 for the first quarter of a wave's items, then 2, 1 and 0.
+__device__ __forceinline__ void progress_priority(int done, int items) {
+    const int q = (4 * done) / max(items, 1);
+    if (q <= 0)
+        __builtin_amdgcn_s_setprio(3);
+    else if (q == 1)
+        __builtin_amdgcn_s_setprio(2);
+    else if (q == 2)
+        __builtin_amdgcn_s_setprio(1);
+    else
+        __builtin_amdgcn_s_setprio(0);
+}
+
+template <int WT, int R, int U, int MR, int KX, bool NORM, int EPI, bool XH = false, bool DX = false, bool XHW = false,
+          bool PRIO = false>
 __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p, int k_pad) {
     static_assert(!XH || (WT == L0H_I8PC && MR == 1 && !NORM && EPI == EPI_STORE), "fp16-row int8 GEMV");
     static_assert(!DX || (XH && !XHW), "direct x reads: the fp16-row int8 GEMV without a twin");
     static_assert(!XHW || XH, "the fp32 twin of an fp16-row int8 GEMV");
+    // PRIO: each wave steps its instruction-issue priority down (s_setprio 3 -> 0) as it works
+    // through its items, so the waves that started later or fell behind win the SIMD's arbitration
+    // and the launch's waves end closer together.
+    static_assert(!PRIO || MR == 1, "progress priority: one activation row");
+    if constexpr (PRIO) __builtin_amdgcn_s_setprio(3);
     extern __shared__ float4 smem4[];
     float* xs = reinterpret_cast<float*>(smem4);  // [MR, k_pad], zero past K
     uint4* xh = reinterpret_cast<uint4*>(smem4);  // XH: [2, k_pad / 16] slots, zero past K
@@ -655,6 +674,7 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p, int
                 g = gn;
                 b = bn;
                 i++;
+                if constexpr (PRIO) progress_priority(i, items);
             }
             if (i + 1 == items) {
                 compute(wb, xqb, b);
@@ -671,6 +691,7 @@ __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p, int
                 g = gn;
                 b = bn;
                 i++;
+                if constexpr (PRIO) progress_priority(i, items);
             }
         }
     }
@@ -698,12 +719,13 @@ size_t tile_bytes(int mr, int k_pad) {
     return (size_t)mr * per_row * sizeof(float);
 }
 
-template <int WT, int R, int U, int MR, int KX, bool NORM, int EPI, bool XH = false, bool DX = false, bool XHW = false>
+template <int WT, int R, int U, int MR, int KX, bool NORM, int EPI, bool XH = false, bool DX = false, bool XHW = false,
+          bool PRIO = false>
 int launch_fast(hipStream_t s, const GemvParams& p) {
     const int k_pad = padded_k<WT, U>(p.k);
     const size_t shmem = DX ? 0 : (XH && !XHW) ? (size_t)k_pad * 2 : tile_bytes<WT>(MR, k_pad);
     if (shmem > kLdsBudget) return fail(L0H_ERR_UNSUPPORTED, "GEMV activation tile exceeds LDS");
-    auto kern = gemv_nk_kernel<WT, R, U, MR, KX, NORM, EPI, XH, DX, XHW>;
+    auto kern = gemv_nk_kernel<WT, R, U, MR, KX, NORM, EPI, XH, DX, XHW, PRIO>;
     // The dynamic tile may reach kLdsBudget on top of the static LDS: raise the limit once.
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsBudget);
@@ -781,20 +803,20 @@ inline bool use_dx(const GemvParams& p, int r) {
     return on && p.k / 16 <= 64 && groups <= 2 * blocks * kWaves;
 }
 
-template <int WT, int R, int U, int KX>
+template <int WT, int R, int U, int KX, bool PRIO = false>
 int dispatch_one(hipStream_t s, const GemvParams& p) {
     if constexpr (WT == L0H_I8PC) {
         if (use_xh(p))
-            return use_dx(p, R) ? launch_fast<WT, R, U, 1, 1, false, EPI_STORE, true, true>(s, p)
-                                : launch_fast<WT, R, U, 1, KX, false, EPI_STORE, true>(s, p);
-        if (use_xhw(p)) return launch_fast<WT, R, U, 1, KX, false, EPI_STORE, true, false, true>(s, p);
+            return use_dx(p, R) ? launch_fast<WT, R, U, 1, 1, false, EPI_STORE, true, true, false, PRIO>(s, p)
+                                : launch_fast<WT, R, U, 1, KX, false, EPI_STORE, true, false, false, PRIO>(s, p);
+        if (use_xhw(p)) return launch_fast<WT, R, U, 1, KX, false, EPI_STORE, true, false, true, PRIO>(s, p);
     }
     switch (p.epilogue) {
-    case EPI_SWIGLU: return launch_fast<WT, R, U, 1, KX, true, EPI_SWIGLU>(s, p);
-    case EPI_QKV: return launch_fast<WT, R, U, 1, KX, true, EPI_QKV>(s, p);
+    case EPI_SWIGLU: return launch_fast<WT, R, U, 1, KX, true, EPI_SWIGLU, false, false, false, PRIO>(s, p);
+    case EPI_QKV: return launch_fast<WT, R, U, 1, KX, true, EPI_QKV, false, false, false, PRIO>(s, p);
     default:
-        return p.norm_w ? launch_fast<WT, R, U, 1, KX, true, EPI_STORE>(s, p)
-                        : launch_fast<WT, R, U, 1, KX, false, EPI_STORE>(s, p);
+        return p.norm_w ? launch_fast<WT, R, U, 1, KX, true, EPI_STORE, false, false, false, PRIO>(s, p)
+                        : launch_fast<WT, R, U, 1, KX, false, EPI_STORE, false, false, false, PRIO>(s, p);
     }
 }
 
@@ -807,15 +829,15 @@ int staged_chunks(const GemvParams& p) {
     return kx;
 }
 
-template <int WT, int R, int U>
+template <int WT, int R, int U, bool PRIO = false>
 int dispatch_mr(hipStream_t s, const GemvParams& p, int mr) {
     if (mr == 1) {
         switch (staged_chunks(p)) {
-        case 1: return dispatch_one<WT, R, U, 1>(s, p);
-        case 2: return dispatch_one<WT, R, U, 2>(s, p);
-        case 4: return dispatch_one<WT, R, U, 4>(s, p);
-        case 8: return dispatch_one<WT, R, U, 8>(s, p);
-        case 16: return dispatch_one<WT, R, U, 16>(s, p);
+        case 1: return dispatch_one<WT, R, U, 1, PRIO>(s, p);
+        case 2: return dispatch_one<WT, R, U, 2, PRIO>(s, p);
+        case 4: return dispatch_one<WT, R, U, 4, PRIO>(s, p);
+        case 8: return dispatch_one<WT, R, U, 8, PRIO>(s, p);
+        case 16: return dispatch_one<WT, R, U, 16, PRIO>(s, p);
         default: return fail(L0H_ERR_UNSUPPORTED, "GEMV activation row exceeds the LDS tile");
         }
     }
@@ -884,7 +906,13 @@ int dispatch_wt(hipStream_t s, const GemvParams& p, int mr) {
     // not 8-row ones (142 registers: 3 blocks per CU). Measured (int8, 896 -> 151936, graph replay,
     // cold weights, two runs each): 8 x 1 items at 3 blocks per CU 27.1 us, 4 x 1 at 4 blocks
     // 24.6 us, 4 x 1 at 5 blocks 25.3 us, 2 x 1 at 6 blocks 24.4-24.6 us, at 8 blocks 25.3 us.
-    if (mr == 1 && C <= 64) return dispatch_mr<WT, 4, 1>(s, p, mr);
+    // These launches also lower each wave's issue priority as it progresses: the later-dispatched
+    // blocks of a CU otherwise lose the arbitration to the older waves and end ~4 us after them.
+    // Measured (896 -> 151936, graph replay, cold weights, three interleaved pairs): fp16 row 24.62-
+    // 24.68 -> 23.79-23.87 us, fp32 row 24.74-24.92 -> 24.32-24.44 us; the 8B shapes showed no
+    // change in a timing copy, and in the 8B decode step every wave starting at priority 3 cost
+    // 0.7 % (538.6 against 542.2 tokens/s, three interleaved pairs), so they keep the priority flat.
+    if (mr == 1 && C <= 64) return dispatch_mr<WT, 4, 1, true>(s, p, mr);
     if (mr == 1 && C <= 128) return dispatch_mr<WT, 4, 2>(s, p, mr);
     return dispatch_mr<WT, 2, 4>(s, p, mr);
 }
