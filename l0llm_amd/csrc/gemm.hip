@@ -547,7 +547,6 @@ __global__ __launch_bounds__(64 * WGM * WGN * KG) __attribute__((amdgpu_waves_pe
     constexpr int STAGE = BM * ROWA + BN * ROWB;  // bytes per stage
     static_assert(KG == 1 || KG == 2 || KG == 4, "K groups");
     constexpr int NW = WGM * WGN * KG;         // waves
-    constexpr int NT = 64 * NW;                // threads
     constexpr int TM = BM / WGM, TN = BN / WGN;
     constexpr int FI = TM / 32, FJ = TN / 32;
     constexpr int GA = BM / 8, GB = BN / RPB;  // 1 KiB loads per stage of A and B
