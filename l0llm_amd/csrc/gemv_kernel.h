@@ -285,14 +285,6 @@ __device__ __forceinline__ float lane_group_sum(float v) {
     return v;
 }
 
-// XH (int8 weights, one fp16 activation row, no RMSNorm, store / residual epilogue): the row is
-// staged as fp16 in two planes of k_pad / 16 slots of 16 bytes, the first 8 and the last 8
-// activations of every weight chunk (pair_halves order), and chunks are computed by chunk_dot_h;
-// there are no bias terms. DX (with XH, for launches of one or two row groups a wave): no staging
-// and no block barrier; each lane reads the 32 bytes of x under each of its weight chunks with the
-// chunk (from L1 / L2: every wave reads the same row), and a clamped chunk past K adds 0. XHW (with
-// XH): the row has an fp32 twin (p.x_wide) and a range flag; a launch whose flag is set stages the
-// twin as fp32 and computes as the fp32 path does, otherwise it is XH (the LDS holds either tile).
 // Issue priority from progress: 3 for the first quarter of a wave's items, then 2, 1 and 0.
 __device__ __forceinline__ void progress_priority(int done, int items) {
     const int q = (4 * done) / max(items, 1);
@@ -306,6 +298,16 @@ __device__ __forceinline__ void progress_priority(int done, int items) {
         __builtin_amdgcn_s_setprio(0);
 }
 
+// XH (int8 weights, one fp16 activation row, no RMSNorm, store / residual epilogue): the row is
+// staged as fp16 in two planes of k_pad / 16 slots of 16 bytes, the first 8 and the last 8
+// activations of every weight chunk (pair_halves order), and chunks are computed by chunk_dot_h;
+// there are no bias terms. DX (with XH, for launches of one or two row groups a wave): no staging
+// and no block barrier; each lane reads the 32 bytes of x under each of its weight chunks with the
+// chunk (from L1 / L2: every wave reads the same row), and a clamped chunk past K adds 0. XHW (with
+// XH): the row has an fp32 twin (p.x_wide) and a range flag; a launch whose flag is set stages the
+// twin as fp32 and computes as the fp32 path does, otherwise it is XH (the LDS holds either tile).
+// PRIO (one activation row): each wave steps its instruction-issue priority down with its
+// progress (progress_priority).
 template <int WT, int R, int U, int MR, int KX, bool NORM, int EPI, bool XH = false, bool DX = false, bool XHW = false,
           bool PRIO = false>
 __global__ __launch_bounds__(kBlock) void gemv_nk_kernel(const GemvParams p, int k_pad) {
