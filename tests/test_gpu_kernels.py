@@ -87,6 +87,26 @@ def test_int8_gemv_fp16_row_short_rows(device, suite, n, k, y_dtype):
         b.free()
 
 
+# Tall matrices of rows of at most 64 int8 chunks: 4-row items at four blocks per CU, each wave
+# stepping its issue priority down with its progress; fp16 and fp32 rows, a last row group that
+# the row count leaves partial (70001, 65537), rows of 32 chunks (K = 512).
+@pytest.mark.parametrize("n,k", [(151936, 896), (70001, 896), (65537, 512)])
+@pytest.mark.parametrize("x_dtype", [l0.F16, l0.F32])
+def test_int8_gemv_tall_short_rows(device, suite, n, k, x_dtype):
+    rng = np.random.default_rng(n + k + x_dtype)
+    q = rng.integers(-127, 128, (n, k)).astype(np.int8)
+    q[0, :] = 127
+    q[-1, :] = -128
+    s = rng.uniform(1e-3, 1e-2, n).astype(np.float16)
+    x = rng.normal(0, 1, k).astype(np.float16 if x_dtype == l0.F16 else np.float32)
+    want = orc.gemv_nk(orc.I8PC, q, x.astype(np.float32), s.view(np.uint16))[0]
+    qb, sb, xb, yb = up(device, q), up(device, s.view(np.uint16)), up(device, x), device.alloc(n * 4)
+    suite.gemv_nk(l0.I8PC, 1, n, k, xb, x_dtype, qb, sb, yb, l0.F32)
+    assert rel_err(yb.read(np.float32, n), want) < 2e-5
+    for b in (qb, sb, xb, yb):
+        b.free()
+
+
 @pytest.mark.parametrize("rows", [2, 3, 5, 8])
 @pytest.mark.parametrize("storage", [l0.I8PC, l0.F16])
 def test_gemv_rows_read_weights_once_per_chunk(device, suite, storage, rows):
