@@ -1103,7 +1103,18 @@ int attention_default_splits(int batch, int nkv, int max_len, int compute_units)
     };
     if (per_cu_env) return splits_for(per_cu_env);
     const int two = splits_for(2);
-    return len / two >= 2048 ? two : splits_for(1);
+    if (len / two >= 2048) return two;
+    // Slices of four steps at one block per CU: twice the splits make them two-step slices, which
+    // the straight-line kernel takes, at two blocks per CU. Measured (fp16, 32 q / 8 kv heads, cold
+    // K / V, graph replay, two runs each): batch 1 x 8192 13.45 -> 12.15 us, 2 x 4096 13.56 ->
+    // 12.42, 4 x 2048 13.45 -> 12.43, 8 x 1024 13.28 -> 12.45; slices of three steps lose (batch 1 x
+    // 6000: 11.13 -> 11.52 us, the doubled slices half empty), so they keep one block per CU.
+    const int one = splits_for(1);
+    const long lo_len = 3L * one * min_pos / 2, hi_len = 2L * one * min_pos;
+    if (len > lo_len && len <= hi_len && 2 * one <= kMaxSplits &&
+        (long)batch * nkv * 2 * one <= 2L * std::max(compute_units, 1))
+        return 2 * one;
+    return one;
 }
 
 size_t attention_partials_bytes(const AttnParams& p) {

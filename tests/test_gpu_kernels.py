@@ -366,10 +366,12 @@ def test_attention_decode_reads_only_written_rows(device, suite, hd, nh, nkv, se
     assert rel_err(out, want) < 1e-4, rel_err(out, want)
 
 
-@pytest.mark.parametrize("batch,seq", [(8, 512), (1, 32768), (8, 8192)])
+@pytest.mark.parametrize("batch,seq", [(8, 512), (1, 32768), (8, 8192), (2, 4096), (1, 7000)])
 def test_attention_decode_batched_fp16(device, suite, batch, seq):
     """GQA 32q/8kv/128, fp16 q/K/V, fp16 out, fp32 softmax. Splits of 128 (8 x 512) and 2048
-    (8 x 8192) positions take the reduce-scattered softmax, 1024 (1 x 32768) the per-slot one."""
+    (8 x 8192) positions take the reduce-scattered softmax, 1024 (1 x 32768) the per-slot one;
+    2 x 4096 and 1 x 7000 (four-step slices at one block per CU) take twice the splits, two-step
+    slices on the straight-line kernel (1 x 7000: the last split partly empty)."""
     rng = np.random.default_rng(batch * seq)
     hd, nh, nkv = 128, 32, 8
     kf = rng.normal(0, 1, (batch, seq, nkv * hd)).astype(np.float16)
