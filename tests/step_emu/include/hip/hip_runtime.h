@@ -170,6 +170,7 @@ inline void s_sleep(int) { std::this_thread::sleep_for(std::chrono::microseconds
 #define __builtin_amdgcn_permlane32_swap emu::permlane32_swap
 #define __builtin_amdgcn_s_barrier() emu::s_barrier()
 #define __builtin_amdgcn_s_sleep(n) emu::s_sleep(n)
+#define __builtin_amdgcn_s_setprio(n) ((void)0)  // issue priority: no effect on a host thread
 #define __builtin_amdgcn_fence(order, scope) std::atomic_thread_fence(std::memory_order_seq_cst)
 #define __builtin_amdgcn_exp2f(x) std::exp2f(x)
 #define __syncthreads() emu::s_barrier()
