@@ -851,7 +851,8 @@ int dispatch_mr(hipStream_t s, const GemvParams& p, int mr) {
 // Rows per wave item (R) and 16-byte chunks per row per lane (U), chosen by the row length: C <= 64
 // chunks per row -> 4 rows x 1 chunk per lane (4 KiB of int8 weights an item), C <= 128 -> 4 x 2,
 // else 2 x 4 (8 KiB); short rows of a matrix with few rows take 2-row
-// items (2 x 1, 2 x 2), long ones 1-row items (1 x 4). Several activation rows use 2 x 4.
+// items (2 x 1, 2 x 2), or 1-row ones (1 x 1) where the matrix has at most one row per wave, long
+// ones 1-row items (1 x 4). Several activation rows use 2 x 4.
 template <int WT>
 int dispatch_wt(hipStream_t s, const GemvParams& p, int mr) {
     const int C = p.k / WTraits<WT>::kElems;
@@ -864,6 +865,21 @@ int dispatch_wt(hipStream_t s, const GemvParams& p, int mr) {
         const long waves = (long)(p.max_blocks > 0 ? p.max_blocks : 512) * kWaves;
         const int r_long = C <= 64 ? 8 : 4;
         if (ceil_div(p.n, r_long) < 4 * waves) {
+            // At most one row per wave of the grid (plain store or residual epilogue, no fused
+            // norm): 1-row items, twice the waves of 2-row items, each waiting on one row. Measured
+            // (int8, K = 896, fp16 row, graph replay, cold weights, three interleaved pairs): 896 ->
+            // 1152 2.45 -> 2.37 us, 896 -> 896 2.44 -> 2.33 us; with more rows than waves 2-row items
+            // stay ahead (896 -> 4864 3.07 against 3.08, 896 -> 9728 3.89 against 4.12).
+            if (C <= 64 && p.n <= waves && !p.norm_w && staged_chunks(p) == 1 &&
+                (p.epilogue == EPI_STORE || p.epilogue == EPI_RESIDUAL)) {
+                if constexpr (WT == L0H_I8PC) {
+                    if (use_xh(p))
+                        return use_dx(p, 1) ? launch_fast<WT, 1, 1, 1, 1, false, EPI_STORE, true, true>(s, p)
+                                            : launch_fast<WT, 1, 1, 1, 1, false, EPI_STORE, true>(s, p);
+                    if (use_xhw(p)) return launch_fast<WT, 1, 1, 1, 1, false, EPI_STORE, true, false, true>(s, p);
+                }
+                return launch_fast<WT, 1, 1, 1, 1, false, EPI_STORE>(s, p);
+            }
             if (C <= 64) return dispatch_mr<WT, 2, 1>(s, p, mr);
             return dispatch_mr<WT, 2, 2>(s, p, mr);
         }

@@ -87,6 +87,28 @@ def test_int8_gemv_fp16_row_short_rows(device, suite, n, k, y_dtype):
         b.free()
 
 
+@pytest.mark.parametrize("storage,x_dtype,n,k", [
+    (l0.I8PC, l0.F32, 1152, 896), (l0.I8PC, l0.F32, 896, 896), (l0.I8PC, l0.F32, 2048, 1024),
+    (l0.I8PC, l0.F32, 2049, 1024), (l0.I8PC, l0.F16, 2048, 896), (l0.I8PC, l0.F16, 1, 896),
+    (l0.F16, l0.F32, 896, 512), (l0.F16, l0.F16, 1001, 256)])
+def test_gemv_one_row_items_few_short_rows(device, suite, storage, x_dtype, n, k):
+    """Matrices of short rows with at most one row per wave of the grid take 1-row items (2049 rows:
+    the 2-row items just past the limit): the staged fp32 row, the fp16 row read with the weight
+    chunks, and fp16 weights, against the oracle."""
+    rng = np.random.default_rng(n + k + 7 * x_dtype + storage)
+    w = rng.normal(0, 0.02, (n, k)).astype(np.float32)
+    x = rng.normal(0, 1, k).astype(np.float16 if x_dtype == l0.F16 else np.float32)
+    dt, ws, s = stored(storage, w)
+    want = orc.gemv_nk(dt, ws, x.astype(np.float32), s)[0]
+    wb, xb, yb = up(device, ws), up(device, x), device.alloc(n * 4)
+    sb = up(device, s) if s is not None else None
+    suite.gemv_nk(storage, 1, n, k, xb, x_dtype, wb, sb, yb, l0.F32)
+    assert rel_err(yb.read(np.float32, n), want) < 2e-5, rel_err(yb.read(np.float32, n), want)
+    for b in (wb, xb, yb, sb):
+        if b is not None:
+            b.free()
+
+
 # Tall matrices of rows of at most 64 int8 chunks: 4-row items at four blocks per CU, each wave
 # stepping its issue priority down with its progress; fp16 and fp32 rows, a last row group that
 # the row count leaves partial (70001, 65537), rows of 32 chunks (K = 512).
