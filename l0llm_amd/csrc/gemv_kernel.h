@@ -884,16 +884,21 @@ int dispatch_wt(hipStream_t s, const GemvParams& p, int mr) {
             return dispatch_mr<WT, 2, 2>(s, p, mr);
         }
     }
-    // Long rows of a matrix with at most two rows per wave of the grid (plain store or residual
-    // epilogue): 1-row items, each wave's rows pipelined one behind the other instead of a 2-row item
-    // with both rows in flight at once. Measured (graph replay, cold weights): 4864 -> 896 (plain
-    // store) int8 5.21 -> 4.59 us, fp16 4.87 -> 4.52 us, 1 x 2 and 1 x 1 items slower; in the 8B int8
-    // decode step (two interleaved runs each) O 4096 -> 4096 5.3-5.7 -> 4.9 us, down 14336 -> 4096
-    // 12.2-12.3 -> 11.6-11.7 us, 544.7-545.1 -> 553.5-554.9 tokens/s. The 8B lm_head (fused norm) in
-    // 1-row items: 81-83 -> 83-90 us a launch, the step unchanged, so it keeps 2-row items.
+    // Long rows with 1-row items, each wave's rows pipelined one behind the other instead of a 2-row
+    // item with both rows in flight at once: a plain store with fewer than two rows per wave of the
+    // grid, and int8 weights against an fp16 row (XH, XHW; store or residual) with at most two.
+    // Measured (graph replay, cold weights): 4864 -> 896 (plain store) int8 5.21 -> 4.59 us, fp16
+    // 4.87 -> 4.52 us, 1 x 2 and 1 x 1 items slower; in the 8B int8 decode step (two interleaved runs
+    // each) O 4096 -> 4096 5.3-5.7 -> 4.9 us, down 14336 -> 4096 12.2-12.3 -> 11.6-11.7 us, 544.7-
+    // 545.1 -> 553.5-554.9 tokens/s. With an fp32 row (staged as fp32: a 1-row item reads twice the
+    // LDS bytes per weight byte) the same O and down shapes in the operator sequence of the drop-in
+    // path ran 293-296 against 300-303 tokens/s (three interleaved pairs), so they keep 2-row items;
+    // so does the 8B lm_head (fused norm; 1-row items 83-90 against 81-83 us, the step unchanged).
     if (mr == 1 && C > 128 && (p.epilogue == EPI_STORE || p.epilogue == EPI_RESIDUAL) && !p.norm_w) {
         const long waves = (long)(p.max_blocks > 0 ? p.max_blocks : 512) * kWaves;
-        if (ceil_div(p.n, 2) <= waves) {
+        bool x16 = false;
+        if constexpr (WT == L0H_I8PC) x16 = use_xh(p) || use_xhw(p);
+        if ((p.epilogue == EPI_STORE && ceil_div(p.n, 2) < waves) || (x16 && ceil_div(p.n, 2) <= waves)) {
             if constexpr (WT == L0H_I8PC) {
                 if (use_xh(p)) {
                     switch (staged_chunks(p)) {
